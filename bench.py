@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of the llamd quantized-matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+
+Headline (BASELINE.json metric "Q6_K matvec HBM GB/s (% of peak)"), on
+the Q6_K expert-FFN matvecs at batch 1 -- gate and up
+W [768 x 2048], down W [2048 x 768], weights from N(0, 0.02) quantized to Q6_K,
+activations N(0, 1) quantized to Q8_K (resident on the device before timing).
+One step = the three matvecs. value = algorithmic bytes / time over exactly
+K steps. Every launch reads a different device copy of its weights (>= 1 GiB
+of copies in rotation) so the 256 MB Infinity Cache cannot serve them.
+
+The same JSON line carries the other configs under "extra" (Q8_0 matvec,
+MoE decode layer tok/s, prefill grouped GEMM, LM head b=1/b=16), the roofline
+of the dominant kernel (q6k_mv_b1: per-launch HIP events on the library
+stream) and the CPU baseline: the C oracle (1 thread, the reference's design)
+timed on this host on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0        # dense int8 MFMA
+QK_K = 256
+GIB = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def q6k_bytes(rows, k):
+    return rows * k // QK_K * 210
+
+
+class Timer:
+    """HIP events on the library stream (where every kernel is launched)."""
+
+    def __init__(self, L, n=2):
+        self.L = L
+        self.ev = [L.llamd_hip_event_create() for _ in range(n)]
+
+    def rec(self, i):
+        if self.L.llamd_hip_event_record(self.ev[i]):
+            raise RuntimeError("event record failed")
+
+    def ms(self, a, b):
+        return float(self.L.llamd_hip_event_elapsed_ms(self.ev[a], self.ev[b]))
+
+    def close(self):
+        for e in self.ev:
+            self.L.llamd_hip_event_destroy(e)
+
+
+def sync(L):
+    if L.llamd_fwd_sync() or L.llamd_fwd_last_error():
+        from llamd_rs_amd._lib import last_error
+        raise RuntimeError(f"device error: {last_error()}")
+
+
+def time_region(L, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    sync(L)
+    t = Timer(L)
+    t.rec(0)
+    for i in range(steps):
+        fn(warmup + i)
+    t.rec(1)
+    ms = t.ms(0, 1)
+    sync(L)
+    t.close()
+    return ms
+
+
+def per_launch_ms(L, fn, n):
+    """Average duration of single launches, each bracketed by its own events."""
+    t = Timer(L, 2 * n)
+    for i in range(n):
+        t.rec(2 * i)
+        fn(i)
+        t.rec(2 * i + 1)
+    sync(L)
+    ds = [t.ms(2 * i, 2 * i + 1) for i in range(n)]
+    t.close()
+    return float(np.mean(ds)), float(np.median(ds))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="skip the large extra configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no "
+              "multi-GPU path; see DESIGN.md for how the path would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    from llamd_rs_amd import rocm, synth
+    from llamd_rs_amd._lib import lib
+    L = lib()
+    if not rocm.available():
+        raise SystemExit("no ROCm device visible")
+    info = rocm.device_info(0)
+    log(f"device: {info.name} {info.arch} CUs={info.compute_units}")
+    K, W = args.steps, args.warmup
+    p = lambda a: a.ctypes.data_as(C.c_void_p)
+
+    # ---- headline: configs[1] -------------------------------------------------
+    shapes = [("gate", 768, 2048, 11), ("up", 768, 2048, 12), ("down", 2048, 768, 13)]
+    per_shape_bytes = {}
+    mats = {}
+    t0 = time.time()
+    for name, rows, k, seed in shapes:
+        mats[name] = synth.q6k_matrix(seed, 0.02, rows, k)
+    log(f"synth weights {time.time() - t0:.1f}s")
+    ncopies = int(np.ceil(1.05 * GIB / sum(len(m) for m in mats.values())))
+    copies = {n: [] for n in mats}
+    t0 = time.time()
+    for name, rows, k, _ in shapes:
+        for _ in range(ncopies):
+            copies[name].append(rocm.DeviceWeights.upload(mats[name], rows, k // QK_K))
+    log(f"uploaded {ncopies} copies per shape ({ncopies * sum(len(m) for m in mats.values()) / GIB:.2f} GiB) "
+        f"in {time.time() - t0:.1f}s")
+    xs = {2048: synth.normal(21, 1.0, 2048), 768: synth.normal(22, 1.0, 768)}
+    acts = {k: rocm.quantize_q8k_on_device(x) for k, x in xs.items()}
+    dq = {k: (rocm.DeviceBuffer.from_array(a.qs), rocm.DeviceBuffer.from_array(a.d)) for k, a in acts.items()}
+    outs = {name: rocm.DeviceBuffer(rows * 4) for name, rows, _, _ in shapes}
+    for name, rows, k, _ in shapes:
+        per_shape_bytes[name] = q6k_bytes(rows, k) + k * 4 + rows * 4   # W + x + y (f32)
+
+    def launch(name, rows, k, i):
+        q, d = dq[k]
+        L.llamd_fwd_matvec(copies[name][i % ncopies].ptr, q.ptr, d.ptr, outs[name].ptr, k // QK_K, rows)
+
+    def step(i):
+        for name, rows, k, _ in shapes:
+            launch(name, rows, k, i)
+
+    ms = time_region(L, step, K, W)
+    bytes_step = sum(per_shape_bytes.values())
+    value = bytes_step * K / (ms * 1e-3) / 1e9
+    log(f"configs[1] step: {ms / K * 1e3:.2f} us, {value:.1f} GB/s")
+
+    shape_res = {}
+    for name, rows, k, _ in shapes:
+        msn = time_region(L, lambda i, n=name, r=rows, kk=k: launch(n, r, kk, i), K, W)
+        avg, med = per_launch_ms(L, lambda i, n=name, r=rows, kk=k: launch(n, r, kk, i), min(K, 200))
+        shape_res[name] = {
+            "rows": rows, "k": k, "bytes": per_shape_bytes[name],
+            "us_back_to_back": msn / K * 1e3,
+            "gbs_back_to_back": per_shape_bytes[name] * K / (msn * 1e-3) / 1e9,
+            "us_per_launch_events": avg * 1e3, "us_per_launch_median": med * 1e3,
+            "gbs_kernel": per_shape_bytes[name] / (avg * 1e-3) / 1e9,
+        }
+        log(f"  {name}: {shape_res[name]}")
+    # dominant kernel for the roofline: q6k_mv_b1 over the three shapes
+    avg_all = np.mean([shape_res[n]["us_per_launch_events"] for n in shape_res])
+    bytes_launch = bytes_step / 3
+    achieved = bytes_launch / (avg_all * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "q6k_mv_b1", "bytes_per_launch": bytes_launch,
+                "avg_launch_us": round(float(avg_all), 3)}
+    for lst in copies.values():
+        for c in lst:
+            c.close()
+    copies = None
+
+    extra = {"configs1_per_shape": shape_res}
+
+    # ---- extra configs ---------------------------------------------------------
+    if not args.quick:
+        extra.update(bench_extra(L, rocm, synth, K, W, p))
+
+    # ---- CPU baseline --------------------------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = bench_cpu(mats, shapes, xs, args.cpu_seconds)
+
+    line = {
+        "metric": "Q6_K matvec HBM GB/s (% of peak); MoE-layer decode tok/s vs llamd-cpu",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms / K, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q6_K; N(0,1) activations)",
+        "config": {"workload": "configs[1]: Q6_K expert-FFN matvecs at batch 1, gate+up [768x2048] "
+                               "and down [2048x768], one launch each per step, >=1 GiB of weight "
+                               "copies in rotation",
+                   "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_extra(L, rocm, synth, K, W, p):
+    out = {}
+    # Q8_0 matvec, configs[0]
+    rows, k = 4096, 2048
+    w = synth.q8_0_matrix(7, 0.02, rows, k)
+    nc = int(np.ceil(1.05 * GIB / len(w)))
+    ws = [rocm.Q8_0Weights(w, rows, k) for _ in range(nc)]
+    x = rocm.DeviceBuffer.from_array(synth.normal(8, 1.0, k))
+    y = rocm.DeviceBuffer(rows * 4)
+
+    def fq(i):
+        L.llamd_hip_fwd_matvec_q8_0(ws[i % nc]._ptr, x.ptr, y.ptr, rows, k)
+    ms = time_region(L, fq, K, W)
+    avg, med = per_launch_ms(L, fq, min(K, 100))
+    by = len(w) + k * 4 + rows * 4
+    out["q8_0_matvec"] = {"rows": rows, "k": k, "bytes": by, "us_back_to_back": ms / K * 1e3,
+                          "gbs_back_to_back": by * K / (ms * 1e-3) / 1e9,
+                          "us_per_launch_events": avg * 1e3, "gbs_kernel": by / (avg * 1e-3) / 1e9}
+    log(f"  q8_0: {out['q8_0_matvec']}")
+    for q in ws:
+        q.close()
+    x.close(); y.close()
+
+    # LM head b=1 and b=16, configs[4]
+    rows, k = 151936, 2048
+    t0 = time.time()
+    w = synth.q6k_matrix(4242, 0.02, rows, k)
+    log(f"LM head synth {time.time() - t0:.1f}s")
+    heads = []
+    for _ in range(4):
+        dw = rocm.DeviceWeights.upload(w, rows, k // QK_K)
+        heads.append((dw, rocm.LmHead(dw, max_seq=16)))
+    xb = rocm.DeviceBuffer.from_array(synth.normal(31, 1.0, 16 * k))
+    logits = rocm.DeviceBuffer(16 * rows * 4)
+    ids = rocm.DeviceBuffer(16 * 4)
+    for nseq in (1, 16):
+        def f(i, nseq=nseq):
+            h = heads[i % 4][1]
+            if L.llamd_hip_lmhead_forward(h.handle, xb.ptr, nseq, logits.ptr, ids.ptr):
+                raise RuntimeError("lmhead")
+        steps = max(10, K // 4)
+        ms = time_region(L, f, steps, 3)
+        by = q6k_bytes(rows, k) + nseq * k * 4 + nseq * rows * 4
+        avg, med = per_launch_ms(L, f, 20)
+        out[f"lm_head_b{nseq}"] = {"us_per_call": ms / steps * 1e3, "bytes": by,
+                                   "gbs": by / (ms / steps * 1e-3) / 1e9,
+                                   "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+                                   "us_per_call_events": avg * 1e3}
+        log(f"  lm_head b{nseq}: {out[f'lm_head_b{nseq}']}")
+    for dw, h in heads:
+        h.close(); dw.close()
+    xb.close(); logits.close(); ids.close()
+    del w
+
+    # MoE decode layer, configs[2]; 4 layers in rotation (2 GB of experts)
+    n_embd, n_ff, n_expert, n_used = 2048, 768, 128, 8
+    t0 = time.time()
+    router = synth.normal(500, 0.02, n_expert * n_embd).reshape(n_expert, n_embd)
+    gate = synth.q6k_matrix(501, 0.02, n_expert * n_ff, n_embd)
+    up = synth.q6k_matrix(502, 0.02, n_expert * n_ff, n_embd)
+    down = synth.q6k_matrix(503, 0.02, n_expert * n_embd, n_ff)
+    log(f"MoE synth {time.time() - t0:.1f}s")
+    layers = [rocm.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used) for _ in range(4)]
+    nx = 64
+    X = rocm.DeviceBuffer.from_array(synth.normal(600, 1.0, nx * n_embd))
+    R = rocm.DeviceBuffer.from_array(synth.normal(601, 1.0, nx * n_embd))
+    O_ = rocm.DeviceBuffer(n_embd * 4)
+    for mode, flag in (("fast", 0), ("exact", 1)):
+        def f(i, flag=flag):
+            xo = X.ptr + (i % nx) * n_embd * 4
+            ro = R.ptr + (i % nx) * n_embd * 4
+            if L.llamd_hip_moe_forward(layers[i % 4].handle, xo, ro, O_.ptr, flag):
+                raise RuntimeError("moe")
+        steps = max(20, K // 2)
+        ms = time_region(L, f, steps, 5)
+        by = n_expert * n_embd * 4 + 24 * q6k_bytes(n_ff, n_embd) + 3 * n_embd * 4
+        out[f"moe_layer_{mode}"] = {"us_per_token": ms / steps * 1e3, "tok_s": steps / (ms * 1e-3),
+                                    "bytes_per_token": by, "gbs": by / (ms / steps * 1e-3) / 1e9}
+        log(f"  moe {mode}: {out[f'moe_layer_{mode}']}")
+    calls, exact_calls = 0, 0
+    for ly in layers:
+        c, e = ly.stats()
+        calls += c; exact_calls += e
+    out["moe_router_exact_fold_calls"] = {"calls": calls, "exact_calls": exact_calls}
+
+    # prefill grouped GEMM, configs[3]: 512 tokens, Zipf 1.1
+    n_tok = 512
+    xs = rocm.DeviceBuffer.from_array(synth.normal(700, 1.0, n_tok * n_embd))
+    ids_h, w_h = synth.zipf_routing(701, 1.1, n_tok, n_expert, n_used)
+    ids_d = rocm.DeviceBuffer.from_array(ids_h.astype(np.int32))
+    w_d = rocm.DeviceBuffer.from_array(w_h)
+    po = rocm.DeviceBuffer(n_tok * n_embd * 4)
+
+    def fp(i):
+        if L.llamd_hip_moe_prefill(layers[i % 4].handle, xs.ptr, ids_d.ptr, w_d.ptr, po.ptr, n_tok):
+            raise RuntimeError("prefill")
+    steps = max(5, K // 20)
+    ms = time_region(L, fp, steps, 2)
+    ops = 2 * n_tok * n_used * (2 * n_ff * n_embd + n_embd * n_ff)
+    used = len(set(ids_h.ravel().tolist()))
+    wbytes = used * 3 * q6k_bytes(n_ff, n_embd)
+    out["prefill_grouped"] = {"tokens": n_tok, "ms_per_pass": ms / steps, "tok_s": n_tok * steps / (ms * 1e-3),
+                              "int_tops": ops / (ms / steps * 1e-3) / 1e12,
+                              "experts_used": used, "weight_bytes": wbytes,
+                              "weight_gbs": wbytes / (ms / steps * 1e-3) / 1e9}
+    log(f"  prefill: {out['prefill_grouped']}")
+    for ly in layers:
+        ly.close()
+    return out
+
+
+def bench_cpu(mats, shapes, xs, seconds):
+    """The oracle (1 thread, scalar -- the reference's CPU design) on a bounded
+    sample of the same workload: repeated configs[1] steps for ~`seconds`."""
+    from oracle import oracle as O
+    cores = 1
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for name, rows, k, _ in shapes:
+            O.matvec_q6k(mats[name], rows, k, xs[k])
+        n += 1
+    dt = time.perf_counter() - t0
+    bytes_step = sum(q6k_bytes(r, k) + k * 4 + r * 4 for _, r, k, _ in shapes)
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except Exception:
+        aff = os.cpu_count()
+    return {"value": round(bytes_step * n / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{n} configs[1] steps (gate+up+down Q6_K matvec incl. Q8_K quantize) in "
+                      f"{dt:.1f}s on 1 of {aff} host threads",
+            "ms_per_step": round(dt / n * 1e3, 3)}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,207 @@
+/*
+ * llamd_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul backend for
+ * llamd.rs.
+ *
+ * The boundary is the one the reference's llamd-rocm crate binds through
+ * `unsafe extern "C"` (crates/llamd-rocm/src/lib.rs:67-137): plain pointers,
+ * int sizes, int return codes (0 ok, -1 failure; pointer-returning calls give
+ * NULL on failure). Functions that exist in the reference keep its name and
+ * signature; each cites the definition it replaces. Functions the reference
+ * does not have are prefixed llamd_hip_ and say so.
+ *
+ * Weights: Q6_K matrices are uploaded with llamd_rocm_upload_q6k, which
+ * re-lays the ggml bytes into this backend's tiled device layout (a pure
+ * byte/bit permutation, see llamd_hip_q6k_tile). Every Q6_K entry point below
+ * takes such a handle. Rows of one matrix are k = blocks*256 weights; an
+ * expert tensor is n_expert matrices uploaded as one (rows*n_expert rows,
+ * rows % 16 == 0) or with llamd_rocm_upload_q6k_experts.
+ *
+ * Activations follow the reference's BlockQ8K split into arrays: qs (int8,
+ * 256 per block), d (f32 per block), bsums (int16, 16 per block).
+ *
+ * Results: every Q6_K matvec output, Q8_K quantization, dequantization,
+ * expert id and argmax id is bit-identical to the reference CPU path
+ * (llamd-quant/llamd-models/llamd-runtime); Q8_0/F32 matvecs and, outside
+ * exact mode, routing weights are within llamd-core::tolerance::REDUCTION.
+ *
+ * Threading: all device work is queued on one library-owned stream
+ * (llamd_fwd_get_stream). Host-in/host-out calls synchronise that stream and
+ * are serialised internally. Device-pointer calls (llamd_fwd_*) are
+ * asynchronous; call llamd_fwd_sync before reading results.
+ */
+#ifndef LLAMD_HIP_H
+#define LLAMD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device inventory ------------------------------------------------------ */
+/* crates/llamd-rocm/kernels/llamd.hip:36-40 */
+int llamd_rocm_device_count(void);
+/* llamd.hip:42-61. On CDNA `wgp_count` is the compute-unit count (256 on
+ * MI355X) and `warp_size` is 64. */
+int llamd_rocm_device_info(int dev, char *name, int name_len, char *arch, int arch_len,
+                           size_t *total_mem, int *wgp_count, int *warp_size);
+/* llamd.hip:63-67 */
+size_t llamd_rocm_free_mem(void);
+/* Not in the reference: message for the last -1/NULL returned on this thread. */
+const char *llamd_hip_last_error(void);
+
+/* ---- raw device memory and the stream ------------------------------------ */
+/* llamd.hip:153-165 */
+void *llamd_rocm_upload(const void *host, size_t bytes);
+void llamd_rocm_release(void *dev);
+/* llamd_forward.hip:711-745 */
+void *llamd_fwd_get_stream(void);
+int llamd_fwd_stream_init(void);
+void *llamd_fwd_alloc(size_t bytes);
+void llamd_fwd_free(void *p);
+int llamd_fwd_upload(void *dst, const void *src, size_t bytes);
+int llamd_fwd_download(void *dst, const void *src, size_t bytes);
+int llamd_fwd_sync(void);
+int llamd_fwd_last_error(void);
+
+/* ---- weight layouts (host-side, no device needed) ------------------------- */
+/* Not in the reference (its closest relative is the planar repack,
+ * crates/llamd-quant/src/dot.rs:349-423). Tiled Q6_K: see llamd_rs_amd/csrc/
+ * host/layout.cpp for the byte map. */
+size_t llamd_hip_q6k_tiled_bytes(int rows, int blocks);
+int llamd_hip_q6k_tile(const void *ggml, int rows, int blocks, void *out);
+int llamd_hip_q6k_untile(const void *tiled, int rows, int blocks, void *ggml_out);
+size_t llamd_hip_q8_0_planar_bytes(int rows, int k);
+int llamd_hip_q8_0_planarize(const void *ggml, int rows, int k, void *out);
+
+/* ---- weight upload -------------------------------------------------------- */
+/* Replaces the llamd_rocm_upload call in DeviceWeights::upload
+ * (crates/llamd-rocm/src/lib.rs:277-308): ggml Q6_K bytes [rows][blocks*210]
+ * -> tiled device copy. Release with llamd_rocm_release. */
+void *llamd_rocm_upload_q6k(const void *ggml, int rows, int blocks);
+/* Not in the reference: n_expert matrices of [rows][blocks*210] each (the 3D
+ * expert tensor of crates/llamd-models/src/model.rs:188-227), each tiled on
+ * its own so rows need not be a multiple of 16. */
+void *llamd_rocm_upload_q6k_experts(const void *ggml, int n_expert, int rows, int blocks);
+/* Not in the reference: Q8_0 [rows][k/32*34] -> planar device copy. */
+void *llamd_hip_upload_q8_0(const void *ggml, int rows, int k);
+
+/* ---- host-in / host-out (correctness and tests) --------------------------- */
+/* llamd.hip:1053-1085: y[r] = dot_q6k_q8k(row r, act), all rows. */
+int llamd_rocm_matvec_q6k_resident(const void *d_w, const int8_t *aq, const float *ad, float *out,
+                                   int blocks, int rows);
+/* llamd.hip:1164-1199: out[e][r] for the n_used experts eid[e] of a weight
+ * uploaded as rows*n_expert rows. Refuses ids out of range, rows that do not
+ * divide the upload, rows <= 0, n_used <= 0 (grouped_expert.rs:204-224). */
+int llamd_rocm_matvec_grouped(const void *d_w, const int32_t *eid, const int8_t *aq,
+                              const float *ad, float *out, int blocks, int rows, int n_used);
+/* Counterpart of llamd_fwd_matvec_grouped_pa (llamd.hip:1334-1346), host in
+ * and out: slot e uses its own activation (aq/ad hold n_used activations). */
+int llamd_hip_matvec_grouped_pa(const void *d_w, const int32_t *eid, const int8_t *aq,
+                                const float *ad, float *out, int blocks, int rows, int n_used);
+/* Not in the reference (its batched kernels cap at 8, llamd_batch.hip:41):
+ * out[s][r] = dot_q6k_q8k(row r, act s) for nseq activations, weights read
+ * once per 16 sequences. */
+int llamd_hip_matvec_q6k_batched(const void *d_w, const int8_t *aq, const float *ad, float *out,
+                                 int blocks, int rows, int nseq);
+/* llamd.hip:1258-1298: bit-exact quantize_q8_k on the device. bsums may be NULL. */
+int llamd_rocm_quantize_q8k(const float *x, int nblocks, int8_t *qs, float *d, int16_t *bsums);
+/* Not in the reference: act = silu(gate) * up (CpuBackend::silu/mul) then
+ * Q8_K, fused. act may be NULL. */
+int llamd_hip_swiglu_q8k(const float *gate, const float *up, int nblocks, float *act, int8_t *qs,
+                         float *d, int16_t *bsums);
+/* Not in the reference: device dequantization (for the EXACT weight check). */
+int llamd_hip_dequant_q6k(const void *d_w, int rows, int blocks, float *out);
+int llamd_hip_dequant_q8_0(const void *d_w, int rows, int k, float *out);
+/* Model::matvec_quant fallback for Q8_0 / F32 (model.rs:253-262), f32 act. */
+int llamd_hip_matvec_q8_0(const void *d_w, const float *x, float *out, int rows, int k);
+/* route(logits, n_used) (crates/llamd-models/src/moe.rs:73-113) on the device. */
+int llamd_hip_route(const float *logits, int n_expert, int n_used, int32_t *ids, float *weights);
+/* argmax per row of x[nseq][n], lowest index on ties (device_forward.rs:23-37). */
+int llamd_hip_argmax(const float *x, int n, int nseq, int32_t *ids);
+
+/* ---- device-pointer launchers on the library stream (asynchronous) -------- */
+/* llamd.hip:1313-1320 */
+void llamd_fwd_matvec(const void *d_w, const int8_t *d_aq, const float *d_ad, float *d_out,
+                      int blocks, int rows);
+/* llamd.hip:1322-1332 */
+void llamd_fwd_matvec_grouped(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                              const float *d_ad, float *d_out, int blocks, int rows, int n_used);
+/* llamd.hip:1334-1346 */
+void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                                 const float *d_ad, float *d_out, int blocks, int rows,
+                                 int n_used);
+/* llamd.hip:1607-1611 (d_bsums may be NULL) */
+void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks);
+/* llamd_forward.hip:802-805 (exact SiLU: glibc-identical expf) */
+void llamd_fwd_silu_mul(const float *gate, const float *up, float *out, int n);
+/* llamd_forward.hip:807-811, from given logits. probs may be NULL. */
+void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
+                      float *weights, float *probs);
+/* llamd_forward.hip:856-861 */
+void llamd_fwd_moe_combine_add(const float *down, const float *weights, const float *residual,
+                               float *out, int n_used, int n_embd);
+/* llamd_forward.hip:819-825; scratch_v/scratch_i hold nblocks partials. */
+void llamd_fwd_argmax(const float *x, int n, float *scratch_v, int32_t *scratch_i, int32_t *out,
+                      int nblocks);
+/* llamd_forward.hip:792-796 (FMA accumulation; REDUCTION vs the reference). */
+void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int rows);
+/* Not in the reference (its Q8_0 path is CPU-only, model.rs:253-262): Q8_0
+ * weight from llamd_hip_upload_q8_0 times an f32 activation. */
+void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, int rows, int k);
+
+/* ---- one MoE decode layer (R8 router -> R9 route -> R11 moe_ffn -> R12) ---- */
+/* Not in the reference as one call: DeviceModel::queue_token's MoE phases
+ * (crates/llamd-runtime/src/device.rs:486-655) behind a handle.
+ * router: f32 [n_expert][n_embd]; gate/up: ggml Q6_K [n_expert][n_ff][n_embd];
+ * down: ggml Q6_K [n_expert][n_embd][n_ff]. */
+void *llamd_hip_moe_create(const float *router, const void *gate, const void *up,
+                           const void *down, int n_embd, int n_ff, int n_expert, int n_used);
+void llamd_hip_moe_destroy(void *h);
+/* flags bit 0: exact mode -- always route on the reference's sequential f32
+ * router fold (bit-identical weights and layer output). Without it ids are
+ * still exact (a rigorous error bound decides when the fold is needed) and
+ * weights are within REDUCTION. Device pointers, asynchronous. d_res may be
+ * NULL (then out = moe_ffn only). */
+int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *d_out, int flags);
+/* Host in/out; ids/weights/logits (optional) receive the routing. */
+int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float *out,
+                               int32_t *ids, float *weights, float *logits, int flags);
+/* Prefill / grouped path: n_tok tokens with GIVEN routing ids/weights
+ * [n_tok][n_used] (device pointers), out [n_tok][n_embd] = moe_ffn per token. */
+int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
+                          float *d_out, int n_tok);
+int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
+                               float *out, int n_tok);
+/* Routing statistics since create: calls, and calls that needed the exact fold. */
+int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls);
+
+/* ---- LM head: Q6_K matvec over the vocabulary + argmax -------------------- */
+/* Not in the reference as one call (device.rs:640-655 queues the same ops).
+ * d_x: [nseq][k] f32, d_logits: [nseq][rows] (always written), d_ids: [nseq].
+ * Scratch for max_seq sequences is allocated at create and kept. */
+void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq);
+void llamd_hip_lmhead_destroy(void *h);
+int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logits,
+                             int32_t *d_ids);
+
+/* ---- timing on the library stream ---------------------------------------- */
+/* Not in the reference (its llamd_rocm_matvec_bench, llamd.hip:1101-1148,
+ * times one kernel; these let the caller bracket any queued sequence). */
+void *llamd_hip_event_create(void);
+void llamd_hip_event_destroy(void *ev);
+int llamd_hip_event_record(void *ev);
+float llamd_hip_event_elapsed_ms(void *start, void *stop);
+/* llamd.hip:1101-1148: one warm launch, then iters launches, total ms. */
+int llamd_rocm_matvec_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,
+                            int rows, int iters, float *ms_out);
+/* llamd.hip:1201-1252 */
+int llamd_rocm_matvec_grouped_bench(const void *d_w, const int32_t *eid, const int8_t *aq,
+                                    const float *ad, int blocks, int rows, int n_used, int iters,
+                                    float *ms_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,828 @@
+// capi.cpp -- the C ABI declared in include/llamd_hip.h.
+//
+// Host-side C++: argument validation, device memory, the library stream, and
+// the MoE-layer / LM-head handles that queue the gfx950 kernels of
+// q6k_mv.hip, q8k.hip, moe.hip and group.hip. Validation happens here, before
+// any launch, so a bad shape or expert id is an error return and never an
+// out-of-bounds device access (the reference does the same checks in its Rust
+// wrappers, crates/llamd-rocm/src/lib.rs:434-470).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/llamd_hip.h"
+#include "launch.hpp"
+
+using namespace llamd;
+
+namespace {
+
+constexpr int QK = 256;
+constexpr int SEGB = 16 * 210;
+
+thread_local char g_err[512] = "";
+std::mutex g_mu;             // serialises host-in/host-out calls and the registry
+hipStream_t g_stream = nullptr;
+
+int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    fail("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+hipStream_t stream() {
+    if (!g_stream) {
+        if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) g_stream = nullptr;
+    }
+    return g_stream;
+}
+
+// Registry of uploaded weights so that every entry point can check that a
+// handle is what it claims and that its shape covers the request.
+enum Kind { KIND_Q6K = 1, KIND_Q8_0 = 2 };
+struct WInfo {
+    Kind kind;
+    int rows;        // rows per expert matrix
+    int blocks;      // 256-blocks per row (Q6_K) or k (Q8_0)
+    int n_expert;    // matrices in the upload
+    size_t stride;   // bytes between expert matrices
+};
+std::unordered_map<const void *, WInfo> g_weights;
+
+bool lookup(const void *p, Kind kind, WInfo *out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_weights.find(p);
+    if (it == g_weights.end() || it->second.kind != kind) return false;
+    *out = it->second;
+    return true;
+}
+
+struct DevBuf {
+    void *p = nullptr;
+    DevBuf() = default;
+    explicit DevBuf(size_t n) { alloc(n); }
+    bool alloc(size_t n) {
+        release();
+        if (n == 0) n = 16;
+        if (hipMalloc(&p, n) != hipSuccess) p = nullptr;
+        return p != nullptr;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+    }
+    ~DevBuf() { release(); }
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    template <class T> T *as() const { return (T *)p; }
+};
+
+bool up(void *dst, const void *src, size_t n) {
+    return hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, stream()), "upload");
+}
+bool down(void *dst, const void *src, size_t n) {
+    return hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, stream()), "download");
+}
+bool sync() { return hip_ok(hipStreamSynchronize(stream()), "synchronize"); }
+
+int quantize_dev(const float *d_x, int8_t *d_qs, int8_t *d_qs_cm, float *d_d, int16_t *d_bs,
+                 int nblocks) {
+    return launch_q8k_quantize(d_x, d_qs, d_qs_cm, d_d, d_bs, nblocks, stream());
+}
+
+// Single-group batched matvec (all rows, nseq activations, identity pairs).
+int batched_dev(const void *w, const int8_t *aq_cm, const float *ad, float *y, int blocks,
+                int rows, int nseq) {
+    return launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, aq_cm,
+                                 ad, y, rows, rows, blocks, nseq, (nseq + 15) / 16, stream());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *llamd_hip_last_error(void) { return g_err; }
+
+// ---- inventory ---------------------------------------------------------------
+int llamd_rocm_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int llamd_rocm_device_info(int dev, char *name, int name_len, char *arch, int arch_len,
+                           size_t *total_mem, int *wgp_count, int *warp_size) {
+    hipDeviceProp_t p;
+    if (!hip_ok(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties")) return -1;
+    if (name && name_len > 0) snprintf(name, name_len, "%s", p.name);
+    if (arch && arch_len > 0) snprintf(arch, arch_len, "%s", p.gcnArchName);
+    if (total_mem) *total_mem = p.totalGlobalMem;
+    if (wgp_count) *wgp_count = p.multiProcessorCount;
+    if (warp_size) *warp_size = p.warpSize;
+    return 0;
+}
+
+size_t llamd_rocm_free_mem(void) {
+    size_t f = 0, t = 0;
+    if (hipMemGetInfo(&f, &t) != hipSuccess) return 0;
+    return f;
+}
+
+// ---- raw memory / stream -------------------------------------------------------
+void *llamd_rocm_upload(const void *host, size_t bytes) {
+    if (!host || !bytes) { fail("upload: empty"); return nullptr; }
+    void *d = nullptr;
+    if (!hip_ok(hipMalloc(&d, bytes), "hipMalloc")) return nullptr;
+    if (!hip_ok(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), "hipMemcpy")) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    return d;
+}
+
+void llamd_rocm_release(void *dev) {
+    if (!dev) return;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_weights.erase(dev);
+    }
+    (void)hipFree(dev);
+}
+
+void *llamd_fwd_get_stream(void) { return (void *)stream(); }
+int llamd_fwd_stream_init(void) { return stream() ? 0 : fail("stream create failed"); }
+
+void *llamd_fwd_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc")) return nullptr;
+    return p;
+}
+void llamd_fwd_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+int llamd_fwd_upload(void *dst, const void *src, size_t bytes) {
+    return up(dst, src, bytes) && sync() ? 0 : -1;
+}
+int llamd_fwd_download(void *dst, const void *src, size_t bytes) {
+    return down(dst, src, bytes) && sync() ? 0 : -1;
+}
+int llamd_fwd_sync(void) { return sync() ? 0 : -1; }
+int llamd_fwd_last_error(void) {
+    return hip_ok(hipGetLastError(), "queued work") ? 0 : -1;
+}
+
+// ---- weight upload -----------------------------------------------------------
+static void *upload_q6k_impl(const void *ggml, int n_expert, int rows, int blocks) {
+    if (!ggml || rows <= 0 || blocks <= 0 || n_expert <= 0) {
+        fail("upload_q6k: bad shape rows=%d blocks=%d n_expert=%d", rows, blocks, n_expert);
+        return nullptr;
+    }
+    const size_t per = llamd_hip_q6k_tiled_bytes(rows, blocks);
+    const size_t ggml_per = (size_t)rows * blocks * 210;
+    void *d = nullptr;
+    if (!hip_ok(hipMalloc(&d, per * n_expert), "hipMalloc")) return nullptr;
+    std::vector<uint8_t> tmp(per);
+    for (int e = 0; e < n_expert; ++e) {
+        llamd_hip_q6k_tile((const uint8_t *)ggml + e * ggml_per, rows, blocks, tmp.data());
+        if (!hip_ok(hipMemcpy((uint8_t *)d + e * per, tmp.data(), per, hipMemcpyHostToDevice),
+                    "hipMemcpy")) {
+            (void)hipFree(d);
+            return nullptr;
+        }
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_weights[d] = WInfo{KIND_Q6K, rows, blocks, n_expert, per};
+    return d;
+}
+
+void *llamd_rocm_upload_q6k(const void *ggml, int rows, int blocks) {
+    return upload_q6k_impl(ggml, 1, rows, blocks);
+}
+
+void *llamd_rocm_upload_q6k_experts(const void *ggml, int n_expert, int rows, int blocks) {
+    return upload_q6k_impl(ggml, n_expert, rows, blocks);
+}
+
+void *llamd_hip_upload_q8_0(const void *ggml, int rows, int k) {
+    const size_t bytes = llamd_hip_q8_0_planar_bytes(rows, k);
+    if (!ggml || !bytes) {
+        fail("upload_q8_0: bad shape rows=%d k=%d", rows, k);
+        return nullptr;
+    }
+    std::vector<uint8_t> tmp(bytes);
+    llamd_hip_q8_0_planarize(ggml, rows, k, tmp.data());
+    void *d = llamd_rocm_upload(tmp.data(), bytes);
+    if (!d) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_weights[d] = WInfo{KIND_Q8_0, rows, k, 1, bytes};
+    return d;
+}
+
+// Resolve (weight, rows-per-expert) to an expert stride and expert count,
+// accepting both upload forms: one tiled matrix of rows*n rows (rows % 16 == 0)
+// or llamd_rocm_upload_q6k_experts.
+static int expert_view(const void *d_w, int rows, int blocks, size_t *stride, int *n_expert) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
+    if (blocks != wi.blocks) return fail("blocks %d != uploaded %d", blocks, wi.blocks);
+    if (rows <= 0) return fail("rows must be positive");
+    if (wi.n_expert > 1) {
+        if (rows != wi.rows) return fail("rows %d != uploaded expert rows %d", rows, wi.rows);
+        *stride = wi.stride;
+        *n_expert = wi.n_expert;
+        return 0;
+    }
+    if (wi.rows % rows) return fail("rows %d does not divide the upload's %d", rows, wi.rows);
+    if (wi.rows != rows && rows % 16) return fail("rows %d not a multiple of 16", rows);
+    *stride = (size_t)(rows / 16) * blocks * SEGB;
+    *n_expert = wi.rows / rows;
+    return 0;
+}
+
+// ---- host-in/host-out ----------------------------------------------------------
+int llamd_rocm_matvec_q6k_resident(const void *d_w, const int8_t *aq, const float *ad, float *out,
+                                   int blocks, int rows) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
+    if (blocks != wi.blocks || rows <= 0 || rows > wi.rows * wi.n_expert || !aq || !ad || !out)
+        return fail("matvec: shape mismatch");
+    if (wi.n_expert > 1 && rows > wi.rows) return fail("matvec: rows span experts");
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf q((size_t)blocks * QK), d((size_t)blocks * 4), y((size_t)rows * 4);
+    if (!q.p || !d.p || !y.p) return fail("hipMalloc");
+    if (!up(q.p, aq, (size_t)blocks * QK) || !up(d.p, ad, (size_t)blocks * 4)) return -1;
+    if (launch_q6k_mv_b1(d_w, 0, nullptr, q.as<int8_t>(), d.as<float>(), y.as<float>(), rows,
+                         blocks, 1, 0, stream()))
+        return fail("launch");
+    if (!down(out, y.p, (size_t)rows * 4) || !sync()) return -1;
+    return 0;
+}
+
+static int grouped_host(const void *d_w, const int32_t *eid, const int8_t *aq, const float *ad,
+                        float *out, int blocks, int rows, int n_used, int per_slot) {
+    if (n_used <= 0) return fail("grouped: no experts");
+    if (!eid || !aq || !ad || !out) return fail("grouped: null pointer");
+    size_t stride = 0;
+    int n_expert = 0;
+    if (expert_view(d_w, rows, blocks, &stride, &n_expert)) return -1;
+    for (int i = 0; i < n_used; ++i)
+        if (eid[i] < 0 || eid[i] >= n_expert)
+            return fail("grouped: expert id %d out of range [0,%d)", eid[i], n_expert);
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int n_act = per_slot ? n_used : 1;
+    DevBuf q((size_t)n_act * blocks * QK), d((size_t)n_act * blocks * 4),
+        y((size_t)rows * n_used * 4), ids((size_t)n_used * 4);
+    if (!q.p || !d.p || !y.p || !ids.p) return fail("hipMalloc");
+    if (!up(q.p, aq, (size_t)n_act * blocks * QK) || !up(d.p, ad, (size_t)n_act * blocks * 4) ||
+        !up(ids.p, eid, (size_t)n_used * 4))
+        return -1;
+    if (launch_q6k_mv_b1(d_w, stride, ids.as<int32_t>(), q.as<int8_t>(), d.as<float>(),
+                         y.as<float>(), rows, blocks, n_used, per_slot, stream()))
+        return fail("launch");
+    if (!down(out, y.p, (size_t)rows * n_used * 4) || !sync()) return -1;
+    return 0;
+}
+
+int llamd_rocm_matvec_grouped(const void *d_w, const int32_t *eid, const int8_t *aq,
+                              const float *ad, float *out, int blocks, int rows, int n_used) {
+    return grouped_host(d_w, eid, aq, ad, out, blocks, rows, n_used, 0);
+}
+
+int llamd_hip_matvec_grouped_pa(const void *d_w, const int32_t *eid, const int8_t *aq,
+                                const float *ad, float *out, int blocks, int rows, int n_used) {
+    return grouped_host(d_w, eid, aq, ad, out, blocks, rows, n_used, 1);
+}
+
+// Batched host entry: quantized activations given in natural order; they are
+// re-ordered class-major on the host for the kernel's operand loads.
+int llamd_hip_matvec_q6k_batched(const void *d_w, const int8_t *aq, const float *ad, float *out,
+                                 int blocks, int rows, int nseq) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
+    if (blocks != wi.blocks || rows <= 0 || rows > wi.rows * wi.n_expert || nseq <= 0 || !aq ||
+        !ad || !out)
+        return fail("batched: shape mismatch");
+    if (wi.n_expert > 1 && rows > wi.rows) return fail("batched: rows span experts");
+    const size_t nq = (size_t)nseq * blocks * QK;
+    std::vector<int8_t> cm(nq);
+    for (size_t b = 0; b < (size_t)nseq * blocks; ++b)
+        for (int e = 0; e < QK; ++e) cm[b * QK + 32 * (e % 8) + e / 8] = aq[b * QK + e];
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf q(nq), d((size_t)nseq * blocks * 4), y((size_t)rows * nseq * 4);
+    if (!q.p || !d.p || !y.p) return fail("hipMalloc");
+    if (!up(q.p, cm.data(), nq) || !up(d.p, ad, (size_t)nseq * blocks * 4)) return -1;
+    if (batched_dev(d_w, q.as<int8_t>(), d.as<float>(), y.as<float>(), blocks, rows, nseq))
+        return fail("launch");
+    if (!down(out, y.p, (size_t)rows * nseq * 4) || !sync()) return -1;
+    return 0;
+}
+
+int llamd_rocm_quantize_q8k(const float *x, int nblocks, int8_t *qs, float *d, int16_t *bsums) {
+    if (nblocks <= 0 || !x || !qs || !d) return fail("quantize: bad arguments");
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf dx((size_t)nblocks * QK * 4), dq((size_t)nblocks * QK), dd((size_t)nblocks * 4),
+        db((size_t)nblocks * 32);
+    if (!dx.p || !dq.p || !dd.p || !db.p) return fail("hipMalloc");
+    if (!up(dx.p, x, (size_t)nblocks * QK * 4)) return -1;
+    if (quantize_dev(dx.as<float>(), dq.as<int8_t>(), nullptr, dd.as<float>(), db.as<int16_t>(),
+                     nblocks))
+        return fail("launch");
+    if (!down(qs, dq.p, (size_t)nblocks * QK) || !down(d, dd.p, (size_t)nblocks * 4)) return -1;
+    if (bsums && !down(bsums, db.p, (size_t)nblocks * 32)) return -1;
+    return sync() ? 0 : -1;
+}
+
+int llamd_hip_swiglu_q8k(const float *gate, const float *upv, int nblocks, float *act, int8_t *qs,
+                         float *d, int16_t *bsums) {
+    if (nblocks <= 0 || !gate || !upv || !qs || !d) return fail("swiglu: bad arguments");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t n = (size_t)nblocks * QK;
+    DevBuf dg(n * 4), du(n * 4), da(n * 4), dq(n), dd((size_t)nblocks * 4), db((size_t)nblocks * 32);
+    if (!dg.p || !du.p || !da.p || !dq.p || !dd.p || !db.p) return fail("hipMalloc");
+    if (!up(dg.p, gate, n * 4) || !up(du.p, upv, n * 4)) return -1;
+    if (launch_swiglu_q8k(dg.as<float>(), du.as<float>(), da.as<float>(), dq.as<int8_t>(), nullptr,
+                          dd.as<float>(), db.as<int16_t>(), nblocks, stream()))
+        return fail("launch");
+    if (act && !down(act, da.p, n * 4)) return -1;
+    if (!down(qs, dq.p, n) || !down(d, dd.p, (size_t)nblocks * 4)) return -1;
+    if (bsums && !down(bsums, db.p, (size_t)nblocks * 32)) return -1;
+    return sync() ? 0 : -1;
+}
+
+int llamd_hip_dequant_q6k(const void *d_w, int rows, int blocks, float *out) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
+    if (wi.n_expert != 1 || rows != wi.rows || blocks != wi.blocks || !out)
+        return fail("dequant: shape mismatch");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t n = (size_t)rows * blocks * QK;
+    DevBuf y(n * 4);
+    if (!y.p) return fail("hipMalloc");
+    if (launch_q6k_dequant(d_w, rows, blocks, y.as<float>(), stream())) return fail("launch");
+    if (!down(out, y.p, n * 4) || !sync()) return -1;
+    return 0;
+}
+
+int llamd_hip_dequant_q8_0(const void *d_w, int rows, int k, float *out) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q8_0, &wi)) return fail("not a Q8_0 weight handle");
+    if (rows != wi.rows || k != wi.blocks || !out) return fail("dequant: shape mismatch");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t n = (size_t)rows * k;
+    DevBuf y(n * 4);
+    if (!y.p) return fail("hipMalloc");
+    if (launch_q8_0_dequant(d_w, rows, k, y.as<float>(), stream())) return fail("launch");
+    if (!down(out, y.p, n * 4) || !sync()) return -1;
+    return 0;
+}
+
+int llamd_hip_matvec_q8_0(const void *d_w, const float *x, float *out, int rows, int k) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q8_0, &wi)) return fail("not a Q8_0 weight handle");
+    if (rows != wi.rows || k != wi.blocks || !x || !out) return fail("matvec_q8_0: shape mismatch");
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf dx((size_t)k * 4), y((size_t)rows * 4);
+    if (!dx.p || !y.p) return fail("hipMalloc");
+    if (!up(dx.p, x, (size_t)k * 4)) return -1;
+    if (launch_q8_0_mv(d_w, dx.as<float>(), y.as<float>(), rows, k, stream())) return fail("launch");
+    if (!down(out, y.p, (size_t)rows * 4) || !sync()) return -1;
+    return 0;
+}
+
+int llamd_hip_route(const float *logits, int n_expert, int n_used, int32_t *ids, float *weights) {
+    if (!logits || !ids || !weights) return fail("route: null pointer");
+    if (n_used <= 0 || n_used > n_expert) return fail("route: %d experts requested of %d", n_used, n_expert);
+    if (n_expert > 256 || n_used > 64) return fail("route: at most 256 experts, 64 used");
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf dl((size_t)n_expert * 4), di((size_t)n_used * 4), dw((size_t)n_used * 4);
+    if (!dl.p || !di.p || !dw.p) return fail("hipMalloc");
+    if (!up(dl.p, logits, (size_t)n_expert * 4)) return -1;
+    if (launch_moe_route(dl.as<float>(), nullptr, nullptr, nullptr, nullptr, n_expert, 0, n_used, 0,
+                         di.as<int32_t>(), dw.as<float>(), nullptr, nullptr, stream()))
+        return fail("launch");
+    if (!down(ids, di.p, (size_t)n_used * 4) || !down(weights, dw.p, (size_t)n_used * 4) || !sync())
+        return -1;
+    return 0;
+}
+
+int llamd_hip_argmax(const float *x, int n, int nseq, int32_t *ids) {
+    if (!x || !ids || n <= 0 || nseq <= 0) return fail("argmax: bad arguments");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int parts = argmax_parts(n);
+    DevBuf dx((size_t)n * nseq * 4), pv((size_t)parts * nseq * 4), pi((size_t)parts * nseq * 4),
+        di((size_t)nseq * 4);
+    if (!dx.p || !pv.p || !pi.p || !di.p) return fail("hipMalloc");
+    if (!up(dx.p, x, (size_t)n * nseq * 4)) return -1;
+    if (launch_argmax(dx.as<float>(), n, n, nseq, pv.as<float>(), pi.as<int>(), di.as<int32_t>(),
+                      stream()))
+        return fail("launch");
+    if (!down(ids, di.p, (size_t)nseq * 4) || !sync()) return -1;
+    return 0;
+}
+
+// ---- device-pointer launchers ------------------------------------------------
+void llamd_fwd_matvec(const void *d_w, const int8_t *d_aq, const float *d_ad, float *d_out,
+                      int blocks, int rows) {
+    launch_q6k_mv_b1(d_w, 0, nullptr, d_aq, d_ad, d_out, rows, blocks, 1, 0, stream());
+}
+
+void llamd_fwd_matvec_grouped(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                              const float *d_ad, float *d_out, int blocks, int rows, int n_used) {
+    size_t stride = 0;
+    int ne = 0;
+    if (expert_view(d_w, rows, blocks, &stride, &ne)) return;
+    launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 0, stream());
+}
+
+void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                                 const float *d_ad, float *d_out, int blocks, int rows,
+                                 int n_used) {
+    size_t stride = 0;
+    int ne = 0;
+    if (expert_view(d_w, rows, blocks, &stride, &ne)) return;
+    launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 1, stream());
+}
+
+void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks) {
+    quantize_dev(d_x, d_qs, nullptr, d_d, nullptr, nblocks);
+}
+
+void llamd_fwd_silu_mul(const float *gate, const float *upv, float *out, int n) {
+    launch_silu_mul(gate, upv, out, n, stream());
+}
+
+void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
+                      float *weights, float *probs) {
+    (void)probs;
+    launch_moe_route(logits, nullptr, nullptr, nullptr, nullptr, n_expert, 0, n_used, 0, ids,
+                     weights, nullptr, nullptr, stream());
+}
+
+void llamd_fwd_moe_combine_add(const float *d, const float *weights, const float *residual,
+                               float *out, int n_used, int n_embd) {
+    launch_moe_combine(d, weights, residual, out, n_used, n_embd, 1, stream());
+}
+
+void llamd_fwd_argmax(const float *x, int n, float *scratch_v, int32_t *scratch_i, int32_t *out,
+                      int nblocks) {
+    (void)nblocks;  // partial count is chosen from n (argmax_parts); scratch must hold it
+    launch_argmax(x, n, n, 1, scratch_v, (int *)scratch_i, out, stream());
+}
+
+void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int rows) {
+    launch_f32_mv(w, x, out, rows, k, stream());
+}
+
+void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, int rows, int k) {
+    launch_q8_0_mv(d_w, d_x, d_out, rows, k, stream());
+}
+
+}  // extern "C"
+
+// ---- MoE layer -------------------------------------------------------------------
+namespace {
+
+struct MoeLayer {
+    int n_embd, n_ff, n_expert, n_used;
+    int be, bf;  // 256-blocks per row of gate/up (n_embd) and down (n_ff)
+    DevBuf router;
+    void *gate = nullptr, *upw = nullptr, *downw = nullptr;
+    size_t sgu = 0, sd = 0;  // expert strides
+    // decode scratch
+    DevBuf xq, xd, logit_f, centre, radius, logits_used, ids, weights, stats;
+    DevBuf g, u, aq, ad, dn;
+    // prefill scratch (grown on demand)
+    int cap_tok = 0;
+    DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_tok, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
+};
+
+}  // namespace
+
+extern "C" {
+
+void *llamd_hip_moe_create(const float *router, const void *gate, const void *upw,
+                           const void *downw, int n_embd, int n_ff, int n_expert, int n_used) {
+    if (!router || !gate || !upw || !downw) { fail("moe_create: null weight"); return nullptr; }
+    if (n_embd <= 0 || n_ff <= 0 || n_embd % QK || n_ff % QK || n_embd % 64) {
+        fail("moe_create: n_embd and n_ff must be multiples of 256");
+        return nullptr;
+    }
+    if (n_expert <= 0 || n_expert > 256 || n_used <= 0 || n_used > n_expert || n_used > 64) {
+        fail("moe_create: need 0 < n_used <= n_expert <= 256, n_used <= 64");
+        return nullptr;
+    }
+    MoeLayer *m = new MoeLayer();
+    m->n_embd = n_embd; m->n_ff = n_ff; m->n_expert = n_expert; m->n_used = n_used;
+    m->be = n_embd / QK; m->bf = n_ff / QK;
+    bool ok = m->router.alloc((size_t)n_expert * n_embd * 4) &&
+              up(m->router.p, router, (size_t)n_expert * n_embd * 4);
+    m->gate = ok ? llamd_rocm_upload_q6k_experts(gate, n_expert, n_ff, m->be) : nullptr;
+    m->upw = m->gate ? llamd_rocm_upload_q6k_experts(upw, n_expert, n_ff, m->be) : nullptr;
+    m->downw = m->upw ? llamd_rocm_upload_q6k_experts(downw, n_expert, n_embd, m->bf) : nullptr;
+    ok = ok && m->downw;
+    if (ok) {
+        m->sgu = llamd_hip_q6k_tiled_bytes(n_ff, m->be);
+        m->sd = llamd_hip_q6k_tiled_bytes(n_embd, m->bf);
+        ok = m->xq.alloc(n_embd) && m->xd.alloc(m->be * 4) && m->logit_f.alloc(n_expert * 4) &&
+             m->centre.alloc(n_expert * 8) && m->radius.alloc(n_expert * 8) &&
+             m->logits_used.alloc(n_expert * 4) && m->ids.alloc(n_used * 4) &&
+             m->weights.alloc(n_used * 4) && m->stats.alloc(16) &&
+             m->g.alloc((size_t)n_used * n_ff * 4) && m->u.alloc((size_t)n_used * n_ff * 4) &&
+             m->aq.alloc((size_t)n_used * n_ff) && m->ad.alloc((size_t)n_used * m->bf * 4) &&
+             m->dn.alloc((size_t)n_used * n_embd * 4);
+        int zero[4] = {0, 0, 0, 0};
+        ok = ok && up(m->stats.p, zero, sizeof zero) && sync();
+    }
+    if (!ok) {
+        llamd_hip_moe_destroy(m);
+        if (!g_err[0]) fail("moe_create: allocation failed");
+        return nullptr;
+    }
+    return m;
+}
+
+void llamd_hip_moe_destroy(void *h) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m) return;
+    (void)hipStreamSynchronize(stream());
+    llamd_rocm_release(m->gate);
+    llamd_rocm_release(m->upw);
+    llamd_rocm_release(m->downw);
+    delete m;
+}
+
+int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *d_out, int flags) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !d_x || !d_out) return fail("moe_forward: null argument");
+    hipStream_t st = stream();
+    int rc = 0;
+    rc |= launch_q8k_quantize(d_x, m->xq.as<int8_t>(), nullptr, m->xd.as<float>(), nullptr, m->be, st);
+    rc |= launch_router_bound(m->router.as<float>(), d_x, m->n_expert, m->n_embd,
+                              m->logit_f.as<float>(), m->centre.as<double>(),
+                              m->radius.as<double>(), st);
+    rc |= launch_moe_route(m->logit_f.as<float>(), m->centre.as<double>(), m->radius.as<double>(),
+                           m->router.as<float>(), d_x, m->n_expert, m->n_embd, m->n_used,
+                           flags & 1, m->ids.as<int32_t>(), m->weights.as<float>(),
+                           m->logits_used.as<float>(), m->stats.as<int>(), st);
+    rc |= launch_q6k_mv_b1(m->gate, m->sgu, m->ids.as<int32_t>(), m->xq.as<int8_t>(),
+                           m->xd.as<float>(), m->g.as<float>(), m->n_ff, m->be, m->n_used, 0, st);
+    rc |= launch_q6k_mv_b1(m->upw, m->sgu, m->ids.as<int32_t>(), m->xq.as<int8_t>(),
+                           m->xd.as<float>(), m->u.as<float>(), m->n_ff, m->be, m->n_used, 0, st);
+    rc |= launch_swiglu_q8k(m->g.as<float>(), m->u.as<float>(), nullptr, m->aq.as<int8_t>(), nullptr,
+                            m->ad.as<float>(), nullptr, m->n_used * m->bf, st);
+    rc |= launch_q6k_mv_b1(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
+                           m->ad.as<float>(), m->dn.as<float>(), m->n_embd, m->bf, m->n_used, 1, st);
+    rc |= launch_moe_combine(m->dn.as<float>(), m->weights.as<float>(), d_res, d_out, m->n_used,
+                             m->n_embd, 1, st);
+    return rc ? fail("moe_forward: launch failed") : 0;
+}
+
+int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float *out, int32_t *ids,
+                               float *weights, float *logits, int flags) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !x || !out) return fail("moe_forward_host: null argument");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t nb = (size_t)m->n_embd * 4;
+    DevBuf dx(nb), dr(nb), dout(nb);
+    if (!dx.p || !dr.p || !dout.p) return fail("hipMalloc");
+    if (!up(dx.p, x, nb)) return -1;
+    if (res && !up(dr.p, res, nb)) return -1;
+    if (llamd_hip_moe_forward(m, dx.as<float>(), res ? dr.as<float>() : nullptr, dout.as<float>(),
+                              flags))
+        return -1;
+    if (!down(out, dout.p, nb)) return -1;
+    if (ids && !down(ids, m->ids.p, (size_t)m->n_used * 4)) return -1;
+    if (weights && !down(weights, m->weights.p, (size_t)m->n_used * 4)) return -1;
+    if (logits && !down(logits, m->logits_used.p, (size_t)m->n_expert * 4)) return -1;
+    return sync() ? 0 : -1;
+}
+
+int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m) return fail("moe_stats: null handle");
+    std::lock_guard<std::mutex> lk(g_mu);
+    int s[4];
+    if (!down(s, m->stats.p, sizeof s) || !sync()) return -1;
+    if (calls) *calls = s[0];
+    if (exact_calls) *exact_calls = s[1];
+    return 0;
+}
+
+int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
+                          float *d_out, int n_tok) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !d_x || !d_ids || !d_w || !d_out || n_tok <= 0) return fail("moe_prefill: bad arguments");
+    const int np = n_tok * m->n_used;
+    if (n_tok > m->cap_tok) {
+        // grown outside any capture; the stream is drained first so no queued
+        // kernel still reads the old buffers
+        if (!sync()) return -1;
+        const size_t NP = (size_t)np;
+        bool ok = m->p_xq.alloc((size_t)n_tok * m->n_embd) && m->p_xd.alloc((size_t)n_tok * m->be * 4) &&
+                  m->p_grp_e.alloc(m->n_expert * 4) && m->p_grp_s.alloc(m->n_expert * 4) &&
+                  m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc((m->n_expert + 1) * 4) &&
+                  m->p_tok.alloc(NP * 4) && m->p_idx.alloc(NP * 4) &&
+                  m->p_g.alloc(NP * m->n_ff * 4) && m->p_u.alloc(NP * m->n_ff * 4) &&
+                  m->p_aq.alloc(NP * m->n_ff) && m->p_ad.alloc(NP * m->bf * 4) &&
+                  m->p_dn.alloc(NP * m->n_embd * 4);
+        if (!ok) { m->cap_tok = 0; return fail("moe_prefill: allocation failed"); }
+        m->cap_tok = n_tok;
+    }
+    hipStream_t st = stream();
+    const int max_sub = np / 16 + m->n_expert;
+    int rc = 0;
+    rc |= launch_moe_group(d_ids, np, m->n_used, m->n_expert, m->p_grp_e.as<int32_t>(),
+                           m->p_grp_s.as<int32_t>(), m->p_grp_c.as<int32_t>(),
+                           m->p_sub.as<int32_t>(), m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(), st);
+    rc |= launch_q8k_quantize(d_x, nullptr, m->p_xq.as<int8_t>(), m->p_xd.as<float>(), nullptr,
+                              n_tok * m->be, st);
+    // gate / up: activation = the pair's token, output row = the pair index
+    rc |= launch_q6k_mv_batched(m->gate, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
+                                m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
+                                m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(),
+                                m->p_xq.as<int8_t>(), m->p_xd.as<float>(), m->p_g.as<float>(),
+                                m->n_ff, m->n_ff, m->be, m->n_expert, max_sub, st);
+    rc |= launch_q6k_mv_batched(m->upw, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
+                                m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
+                                m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(),
+                                m->p_xq.as<int8_t>(), m->p_xd.as<float>(), m->p_u.as<float>(),
+                                m->n_ff, m->n_ff, m->be, m->n_expert, max_sub, st);
+    rc |= launch_swiglu_q8k(m->p_g.as<float>(), m->p_u.as<float>(), nullptr, nullptr,
+                            m->p_aq.as<int8_t>(), m->p_ad.as<float>(), nullptr, np * m->bf, st);
+    // down: activation and output are both the pair
+    rc |= launch_q6k_mv_batched(m->downw, m->sd, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
+                                m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
+                                m->p_idx.as<int32_t>(), m->p_idx.as<int32_t>(),
+                                m->p_aq.as<int8_t>(), m->p_ad.as<float>(), m->p_dn.as<float>(),
+                                m->n_embd, m->n_embd, m->bf, m->n_expert, max_sub, st);
+    rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, nullptr, d_out, m->n_used, m->n_embd, n_tok, st);
+    return rc ? fail("moe_prefill: launch failed") : 0;
+}
+
+int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
+                               float *out, int n_tok) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !x || !ids || !w || !out || n_tok <= 0) return fail("moe_prefill_host: bad arguments");
+    const int np = n_tok * m->n_used;
+    for (int i = 0; i < np; ++i)
+        if (ids[i] < 0 || ids[i] >= m->n_expert) return fail("moe_prefill_host: bad expert id %d", ids[i]);
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t nx = (size_t)n_tok * m->n_embd * 4;
+    DevBuf dx(nx), di((size_t)np * 4), dw((size_t)np * 4), dout(nx);
+    if (!dx.p || !di.p || !dw.p || !dout.p) return fail("hipMalloc");
+    if (!up(dx.p, x, nx) || !up(di.p, ids, (size_t)np * 4) || !up(dw.p, w, (size_t)np * 4)) return -1;
+    if (llamd_hip_moe_prefill(m, dx.as<float>(), di.as<int32_t>(), dw.as<float>(), dout.as<float>(),
+                              n_tok))
+        return -1;
+    if (!down(out, dout.p, nx) || !sync()) return -1;
+    return 0;
+}
+
+}  // extern "C"
+
+// ---- LM head ---------------------------------------------------------------------
+namespace {
+struct LmHead {
+    const void *w;
+    int rows, blocks, cap;
+    DevBuf xq, xq_cm, xd, pv, pi;
+};
+}  // namespace
+
+extern "C" {
+
+void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq) {
+    WInfo wi;
+    if (!lookup(d_w, KIND_Q6K, &wi) || wi.n_expert != 1 || wi.rows != rows || wi.blocks != blocks) {
+        fail("lmhead_create: weight handle does not match rows=%d blocks=%d", rows, blocks);
+        return nullptr;
+    }
+    if (max_seq <= 0) { fail("lmhead_create: max_seq must be positive"); return nullptr; }
+    LmHead *l = new LmHead();
+    l->w = d_w; l->rows = rows; l->blocks = blocks; l->cap = max_seq;
+    const int parts = argmax_parts(rows);
+    const size_t nq = (size_t)max_seq * blocks * QK;
+    if (!l->xq.alloc(nq) || !l->xq_cm.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
+        !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4)) {
+        delete l;
+        fail("lmhead_create: allocation failed");
+        return nullptr;
+    }
+    return l;
+}
+
+void llamd_hip_lmhead_destroy(void *h) {
+    if (!h) return;
+    (void)hipStreamSynchronize(stream());
+    delete (LmHead *)h;
+}
+
+int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logits, int32_t *d_ids) {
+    LmHead *l = (LmHead *)h;
+    if (!l || !d_x || !d_logits || !d_ids || nseq <= 0 || nseq > l->cap)
+        return fail("lmhead_forward: bad arguments");
+    hipStream_t st = stream();
+    int rc = 0;
+    if (nseq == 1) {
+        rc |= launch_q8k_quantize(d_x, l->xq.as<int8_t>(), nullptr, l->xd.as<float>(), nullptr,
+                                  l->blocks, st);
+        rc |= launch_q6k_mv_b1(l->w, 0, nullptr, l->xq.as<int8_t>(), l->xd.as<float>(), d_logits,
+                               l->rows, l->blocks, 1, 0, st);
+    } else {
+        rc |= launch_q8k_quantize(d_x, nullptr, l->xq_cm.as<int8_t>(), l->xd.as<float>(), nullptr,
+                                  nseq * l->blocks, st);
+        rc |= batched_dev(l->w, l->xq_cm.as<int8_t>(), l->xd.as<float>(), d_logits, l->blocks,
+                          l->rows, nseq);
+    }
+    rc |= launch_argmax(d_logits, l->rows, l->rows, nseq, l->pv.as<float>(), l->pi.as<int>(), d_ids, st);
+    return rc ? fail("lmhead_forward: launch failed") : 0;
+}
+
+// ---- timing ----------------------------------------------------------------------
+void *llamd_hip_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) return nullptr;
+    return (void *)e;
+}
+void llamd_hip_event_destroy(void *ev) {
+    if (ev) (void)hipEventDestroy((hipEvent_t)ev);
+}
+int llamd_hip_event_record(void *ev) {
+    return hip_ok(hipEventRecord((hipEvent_t)ev, stream()), "hipEventRecord") ? 0 : -1;
+}
+float llamd_hip_event_elapsed_ms(void *a, void *b) {
+    float ms = -1.f;
+    if (hipEventSynchronize((hipEvent_t)b) != hipSuccess) return -1.f;
+    if (hipEventElapsedTime(&ms, (hipEvent_t)a, (hipEvent_t)b) != hipSuccess) return -1.f;
+    return ms;
+}
+
+static int bench_common(const void *d_w, const int32_t *eid, const int8_t *aq, const float *ad,
+                        int blocks, int rows, int n_used, int iters, float *ms_out) {
+    if (iters <= 0 || !ms_out || !aq || !ad) return fail("bench: bad arguments");
+    size_t stride = 0;
+    int ne = 1;
+    if (eid) {
+        if (expert_view(d_w, rows, blocks, &stride, &ne)) return -1;
+        for (int i = 0; i < n_used; ++i)
+            if (eid[i] < 0 || eid[i] >= ne) return fail("bench: bad expert id");
+    } else {
+        WInfo wi;
+        if (!lookup(d_w, KIND_Q6K, &wi) || wi.blocks != blocks || rows > wi.rows * wi.n_expert)
+            return fail("bench: weight handle mismatch");
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    DevBuf q((size_t)blocks * QK), d((size_t)blocks * 4), y((size_t)rows * n_used * 4),
+        ids((size_t)n_used * 4);
+    if (!q.p || !d.p || !y.p || !ids.p) return fail("hipMalloc");
+    if (!up(q.p, aq, (size_t)blocks * QK) || !up(d.p, ad, (size_t)blocks * 4)) return -1;
+    if (eid && !up(ids.p, eid, (size_t)n_used * 4)) return -1;
+    hipStream_t st = stream();
+    auto launch = [&]() {
+        return launch_q6k_mv_b1(d_w, stride, eid ? ids.as<int32_t>() : nullptr, q.as<int8_t>(),
+                                d.as<float>(), y.as<float>(), rows, blocks, n_used, 0, st);
+    };
+    if (launch() || !sync()) return fail("bench: warm launch failed");
+    hipEvent_t t0, t1;
+    if (hipEventCreate(&t0) != hipSuccess) return fail("hipEventCreate");
+    if (hipEventCreate(&t1) != hipSuccess) { (void)hipEventDestroy(t0); return fail("hipEventCreate"); }
+    int rc = -1;
+    if (hipEventRecord(t0, st) == hipSuccess) {
+        int bad = 0;
+        for (int i = 0; i < iters; ++i) bad |= launch();
+        if (!bad && hipEventRecord(t1, st) == hipSuccess && hipEventSynchronize(t1) == hipSuccess &&
+            hipEventElapsedTime(ms_out, t0, t1) == hipSuccess)
+            rc = 0;
+    }
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    return rc ? fail("bench: timing failed") : 0;
+}
+
+int llamd_rocm_matvec_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,
+                            int rows, int iters, float *ms_out) {
+    return bench_common(d_w, nullptr, aq, ad, blocks, rows, 1, iters, ms_out);
+}
+
+int llamd_rocm_matvec_grouped_bench(const void *d_w, const int32_t *eid, const int8_t *aq,
+                                    const float *ad, int blocks, int rows, int n_used, int iters,
+                                    float *ms_out) {
+    if (n_used <= 0 || !eid) return fail("grouped bench: no experts");
+    return bench_common(d_w, eid, aq, ad, blocks, rows, n_used, iters, ms_out);
+}
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+// group.hip -- expert grouping for the prefill path.
+//
+// The design of the reference's moe_group.comp (crates/llamd-vulkan/shaders/
+// moe_group.comp:37-82) on one gfx950 workgroup: a counting sort of the
+// n_tok * n_used (token, slot) pairs by expert -- LDS histogram, prefix sum,
+// scatter -- giving each expert a contiguous run of pairs. The order of pairs
+// inside one expert's run depends on atomic arrival, which is harmless: each
+// pair's result is computed independently and written to its own output row
+// (the pair index), so the expert-major result equals the token-major one
+// exactly, the property crates/llamd-testing/tests/vulkan_prefill.rs:268-333
+// holds the reference's Vulkan path to.
+//
+// Outputs (all experts are groups, empty ones included):
+//   grp_expert[e] = e, grp_start[e], grp_count[e],
+//   sub_start[0..n_expert] = prefix sum of ceil(count/16) (16-token MFMA
+//   sub-tiles), pair_tok[i] = token of the i-th sorted pair, pair_idx[i] = its
+//   pair index t * n_used + k.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace llamd {
+namespace {
+
+constexpr int GROUP_MAX_EXPERTS = 1024;
+
+__global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pairs, int n_used,
+                                                  int n_expert, int32_t *grp_expert,
+                                                  int32_t *grp_start, int32_t *grp_count,
+                                                  int32_t *sub_start, int32_t *pair_tok,
+                                                  int32_t *pair_idx) {
+    __shared__ int hist[GROUP_MAX_EXPERTS];
+    __shared__ int cursor[GROUP_MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < n_expert; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < n_pairs; p += blockDim.x) atomicAdd(&hist[ids[p]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int start = 0, sub = 0;
+        for (int e = 0; e < n_expert; ++e) {
+            const int c = hist[e];
+            grp_expert[e] = e;
+            grp_start[e] = start;
+            grp_count[e] = c;
+            sub_start[e] = sub;
+            cursor[e] = start;
+            start += c;
+            sub += (c + 15) / 16;
+        }
+        sub_start[n_expert] = sub;
+    }
+    __syncthreads();
+    for (int p = tid; p < n_pairs; p += blockDim.x) {
+        const int pos = atomicAdd(&cursor[ids[p]], 1);
+        pair_tok[pos] = p / n_used;
+        pair_idx[pos] = p;
+    }
+}
+
+}  // namespace
+
+int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
+                     int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
+                     int32_t *sub_start, int32_t *pair_tok, int32_t *pair_idx, hipStream_t st) {
+    if (n_expert > GROUP_MAX_EXPERTS || n_expert <= 0) return -1;
+    hipLaunchKernelGGL(moe_group, dim3(1), dim3(1024), 0, st, ids, n_pairs, n_used, n_expert,
+                       grp_expert, grp_start, grp_count, sub_start, pair_tok, pair_idx);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace llamd

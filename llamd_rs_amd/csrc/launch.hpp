@@ -1,0 +1,56 @@
+// launch.hpp -- host-side launchers of the gfx950 kernels (one per kernel
+// family). Every launcher enqueues on the given stream and returns 0, or -1
+// if the launch was rejected. Shapes are validated by the callers in capi.cpp
+// before any launcher is reached.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace llamd {
+
+// q6k_mv.hip
+int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
+                     const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
+                     hipStream_t st);
+// Expert-grouped batched matvec (see q6k_mv.hip). sub_start has n_groups+1
+// entries; max_subtiles bounds sub_start[n_groups] and sizes the grid. With
+// grp_expert == nullptr there is a single group (expert 0) of n_groups pairs.
+int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
+                          const int32_t *grp_start, const int32_t *grp_count,
+                          const int32_t *sub_start, const int32_t *pair_act,
+                          const int32_t *pair_out, const int8_t *aq_cm, const float *ad, float *y,
+                          int ldy, int rows, int blocks, int n_groups, int max_subtiles,
+                          hipStream_t st);
+int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
+
+// q8k.hip
+int launch_q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm, float *d, int16_t *bsums,
+                        int nblocks, hipStream_t st);
+int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs,
+                      int8_t *qs_cm, float *d, int16_t *bsums, int nblocks, hipStream_t st);
+// moe grouping (group.hip): counting sort of (token, slot) pairs by expert
+int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
+                     int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
+                     int32_t *sub_start, int32_t *pair_tok, int32_t *pair_idx,
+                     hipStream_t st);
+int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipStream_t st);
+
+// moe.hip
+int launch_router_bound(const float *w, const float *x, int n_expert, int k, float *logit_f,
+                        double *centre, double *radius, hipStream_t st);
+int launch_moe_route(const float *logit_f, const double *centre, const double *radius,
+                     const float *w, const float *x, int n_expert, int k, int n_used,
+                     int force_exact, int32_t *ids, float *weights, float *logits_used,
+                     int *stats, hipStream_t st);
+int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
+                       int n_used, int n_embd, int n_tok, hipStream_t st);
+int argmax_parts(int n);
+int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, int32_t *out,
+                  hipStream_t st);
+int launch_q8_0_mv(const void *planar, const float *x, float *y, int rows, int k, hipStream_t st);
+int launch_q8_0_dequant(const void *planar, int rows, int k, float *out, hipStream_t st);
+int launch_f32_mv(const float *w, const float *x, float *y, int rows, int k, hipStream_t st);
+
+}  // namespace llamd

@@ -1,0 +1,179 @@
+"""Q6_K / Q8_0 matvec kernels on the MI355X against the CPU oracle.
+
+The bar is stricter than the reference's own GPU tests (rocm_oracle.rs,
+grouped_expert.rs, planar.rs hold their kernels to REDUCTION against the CPU):
+these kernels replay the reference's integer lanes and ordered float epilogue,
+so every Q6_K output is compared BIT-FOR-BIT (tolerance EXACT).
+"""
+import numpy as np
+import pytest
+
+import helpers as H
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+QK_K = 256
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def cpu_rows(w, rows, blocks, act):
+    return O.matvec_q6k_act(w, rows, blocks * QK_K, act)
+
+
+def test_device_reports_cdna4(gpu):
+    info = gpu.device_info(0)
+    print(info)
+    assert info.arch.startswith("gfx950"), info.arch
+    assert info.wave_size == 64
+    assert info.total_mem > (200 << 30)
+
+
+def test_device_quantization_is_identical_to_the_host(gpu):      # grouped_expert.rs:226-260
+    x = np.concatenate([H.q8k_cases(), np.random.default_rng(0).standard_normal(64 * QK_K)]
+                       ).astype(np.float32)
+    host = O.quantize_q8_k(x)
+    dev = gpu.quantize_q8k_on_device(x)
+    assert bits_equal(host.d, dev.d)
+    assert np.array_equal(host.qs, dev.qs)
+    assert np.array_equal(host.bsums, dev.bsums)
+
+
+def test_swiglu_quantize_is_identical_to_the_host(gpu):
+    rng = np.random.default_rng(1)
+    g = (rng.standard_normal(24 * QK_K) * 4).astype(np.float32)
+    u = rng.standard_normal(24 * QK_K).astype(np.float32)
+    g[:8] = [0.0, -0.0, 88.0, -88.0, 104.0, -104.0, 1e-30, -1e-30]
+    act, q = gpu.swiglu_q8k_on_device(g, u)
+    want = O.mul(O.silu(g), u)
+    assert bits_equal(act, want)
+    hq = O.quantize_q8_k(want)
+    assert bits_equal(q.d, hq.d) and np.array_equal(q.qs, hq.qs) and np.array_equal(q.bsums, hq.bsums)
+
+
+@pytest.mark.parametrize("rows,blocks,seed", [(1, 1, 3), (8, 4, 5), (64, 8, 11), (7, 8, 13),
+                                              (33, 3, 17), (16, 16, 19)])
+def test_gpu_matvec_matches_the_cpu_reference(gpu, rows, blocks, seed):   # rocm_oracle.rs:79-108
+    w = H.weights(rows, blocks, seed)
+    act = O.quantize_q8_k(H.sample(blocks * QK_K, seed + 100))
+    dev = gpu.DeviceWeights.upload(w, rows, blocks)
+    got = dev.matvec(gpu.BlockQ8K(act.d, act.qs, act.bsums))
+    assert bits_equal(got, cpu_rows(w, rows, blocks, act))
+
+
+@pytest.mark.parametrize("rows,k", [(768, 2048), (2048, 768), (4096, 2048), (512, 4096)])
+def test_config_shapes_bit_exact(gpu, rows, k):
+    """The expert gate/up/down shapes and attention shapes, weights from this
+    project's Q6_K quantizer on N(0, 0.02), activations N(0, 1)."""
+    from llamd_rs_amd import synth
+    blocks = k // QK_K
+    w = synth.q6k_matrix(1234 + rows, 0.02, rows, k)
+    x = synth.normal(99 + k, 1.0, k)
+    act = O.quantize_q8_k(x)
+    dev = gpu.DeviceWeights.upload(w, rows, blocks)
+    got = dev.matvec(gpu.quantize_q8k_on_device(x))
+    assert bits_equal(got, cpu_rows(w, rows, blocks, act))
+
+
+def test_dequantized_weights_are_exact(gpu):
+    for rows, blocks, seed in [(16, 8, 1), (21, 3, 2)]:
+        w = H.synth(rows, blocks, seed)
+        dev = gpu.DeviceWeights.upload(w, rows, blocks)
+        got = dev.dequantize()
+        want = O.dequantize(14, w, rows * blocks * QK_K).reshape(rows, -1)
+        assert bits_equal(got, want)
+
+
+def test_grouped_matches_the_ungrouped_kernel_exactly(gpu):      # grouped_expert.rs:66-118
+    rows, k, n_expert = 2048, 768, 16
+    blocks = k // QK_K
+    w = H.synth(rows * n_expert, blocks, 0x5EED)
+    act = gpu.quantize_q8k_on_device(H.sin_ramp(k, 0.017))
+    ids = [3, 0, 15, 7, 7, 1, 11, 2]
+    dw = gpu.DeviceWeights.upload(w, rows * n_expert, blocks)
+    got = dw.matvec_grouped(act, ids, rows)
+    per = rows * blocks * 210
+    for e, eid in enumerate(ids):
+        single = gpu.DeviceWeights.upload(w[eid * per:(eid + 1) * per], rows, blocks)
+        assert bits_equal(got[e * rows:(e + 1) * rows], single.matvec(act)), eid
+
+
+def test_grouped_matches_the_scalar_cpu(gpu):                    # grouped_expert.rs:120-180
+    rows, k, n_expert = 512, 768, 8
+    blocks = k // QK_K
+    w = H.synth(rows * n_expert, blocks, 0x1234)
+    x = H.cos_ramp(k, 0.021)
+    act = O.quantize_q8_k(x)
+    ids = [5, 2, 7, 0]
+    dw = gpu.DeviceWeights.upload(w, rows * n_expert, blocks)
+    got = dw.matvec_grouped(gpu.BlockQ8K(act.d, act.qs, act.bsums), ids, rows)
+    per = rows * blocks * 210
+    cpu = np.concatenate([cpu_rows(w[e * per:(e + 1) * per], rows, blocks, act) for e in ids])
+    assert bits_equal(got, cpu)
+
+
+def test_a_repeated_expert_gives_a_repeated_block(gpu):          # grouped_expert.rs:182-201
+    rows, k, n_expert = 256, 512, 4
+    w = H.synth(rows * n_expert, k // QK_K, 0xABCD)
+    act = gpu.quantize_q8k_on_device(H.cos_ramp(k, 0.03))
+    dw = gpu.DeviceWeights.upload(w, rows * n_expert, k // QK_K)
+    got = dw.matvec_grouped(act, [2, 2], rows)
+    assert bits_equal(got[:rows], got[rows:])
+
+
+def test_bad_expert_ids_are_refused(gpu):                        # grouped_expert.rs:203-224
+    rows, k, n_expert = 64, 256, 2
+    w = H.synth(rows * n_expert, 1, 7)
+    act = gpu.quantize_q8k_on_device(np.full(k, 0.5, np.float32))
+    dw = gpu.DeviceWeights.upload(w, rows * n_expert, 1)
+    for ids, r in [([2], rows), ([-1], rows), ([0], rows + 1)]:
+        with pytest.raises(gpu.HipError):
+            dw.matvec_grouped(act, ids, r)
+    for ids, r in [([0], 0), ([], rows)]:
+        with pytest.raises((ValueError, gpu.HipError)):
+            dw.matvec_grouped(act, ids, r)
+
+
+def test_grouped_per_activation_down_projection(gpu):
+    """The down projection: each routed expert has its own activation."""
+    rows, k, n_expert = 2048, 768, 6
+    blocks = k // QK_K
+    w = H.weights(rows * n_expert, blocks, 77)
+    ids = [4, 1, 5]
+    acts = [O.quantize_q8_k(H.sin_ramp(k, 0.019, phase=1.7 * s)) for s in range(3)]
+    dw = gpu.DeviceWeights.upload_experts(w, n_expert, rows, blocks)
+    got = dw.matvec_grouped_pa([gpu.BlockQ8K(a.d, a.qs, a.bsums) for a in acts], ids, rows)
+    per = rows * blocks * 210
+    cpu = np.concatenate([cpu_rows(w[e * per:(e + 1) * per], rows, blocks, a) for e, a in zip(ids, acts)])
+    assert bits_equal(got, cpu)
+
+
+@pytest.mark.parametrize("rows,k,nseq", [(256, 768, 1), (1024, 2048, 4), (512, 4096, 16),
+                                         (256, 2048, 17), (100, 512, 3)])
+def test_batched_agrees_bit_for_bit(gpu, rows, k, nseq):         # planar.rs:194-250 (udot)
+    blocks = k // QK_K
+    w = H.weights(rows, blocks, 97 + rows)
+    acts = [O.quantize_q8_k(H.sin_ramp(k, 0.017, phase=1.7 * s)) for s in range(nseq)]
+    dw = gpu.DeviceWeights.upload(w, rows, blocks)
+    got = dw.matvec_batched([gpu.BlockQ8K(a.d, a.qs, a.bsums) for a in acts])
+    for s, a in enumerate(acts):
+        assert bits_equal(got[s], cpu_rows(w, rows, blocks, a)), s
+
+
+def test_q8_0_matvec_within_reduction(gpu):
+    """W [4096 x 2048] Q8_0 from N(0, 0.02), x ~ N(0, 1): the
+    reference dequantizes and sums sequentially (model.rs:253-262)."""
+    from llamd_rs_amd import synth
+    rows, k = 4096, 2048
+    w = synth.q8_0_matrix(7, 0.02, rows, k)
+    x = synth.normal(8, 1.0, k)
+    dev = gpu.Q8_0Weights(w, rows, k)
+    assert bits_equal(dev.dequantize(), O.dequantize(8, w, rows * k).reshape(rows, k))
+    got = dev.matvec(x)
+    cpu = O.matvec_q8_0(w, rows, k, x)
+    idx, dev_ = O.max_deviation(got, cpu)
+    assert dev_ <= O.REDUCTION, (idx, got[idx], cpu[idx])

@@ -1,0 +1,196 @@
+"""Routing, the MoE decode layer, prefill grouping and the LM head on the
+MI355X against the CPU oracle. Expert ids and argmax ids: EXACT. Layer
+outputs: EXACT in exact-router mode, within REDUCTION * max(rms, 1) in the
+default mode (routing weights from the parallel router sum)."""
+import numpy as np
+import pytest
+
+import helpers as H
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+QK_K = 256
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+CASES = [([0.1, 5.0, 0.2, 3.0, 0.3], 2), ([1, 2, 3, 4, 5, 6, 7, 8], 3), ([10.0, 9.0, 0.0, 0.0], 2),
+         ([3.0, 1.0, 4.0, 1.0, 5.0], 2), ([1.0, 1.0, 1.0, 1.0], 2), ([0.0, -800.0, -800.0, -800.0], 3),
+         ([0.0, -800.0, -900.0, -850.0], 3)]
+
+
+@pytest.mark.parametrize("logits,n_used", CASES)
+def test_route_known_answers(gpu, logits, n_used):               # moe.rs:115-247
+    want = O.route(logits, n_used)
+    got = gpu.route(logits, n_used)
+    assert list(got.experts) == list(want.experts)
+    assert bits_equal(got.weights, want.weights)
+
+
+def test_route_random_and_tied_logits(gpu):
+    rng = np.random.default_rng(0)
+    for t in range(200):
+        lg = rng.standard_normal(128).astype(np.float32) * 2
+        if t % 3 == 0:
+            lg[rng.integers(0, 128, 20)] = lg[5]          # exact ties
+        if t % 5 == 0:
+            lg[7] = np.nextafter(lg[9], np.float32(10))   # one-ulp neighbours
+        want = O.route(lg, 8)
+        got = gpu.route(lg, 8)
+        assert list(got.experts) == list(want.experts), t
+        assert bits_equal(got.weights, want.weights), t
+
+
+def test_route_refuses_impossible_requests(gpu):
+    with pytest.raises(ValueError):
+        gpu.route([1.0, 2.0], 0)
+    with pytest.raises(ValueError):
+        gpu.route([1.0, 2.0], 3)
+
+
+def test_argmax_lowest_index(gpu):
+    v = np.zeros((3, 10000), np.float32)
+    v[0, [17, 5000, 9999]] = 3.0
+    v[1] = np.random.default_rng(1).standard_normal(10000)
+    v[2, :] = -np.inf
+    ids = gpu.argmax(v)
+    assert list(ids) == [O.argmax(v[0]), O.argmax(v[1]), O.argmax(v[2])] == [17, int(np.argmax(v[1])), 0]
+
+
+def make_layer(n_embd, n_ff, n_expert, seed):
+    from llamd_rs_amd import synth
+    router = synth.normal(seed, 0.02, n_expert * n_embd).reshape(n_expert, n_embd)
+    gate = synth.q6k_matrix(seed + 1, 0.02, n_expert * n_ff, n_embd)
+    up = synth.q6k_matrix(seed + 2, 0.02, n_expert * n_ff, n_embd)
+    down = synth.q6k_matrix(seed + 3, 0.02, n_expert * n_embd, n_ff)
+    return router, gate, up, down
+
+
+@pytest.fixture(scope="module")
+def qwen_layer(gpu):
+    """hidden 2048, 128 experts of Q6_K gate/up [768 x 2048] and
+    down [2048 x 768], f32 router [128 x 2048], top-8."""
+    n_embd, n_ff, n_expert, n_used = 2048, 768, 128, 8
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 500)
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    yield layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    layer.close()
+
+
+def test_moe_layer_ids_exact_and_output_close(gpu, qwen_layer):
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    for t in range(6):
+        x = synth.normal(1000 + t, 1.0, n_embd)
+        res = synth.normal(2000 + t, 1.0, n_embd)
+        want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+        out, r, lg_used = layer.forward(x, res)
+        assert list(r.experts) == list(ids), t
+        assert np.max(np.abs(r.weights - w)) <= O.REDUCTION
+        bound = O.REDUCTION * max(H.rms(want), 1.0)
+        assert np.max(np.abs(out - want)) <= bound, t
+
+
+def test_moe_layer_exact_mode_is_bit_identical(gpu, qwen_layer):
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    for t in range(3):
+        x = synth.normal(3000 + t, 1.0, n_embd)
+        res = synth.normal(4000 + t, 1.0, n_embd)
+        want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+        out, r, lg_used = layer.forward(x, res, exact=True)
+        assert bits_equal(lg_used, lg)
+        assert list(r.experts) == list(ids)
+        assert bits_equal(r.weights, w)
+        assert bits_equal(out, want), t
+    calls, exact_calls = layer.stats()
+    assert exact_calls >= 3
+
+
+def test_moe_layer_near_tied_router_stays_exact(gpu):
+    """A router whose top experts are separated by far less than the float
+    error of the parallel sum: the ids must still be the CPU's."""
+    n_embd, n_ff, n_expert, n_used = 256, 256, 16, 4
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 900)
+    router = router.copy()
+    for e in (3, 8, 12):
+        router[e] = router[5]
+    router[9] = router[5] * np.float32(1 + 2 ** -22)
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    rng = np.random.default_rng(3)
+    for t in range(10):
+        x = rng.standard_normal(n_embd).astype(np.float32)
+        x = x * np.sign(router[5] @ x)      # make the tied group win
+        want, lg, ids, w = O.moe_layer(x, np.zeros(n_embd, np.float32), n_embd, n_ff, n_expert,
+                                       n_used, router, gate, up, down)
+        out, r, _ = layer.forward(x)
+        assert list(r.experts) == list(ids), (t, r.experts, ids)
+    layer.close()
+
+
+def test_prefill_grouped_equals_token_major(gpu):
+    """R14: expert-grouped prefill == per-token moe_ffn, EXACT, including a
+    1-token case and an expert with more than 16 tokens."""
+    from llamd_rs_amd import synth
+    n_embd, n_ff, n_expert, n_used = 512, 256, 16, 4
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 700)
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    for n_tok in (1, 5, 37):
+        x = synth.normal(10 + n_tok, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+        ids, w = synth.zipf_routing(20 + n_tok, 1.1, n_tok, n_expert, n_used)
+        got = layer.prefill(x, ids.astype(np.int32), w)
+        want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
+        assert bits_equal(got, want), n_tok
+    layer.close()
+
+
+def test_prefill_config_shape_sample(gpu, qwen_layer):
+    """configs[3] shapes (hidden 2048, 128 experts, top-8, Zipf 1.1) on 48 tokens."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    n_tok = 48
+    x = synth.normal(77, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+    ids, w = synth.zipf_routing(78, 1.1, n_tok, n_expert, n_used)
+    got = layer.prefill(x, ids.astype(np.int32), w)
+    want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
+    assert bits_equal(got, want)
+
+
+@pytest.fixture(scope="module")
+def lm_head(gpu):
+    from llamd_rs_amd import synth
+    rows, k = 151936, 2048
+    w = synth.q6k_matrix(4242, 0.02, rows, k)
+    dw = gpu.DeviceWeights.upload(w, rows, k // QK_K)
+    head = gpu.LmHead(dw, max_seq=16)
+    yield head, w, rows, k
+    head.close()
+    dw.close()
+
+
+def test_lm_head_b1_logits_and_argmax_exact(gpu, lm_head):
+    from llamd_rs_amd import synth
+    head, w, rows, k = lm_head
+    x = synth.normal(31, 1.0, k)
+    logits, ids = head.forward(x)
+    want = O.matvec_q6k(w, rows, k, x)
+    assert bits_equal(logits[0], want)
+    assert ids[0] == O.argmax(want)
+
+
+def test_lm_head_b16_argmax_exact(gpu, lm_head):
+    from llamd_rs_amd import synth
+    head, w, rows, k = lm_head
+    x = synth.normal(32, 1.0, 16 * k).reshape(16, k)
+    logits, ids = head.forward(x)
+    for s in (0, 7, 15):
+        want = O.matvec_q6k(w, rows, k, x[s])
+        assert bits_equal(logits[s], want), s
+    # argmax of every sequence against the oracle's argmax of the GPU logits
+    # (identical bits) -- and of the CPU logits for the three checked above
+    for s in range(16):
+        assert ids[s] == O.argmax(logits[s]), s
