@@ -50,6 +50,10 @@ int llamd_rocm_device_info(int dev, char *name, int name_len, char *arch, int ar
 size_t llamd_rocm_free_mem(void);
 /* Not in the reference: message for the last -1/NULL returned on this thread. */
 const char *llamd_hip_last_error(void);
+/* Not in the reference: tuning overrides for measurement. Returns the previous
+ * value, -1 for an unknown key. "mv_ks": waves per 16-row tile of the Q6_K
+ * matvec (1, 2 or 4; 0 = chosen from the shape). */
+int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */
 /* llamd.hip:153-165 */

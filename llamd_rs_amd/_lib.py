@@ -35,6 +35,7 @@ SIGNATURES = {
     "llamd_rocm_device_info": (i32, [i32, cp, i32, cp, i32, C.POINTER(sz), i32p, i32p]),
     "llamd_rocm_free_mem": (sz, []),
     "llamd_hip_last_error": (cp, []),
+    "llamd_hip_tune": (i32, [cp, i32]),
     "llamd_rocm_upload": (vp, [vp, sz]),
     "llamd_rocm_release": (None, [vp]),
     "llamd_fwd_get_stream": (vp, []),

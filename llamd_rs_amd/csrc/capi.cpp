@@ -117,6 +117,16 @@ extern "C" {
 
 const char *llamd_hip_last_error(void) { return g_err; }
 
+int llamd_hip_tune(const char *key, int value) {
+    if (!key) return fail("tune: null key");
+    if (!strcmp(key, "mv_ks")) {
+        const int prev = g_tune_mv_ks;
+        g_tune_mv_ks = value;
+        return prev;
+    }
+    return fail("tune: unknown key %s", key);
+}
+
 // ---- inventory ---------------------------------------------------------------
 int llamd_rocm_device_count(void) {
     int n = 0;
@@ -411,8 +421,8 @@ int llamd_hip_route(const float *logits, int n_expert, int n_used, int32_t *ids,
     DevBuf dl((size_t)n_expert * 4), di((size_t)n_used * 4), dw((size_t)n_used * 4);
     if (!dl.p || !di.p || !dw.p) return fail("hipMalloc");
     if (!up(dl.p, logits, (size_t)n_expert * 4)) return -1;
-    if (launch_moe_route(dl.as<float>(), nullptr, nullptr, nullptr, nullptr, n_expert, 0, n_used, 0,
-                         di.as<int32_t>(), dw.as<float>(), nullptr, nullptr, stream()))
+    if (launch_route_logits(dl.as<float>(), n_expert, n_used, di.as<int32_t>(), dw.as<float>(),
+                            stream()))
         return fail("launch");
     if (!down(ids, di.p, (size_t)n_used * 4) || !down(weights, dw.p, (size_t)n_used * 4) || !sync())
         return -1;
@@ -468,8 +478,7 @@ void llamd_fwd_silu_mul(const float *gate, const float *upv, float *out, int n) 
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs) {
     (void)probs;
-    launch_moe_route(logits, nullptr, nullptr, nullptr, nullptr, n_expert, 0, n_used, 0, ids,
-                     weights, nullptr, nullptr, stream());
+    launch_route_logits(logits, n_expert, n_used, ids, weights, stream());
 }
 
 void llamd_fwd_moe_combine_add(const float *d, const float *weights, const float *residual,
@@ -503,8 +512,9 @@ struct MoeLayer {
     void *gate = nullptr, *upw = nullptr, *downw = nullptr;
     size_t sgu = 0, sd = 0;  // expert strides
     // decode scratch
-    DevBuf xq, xd, logit_f, centre, radius, logits_used, ids, weights, stats;
-    DevBuf g, u, aq, ad, dn;
+    DevBuf xq, xd, logit_f, centre, radius, exact_l, logits_used, ids, weights, stats, flag,
+        counters;
+    DevBuf g, aq, ad, dn;
     // prefill scratch (grown on demand)
     int cap_tok = 0;
     DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_tok, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
@@ -539,13 +549,15 @@ void *llamd_hip_moe_create(const float *router, const void *gate, const void *up
         m->sd = llamd_hip_q6k_tiled_bytes(n_embd, m->bf);
         ok = m->xq.alloc(n_embd) && m->xd.alloc(m->be * 4) && m->logit_f.alloc(n_expert * 4) &&
              m->centre.alloc(n_expert * 8) && m->radius.alloc(n_expert * 8) &&
+             m->exact_l.alloc(n_expert * 4) && m->flag.alloc(16) && m->counters.alloc(16) &&
              m->logits_used.alloc(n_expert * 4) && m->ids.alloc(n_used * 4) &&
              m->weights.alloc(n_used * 4) && m->stats.alloc(16) &&
-             m->g.alloc((size_t)n_used * n_ff * 4) && m->u.alloc((size_t)n_used * n_ff * 4) &&
+             m->g.alloc((size_t)2 * n_used * n_ff * 4) &&
              m->aq.alloc((size_t)n_used * n_ff) && m->ad.alloc((size_t)n_used * m->bf * 4) &&
              m->dn.alloc((size_t)n_used * n_embd * 4);
         int zero[4] = {0, 0, 0, 0};
-        ok = ok && up(m->stats.p, zero, sizeof zero) && sync();
+        ok = ok && up(m->stats.p, zero, sizeof zero) && up(m->counters.p, zero, sizeof zero) &&
+             up(m->flag.p, zero, sizeof zero) && sync();
     }
     if (!ok) {
         llamd_hip_moe_destroy(m);
@@ -570,19 +582,33 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
     if (!m || !d_x || !d_out) return fail("moe_forward: null argument");
     hipStream_t st = stream();
     int rc = 0;
-    rc |= launch_q8k_quantize(d_x, m->xq.as<int8_t>(), nullptr, m->xd.as<float>(), nullptr, m->be, st);
-    rc |= launch_router_bound(m->router.as<float>(), d_x, m->n_expert, m->n_embd,
-                              m->logit_f.as<float>(), m->centre.as<double>(),
-                              m->radius.as<double>(), st);
-    rc |= launch_moe_route(m->logit_f.as<float>(), m->centre.as<double>(), m->radius.as<double>(),
-                           m->router.as<float>(), d_x, m->n_expert, m->n_embd, m->n_used,
-                           flags & 1, m->ids.as<int32_t>(), m->weights.as<float>(),
-                           m->logits_used.as<float>(), m->stats.as<int>(), st);
+    RouterLaunch rl;
+    rl.w = m->router.as<float>();
+    rl.x = d_x;
+    rl.n_expert = m->n_expert;
+    rl.k = m->n_embd;
+    rl.n_used = m->n_used;
+    rl.force_exact = flags & 1;
+    rl.logit_f = m->logit_f.as<float>();
+    rl.centre = m->centre.as<double>();
+    rl.radius = m->radius.as<double>();
+    rl.exact_l = m->exact_l.as<float>();
+    rl.ids = m->ids.as<int32_t>();
+    rl.weights = m->weights.as<float>();
+    rl.logits_used = m->logits_used.as<float>();
+    rl.flag = m->flag.as<int>();
+    rl.counters = m->counters.as<int>();
+    rl.stats = m->stats.as<int>();
+    rl.xq = m->xq.as<int8_t>();
+    rl.xd = m->xd.as<float>();
+    rl.xblocks = m->be;
+    rc |= launch_router(rl, st);
+    // gate and up in one launch: g holds [gate | up] x n_used x n_ff
     rc |= launch_q6k_mv_b1(m->gate, m->sgu, m->ids.as<int32_t>(), m->xq.as<int8_t>(),
-                           m->xd.as<float>(), m->g.as<float>(), m->n_ff, m->be, m->n_used, 0, st);
-    rc |= launch_q6k_mv_b1(m->upw, m->sgu, m->ids.as<int32_t>(), m->xq.as<int8_t>(),
-                           m->xd.as<float>(), m->u.as<float>(), m->n_ff, m->be, m->n_used, 0, st);
-    rc |= launch_swiglu_q8k(m->g.as<float>(), m->u.as<float>(), nullptr, m->aq.as<int8_t>(), nullptr,
+                           m->xd.as<float>(), m->g.as<float>(), m->n_ff, m->be, m->n_used, 0, st,
+                           m->upw);
+    rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
+                            nullptr, m->aq.as<int8_t>(), nullptr,
                             m->ad.as<float>(), nullptr, m->n_used * m->bf, st);
     rc |= launch_q6k_mv_b1(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
                            m->ad.as<float>(), m->dn.as<float>(), m->n_embd, m->bf, m->n_used, 1, st);

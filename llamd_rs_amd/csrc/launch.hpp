@@ -10,10 +10,15 @@
 
 namespace llamd {
 
+// Tuning overrides (0 = automatic); set through llamd_hip_tune.
+extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4
+
 // q6k_mv.hip
+// y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
+// w_b (gate and up in one launch).
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st);
+                     hipStream_t st, const void *w_b = nullptr);
 // Expert-grouped batched matvec (see q6k_mv.hip). sub_start has n_groups+1
 // entries; max_subtiles bounds sub_start[n_groups] and sizes the grid. With
 // grp_expert == nullptr there is a single group (expert 0) of n_groups pairs.
@@ -38,12 +43,24 @@ int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
 int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipStream_t st);
 
 // moe.hip
-int launch_router_bound(const float *w, const float *x, int n_expert, int k, float *logit_f,
-                        double *centre, double *radius, hipStream_t st);
-int launch_moe_route(const float *logit_f, const double *centre, const double *radius,
-                     const float *w, const float *x, int n_expert, int k, int n_used,
-                     int force_exact, int32_t *ids, float *weights, float *logits_used,
-                     int *stats, hipStream_t st);
+// Router + route for one token (moe.hip): router_fast then router_exact
+// (the latter exits at once unless the fast pass could not prove the order).
+struct RouterLaunch {
+    const float *w, *x;
+    int n_expert, k, n_used, force_exact;
+    float *logit_f;
+    double *centre, *radius;
+    float *exact_l;
+    int32_t *ids;
+    float *weights, *logits_used;
+    int *flag, *counters, *stats;
+    int8_t *xq;
+    float *xd;
+    int xblocks;
+};
+int launch_router(const RouterLaunch &l, hipStream_t st);
+int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
+                        float *weights, hipStream_t st);
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
                        int n_used, int n_embd, int n_tok, hipStream_t st);
 int argmax_parts(int n);

@@ -30,6 +30,7 @@
 #include "common.hpp"
 #include "expf_ref.h"
 #include "launch.hpp"
+#include "q8k_wave.hpp"
 
 namespace llamd {
 namespace {
@@ -37,178 +38,118 @@ namespace {
 constexpr int ROUTE_MAX_EXPERTS = 256;
 constexpr int ROUTE_MAX_USED = 64;
 
-// ---- 1. router logits with a rigorous error radius -------------------------
-// One wave per expert row. Lane l owns elements [l*per, (l+1)*per).
-__global__ __launch_bounds__(256) void router_bound(const float *w, const float *x, int n_expert,
-                                                    int k, float *logit_f, double *centre,
-                                                    double *radius) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= n_expert) return;
-    const int per = k / 64;
-    const float *wr = w + (size_t)row * k + (size_t)lane * per;
-    const float *xr = x + (size_t)lane * per;
-
-    double tot = 0.0, absum = 0.0;
-    for (int i = 0; i < per; ++i) {
-        const float p = wr[i] * xr[i];  // the reference's rounded product
-        tot += (double)p;
-        absum += fabs((double)p);
-    }
-    // exclusive scan of lane totals
-    double incl = tot;
-    for (int o = 1; o < 64; o <<= 1) {
-        const double v = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += v;
-    }
-    double pre = __shfl_up(incl, 1, 64);
-    if (lane == 0) pre = 0.0;
-    // sum of |prefix sums| over global indices 1..k-1 (the fold's k >= 2)
-    double sabs = 0.0;
-    double run = pre;
-    for (int i = 0; i < per; ++i) {
-        const float p = wr[i] * xr[i];
-        run += (double)p;
-        if (lane * per + i >= 1) sabs += fabs(run);
-    }
-    const double S = wave_sum_d(tot);
-    const double A = wave_sum_d(absum);
-    const double SA = wave_sum_d(sabs);
-    if (lane == 0) {
-        const double u = 0x1p-24;
-        const double n = (double)k;
-        const double gam = n * u / (1.0 - n * u);
-        // double rounding in the scan and the sums: far below 1e-9 * A
-        const double r = u / (1.0 - u) * (SA + n * gam * A) * (1.0 + 1e-6) + 1e-9 * A + 1e-30;
-        centre[row] = S;
-        radius[row] = r;
-        logit_f[row] = (float)S;
-    }
-}
-
-// ---- 2. routing -------------------------------------------------------------
-struct RouteShared {
+// ---- routing core, shared by the kernels below ---------------------------
+// One workgroup (any multiple of 64 threads) routes n_expert <= 256 experts
+// held in LDS. `c`/`r` are the centre and radius of every logit; `l` the
+// float logits the probabilities are computed from.
+struct RouteLds {
     double c[ROUTE_MAX_EXPERTS];
     double r[ROUTE_MAX_EXPERTS];
     float l[ROUTE_MAX_EXPERTS];
     float p[ROUTE_MAX_EXPERTS];
     int sorted[ROUTE_MAX_EXPERTS];
-    float tile[ROUTE_MAX_EXPERTS][33];
+    float mx, total;
     int flag;
 };
 
-// Exact reference fold for every row: s = -0.0; s += w[t] * x[t] in order.
-__device__ void exact_logits(const float *w, const float *x, int n_expert, int k, RouteShared &sh) {
-    const int tid = threadIdx.x;
-    float acc = -0.0f;
-    for (int t0 = 0; t0 < k; t0 += 32) {
-        const int cols = (k - t0) < 32 ? (k - t0) : 32;
-        for (int idx = tid; idx < n_expert * 32; idx += blockDim.x) {
-            const int r = idx >> 5, c = idx & 31;
-            sh.tile[r][c] = c < cols ? w[(size_t)r * k + t0 + c] : 0.0f;
+// Rank experts by key (descending), ties to the lower index: the order of
+// Rust's stable sort_by in moe.rs:93-100 for a total order.
+template <class T>
+__device__ void rank_desc(const T *key, int n, int *sorted) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const T ki = key[i];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const T kj = key[j];
+            rank += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
         }
-        __syncthreads();
-        if (tid < n_expert) {
-            for (int c = 0; c < cols; ++c) {
-                const float p = sh.tile[tid][c] * x[t0 + c];
-                acc = acc + p;
-            }
-        }
-        __syncthreads();
+        sorted[rank] = i;
     }
-    if (tid < n_expert) sh.l[tid] = acc;
     __syncthreads();
 }
 
-// Single workgroup of 256 threads; n_expert <= 256.
-__global__ __launch_bounds__(256) void moe_route(const float *logit_f, const double *centre,
-                                                 const double *radius, const float *w,
-                                                 const float *x, int n_expert, int k, int n_used,
-                                                 int force_exact, int32_t *ids, float *weights,
-                                                 float *logits_used, int *stats) {
-    __shared__ RouteShared sh;
-    const int tid = threadIdx.x;
-    if (tid < n_expert) {
-        // without a centre the given logits are exact (radius 0)
-        sh.c[tid] = centre ? centre[tid] : (double)logit_f[tid];
-        sh.r[tid] = centre ? radius[tid] : 0.0;
-        sh.l[tid] = logit_f[tid];
-    }
+// Workgroup-wide max of a double (order-free), result on every thread.
+__device__ double block_max_d(double v, double *red) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmax(v, shfl_xor_d(v, m));
+    const int w = threadIdx.x >> 6;
     __syncthreads();
-    // rank by centre, ties to the lower index
-    if (tid < n_expert) {
-        const double ci = sh.c[tid];
-        int rank = 0;
-        for (int j = 0; j < n_expert; ++j) {
-            const double cj = sh.c[j];
-            rank += (cj > ci || (cj == ci && j < tid)) ? 1 : 0;
-        }
-        sh.sorted[rank] = tid;
-    }
+    if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
-    if (tid == 0) {
-        bool ok = !force_exact;
-        double cmax = sh.c[sh.sorted[0]];
-        for (int q = 0; q < n_expert && ok; ++q) ok = !isnan(sh.c[q]) && !isinf(sh.c[q]);
-        // Separation needed on top of the two radii so that the reference's
-        // probabilities cannot collapse to equal floats (then its tie rule,
-        // index order, would decide): exp(l - max) / total keeps a relative
-        // gap of 1e-6 well clear of f32 rounding.
+    double r = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = fmax(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+// Sequential f32 sum v[0] + v[1] + ... from -0.0 (Rust's .sum()), on one
+// thread, with the loads batched ahead of the dependent adds.
+__device__ float seq_sum(const float *v, int n) {
+    float acc = -0.0f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const float4 a = *(const float4 *)(v + i);
+        const float4 b = *(const float4 *)(v + i + 4);
+        acc = acc + a.x; acc = acc + a.y; acc = acc + a.z; acc = acc + a.w;
+        acc = acc + b.x; acc = acc + b.y; acc = acc + b.z; acc = acc + b.w;
+    }
+    for (; i < n; ++i) acc = acc + v[i];
+    return acc;
+}
+
+// Is the order of the n_used best logits (and the set) provably the
+// reference's? Result in sh.flag (0 = proven, 1 = not), on every thread.
+__device__ void decide(RouteLds &sh, int n_expert, int n_used, int force_exact, double *red) {
+    // every centre finite; the largest (c + r) outside the chosen set
+    double bad = 0.0, mrest = -DBL_MAX;
+    for (int q = threadIdx.x; q < n_expert; q += blockDim.x) {
+        const int j = sh.sorted[q];
+        if (isnan(sh.c[j]) || isinf(sh.c[j])) bad = 1.0;
+        if (q >= n_used) mrest = fmax(mrest, sh.c[j] + sh.r[j]);
+    }
+    bad = block_max_d(bad, red);
+    mrest = block_max_d(mrest, red);
+    if (threadIdx.x == 0) {
+        bool ok = !force_exact && bad == 0.0;
+        const double cmax = sh.c[sh.sorted[0]];
+        // Separation required on top of the two radii so the reference's
+        // probabilities exp(l - max) / total cannot collapse to equal floats
+        // (where its tie rule, index order, would decide): 1e-6 relative
+        // keeps well clear of f32 rounding.
         const double rel = 1e-6 * (1.0 + fabs(cmax));
         for (int q = 0; ok && q + 1 < n_used; ++q) {
             const int a = sh.sorted[q], b = sh.sorted[q + 1];
             ok = (sh.c[a] - sh.r[a]) - (sh.c[b] + sh.r[b]) > rel * (1.0 + fabs(sh.c[a]));
         }
         if (ok && n_used < n_expert) {
-            double mrest = -DBL_MAX;
-            for (int q = n_used; q < n_expert; ++q) {
-                const int j = sh.sorted[q];
-                mrest = fmax(mrest, sh.c[j] + sh.r[j]);
-            }
             const int last = sh.sorted[n_used - 1];
             ok = (sh.c[last] - sh.r[last]) - mrest > rel * (1.0 + fabs(sh.c[last]));
         }
-        // every chosen probability must stay far from underflow, where
-        // exp() == 0 ties would fall back to index order
+        // chosen probabilities must stay far from exp() underflow, where
+        // zero-probability ties would fall back to index order
         if (ok) ok = (sh.c[sh.sorted[n_used - 1]] - cmax) > -80.0;
         sh.flag = ok ? 0 : 1;
     }
     __syncthreads();
-    const bool exact = sh.flag != 0;
-    // with no weights the given logits are already the reference's bits
-    if (exact && w) exact_logits(w, x, n_expert, k, sh);
+}
 
-    // softmax exactly as moe.rs:82-87
-    if (tid == 0) {
-        float mx = -INFINITY;
-        for (int i = 0; i < n_expert; ++i) mx = fmaxf(mx, sh.l[i]);
-        sh.tile[0][0] = mx;
-    }
+// softmax over sh.l exactly as moe.rs:82-87 (max fold, exp, sequential
+// total from -0.0, divide), then, if `resort`, rank by probability; then
+// gather, clamp and renormalise (moe.rs:103-105) into ids/weights.
+__device__ void finish_route(RouteLds &sh, int n_expert, int n_used, bool resort, int32_t *ids,
+                             float *weights, float *logits_used, double *red) {
+    const int tid = threadIdx.x;
+    // f32::max fold: NaN-ignoring and order-free
+    double m = -INFINITY;
+    for (int i = tid; i < n_expert; i += blockDim.x)
+        if (!isnan(sh.l[i])) m = fmax(m, (double)sh.l[i]);
+    const float mx = (float)block_max_d(m, red);
+    for (int i = tid; i < n_expert; i += blockDim.x) sh.p[i] = expf_ref(sh.l[i] - mx);
     __syncthreads();
-    const float mx = sh.tile[0][0];
-    if (tid < n_expert) sh.p[tid] = expf_ref(sh.l[tid] - mx);
+    if (tid == 0) sh.total = seq_sum(sh.p, n_expert);
     __syncthreads();
-    if (tid == 0) {
-        float total = -0.0f;
-        for (int i = 0; i < n_expert; ++i) total = total + sh.p[i];
-        sh.tile[0][1] = total;
-    }
+    for (int i = tid; i < n_expert; i += blockDim.x) sh.p[i] = sh.p[i] / sh.total;
     __syncthreads();
-    if (tid < n_expert) sh.p[tid] = sh.p[tid] / sh.tile[0][1];
-    __syncthreads();
-    if (exact) {
-        // stable sort by probability desc, ties to the lower index (moe.rs:93-100)
-        if (tid < n_expert) {
-            const float pi = sh.p[tid];
-            int rank = 0;
-            for (int j = 0; j < n_expert; ++j) {
-                const float pj = sh.p[j];
-                rank += (pj > pi || (pj == pi && j < tid)) ? 1 : 0;
-            }
-            sh.sorted[rank] = tid;
-        }
-        __syncthreads();
-    }
+    if (resort) rank_desc(sh.p, n_expert, sh.sorted);
     if (tid == 0) {
         float raw[ROUTE_MAX_USED];
         float wsum = -0.0f;
@@ -221,12 +162,194 @@ __global__ __launch_bounds__(256) void moe_route(const float *logit_f, const dou
             ids[q] = sh.sorted[q];
             weights[q] = raw[q] / wsum;
         }
-        if (stats) {
-            stats[0] += 1;
-            stats[1] += exact ? 1 : 0;
+    }
+    if (logits_used)
+        for (int i = tid; i < n_expert; i += blockDim.x) logits_used[i] = sh.l[i];
+}
+
+// Loads that must see other workgroups' stores from the same kernel: bypass
+// the per-CU vector cache.
+__device__ __forceinline__ double load_dev(const double *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in exactly one workgroup: the last of `n` to arrive. The
+// counter returns to zero for the next launch.
+__device__ bool last_arrival(int *counter, int n) {
+    __shared__ int is_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const int prev = atomicAdd(counter, 1);
+        is_last = prev == n - 1;
+        if (is_last) {
+            __threadfence();
+            atomicExch(counter, 0);
         }
     }
-    if (logits_used && tid < n_expert) logits_used[tid] = sh.l[tid];
+    __syncthreads();
+    return is_last != 0;
+}
+
+struct RouterArgs {
+    const float *w;          // f32 router [n_expert][k]
+    const float *x;          // [k]
+    int n_expert, k, n_used, force_exact;
+    float *logit_f;          // [n_expert] float(centre)
+    double *centre, *radius; // [n_expert]
+    float *exact_l;          // [n_expert] reference fold (exact pass)
+    int32_t *ids;            // [n_used]
+    float *weights;          // [n_used]
+    float *logits_used;      // [n_expert] the logits the routing used
+    int *flag;               // 1: the exact pass must run
+    int *counters;           // [2] arrival counters (zero between launches)
+    int *stats;              // [2] calls, calls that needed the exact pass
+    // fused Q8_K quantisation of x for the expert matvecs
+    int8_t *xq;
+    float *xd;
+    int xblocks;
+};
+
+// ---- 1. router logits with a rigorous error radius, then the fast route ----
+// Workgroups [0, nr): one wave per expert row; lane l owns elements
+// [l*k/64, (l+1)*k/64). Workgroups [nr, nr + nq): Q8_K of x, a wave per block.
+// The last router workgroup to finish ranks the centres and routes when the
+// order is proven; otherwise it raises `flag` for router_exact.
+__global__ __launch_bounds__(256) void router_fast(RouterArgs a) {
+    const int nr = (a.n_expert + 3) / 4;
+    const int lane = threadIdx.x & 63;
+    if ((int)blockIdx.x >= nr) {
+        const int blk = ((int)blockIdx.x - nr) * 4 + (threadIdx.x >> 6);
+        if (blk < a.xblocks) {
+            const float4 xv = *(const float4 *)(a.x + (size_t)blk * QK_K + 4 * lane);
+            const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+            quantize_block_wave(v, lane, a.xq + (size_t)blk * QK_K, a.xd + blk);
+        }
+        return;
+    }
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row < a.n_expert) {
+        const int per = a.k / 64;
+        const float *wr = a.w + (size_t)row * a.k + (size_t)lane * per;
+        const float *xr = a.x + (size_t)lane * per;
+        double tot = 0.0, absum = 0.0;
+        for (int i = 0; i < per; i += 4) {
+            const float4 w4 = *(const float4 *)(wr + i);
+            const float4 x4 = *(const float4 *)(xr + i);
+            // the reference's rounded products
+            const float p0 = w4.x * x4.x, p1 = w4.y * x4.y, p2 = w4.z * x4.z, p3 = w4.w * x4.w;
+            tot += (double)p0; tot += (double)p1; tot += (double)p2; tot += (double)p3;
+            absum += fabs((double)p0) + fabs((double)p1) + fabs((double)p2) + fabs((double)p3);
+        }
+        double incl = tot;
+        for (int o = 1; o < 64; o <<= 1) {
+            const double v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        double pre = __shfl_up(incl, 1, 64);
+        if (lane == 0) pre = 0.0;
+        double sabs = 0.0, run = pre;
+        for (int i = 0; i < per; i += 4) {
+            const float4 w4 = *(const float4 *)(wr + i);
+            const float4 x4 = *(const float4 *)(xr + i);
+            const float pr[4] = {w4.x * x4.x, w4.y * x4.y, w4.z * x4.z, w4.w * x4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                run += (double)pr[j];
+                if (lane * per + i + j >= 1) sabs += fabs(run);
+            }
+        }
+        const double S = wave_sum_d(tot);
+        const double A = wave_sum_d(absum);
+        const double SA = wave_sum_d(sabs);
+        if (lane == 0) {
+            const double u = 0x1p-24;
+            const double n = (double)a.k;
+            const double gam = n * u / (1.0 - n * u);
+            // |fold - S| <= u/(1-u) sum|S^_k|, |S^_k| <= |S_k| + gamma A; the
+            // double-precision scan and sums add far less than 1e-9 A
+            const double r = u / (1.0 - u) * (SA + n * gam * A) * (1.0 + 1e-6) + 1e-9 * A + 1e-30;
+            a.centre[row] = S;
+            a.radius[row] = r;
+            a.logit_f[row] = (float)S;
+        }
+    }
+    if (!last_arrival(&a.counters[0], nr)) return;
+    __shared__ RouteLds sh;
+    __shared__ double red[4];
+    for (int i = threadIdx.x; i < a.n_expert; i += blockDim.x) {
+        sh.c[i] = load_dev(&a.centre[i]);
+        sh.r[i] = load_dev(&a.radius[i]);
+        sh.l[i] = load_dev(&a.logit_f[i]);
+    }
+    __syncthreads();
+    rank_desc(sh.c, a.n_expert, sh.sorted);
+    decide(sh, a.n_expert, a.n_used, a.force_exact, red);
+    if (threadIdx.x == 0) {
+        *a.flag = sh.flag;
+        if (a.stats) a.stats[0] += 1;
+    }
+    if (sh.flag == 0)
+        finish_route(sh, a.n_expert, a.n_used, false, a.ids, a.weights, a.logits_used, red);
+}
+
+// ---- 2. the reference's exact fold, only when router_fast could not prove --
+// One workgroup (one wave) per expert row: products of 64 columns at a time
+// are staged in LDS and lane 0 adds them in order, s = -0.0; s += w[t]*x[t]
+// (model.rs:253-262), while the next 64 columns load. The last row to finish
+// routes on the exact logits with the reference's own sort.
+__global__ __launch_bounds__(64) void router_exact(RouterArgs a) {
+    if (__hip_atomic_load(a.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;
+    const int row = blockIdx.x;
+    const int lane = threadIdx.x;
+    __shared__ float prod[2][64];
+    const float *wr = a.w + (size_t)row * a.k;
+    float wv = lane < a.k ? wr[lane] : 0.0f;
+    float xv = lane < a.k ? a.x[lane] : 0.0f;
+    float acc = -0.0f;
+    int buf = 0;
+    for (int t0 = 0; t0 < a.k; t0 += 64) {
+        prod[buf][lane] = wv * xv;
+        if (t0 + 64 + lane < a.k) {
+            wv = wr[t0 + 64 + lane];
+            xv = a.x[t0 + 64 + lane];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane == 0) {
+            const int cols = min(64, a.k - t0);
+            for (int c = 0; c < cols; ++c) acc = acc + prod[buf][c];
+        }
+        buf ^= 1;
+    }
+    if (lane == 0) a.exact_l[row] = acc;
+    if (!last_arrival(&a.counters[1], a.n_expert)) return;
+    __shared__ RouteLds sh;
+    __shared__ double red[4];
+    for (int i = threadIdx.x; i < a.n_expert; i += blockDim.x) sh.l[i] = load_dev(&a.exact_l[i]);
+    __syncthreads();
+    finish_route(sh, a.n_expert, a.n_used, true, a.ids, a.weights, a.logits_used, red);
+    if (threadIdx.x == 0 && a.stats) a.stats[1] += 1;
+}
+
+// Routing from given logits (llamd_hip_route / llamd_fwd_router): exact
+// inputs, radius 0; ties or near-collapses go through the reference's sort.
+__global__ __launch_bounds__(256) void route_logits(const float *logits, int n_expert, int n_used,
+                                                    int32_t *ids, float *weights) {
+    __shared__ RouteLds sh;
+    __shared__ double red[4];
+    for (int i = threadIdx.x; i < n_expert; i += blockDim.x) {
+        sh.l[i] = logits[i];
+        sh.c[i] = (double)logits[i];
+        sh.r[i] = 0.0;
+    }
+    __syncthreads();
+    rank_desc(sh.c, n_expert, sh.sorted);
+    decide(sh, n_expert, n_used, 0, red);
+    finish_route(sh, n_expert, n_used, sh.flag != 0, ids, weights, nullptr, red);
 }
 
 // ---- 3. weighted combine + residual (layer.rs:245-258, 281-287) -------------
@@ -373,19 +496,23 @@ __global__ __launch_bounds__(256) void f32_mv(const float *w, const float *x, fl
 
 }  // namespace
 
-int launch_router_bound(const float *w, const float *x, int n_expert, int k, float *logit_f,
-                        double *centre, double *radius, hipStream_t st) {
-    hipLaunchKernelGGL(router_bound, dim3((n_expert + 3) / 4), dim3(256), 0, st, w, x, n_expert, k,
-                       logit_f, centre, radius);
+int launch_router(const RouterLaunch &l, hipStream_t st) {
+    RouterArgs a;
+    a.w = l.w; a.x = l.x; a.n_expert = l.n_expert; a.k = l.k; a.n_used = l.n_used;
+    a.force_exact = l.force_exact; a.logit_f = l.logit_f; a.centre = l.centre;
+    a.radius = l.radius; a.exact_l = l.exact_l; a.ids = l.ids; a.weights = l.weights;
+    a.logits_used = l.logits_used; a.flag = l.flag; a.counters = l.counters; a.stats = l.stats;
+    a.xq = l.xq; a.xd = l.xd; a.xblocks = l.xblocks;
+    const int nr = (l.n_expert + 3) / 4, nq = (l.xblocks + 3) / 4;
+    hipLaunchKernelGGL(router_fast, dim3(nr + nq), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(router_exact, dim3(l.n_expert), dim3(64), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_moe_route(const float *logit_f, const double *centre, const double *radius,
-                     const float *w, const float *x, int n_expert, int k, int n_used,
-                     int force_exact, int32_t *ids, float *weights, float *logits_used,
-                     int *stats, hipStream_t st) {
-    hipLaunchKernelGGL(moe_route, dim3(1), dim3(256), 0, st, logit_f, centre, radius, w, x,
-                       n_expert, k, n_used, force_exact, ids, weights, logits_used, stats);
+int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
+                        float *weights, hipStream_t st) {
+    hipLaunchKernelGGL(route_logits, dim3(1), dim3(256), 0, st, logits, n_expert, n_used, ids,
+                       weights);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -44,6 +44,8 @@ struct MvParams {
     float *y;                 // [n_slots][rows]
     int rows, tiles, blocks, n_slots;
     int act_per_slot;         // 1: slot i uses activation i; 0: all use activation 0
+    const uint8_t *w_b;       // slots >= slots_a read this weight (ids[slot - slots_a])
+    int slots_a;              // (gate and up of the same experts in one launch)
 };
 
 __device__ __forceinline__ long make_amask(const uint32_t g[4], int c, int n, bool valid) {
@@ -69,69 +71,203 @@ __device__ __forceinline__ long unpack_codes(const uint32_t nib[8], const uint32
     return (long)((uint64_t)b0 | ((uint64_t)b1 << 32));
 }
 
-// One wave = one (slot, tile) item. 4 waves per workgroup.
+// v_perm_b32 selectors that build the A-mask dwords (see make_amask) with one
+// permute each: for class c the pair (a[16j + c], a[16j + c + 8]) sits in
+// byte (c & 3) of g[c >> 2] and of g[2 + (c >> 2)]; selector byte values
+// 0..3 pick from the second operand, 4..7 from the first, 0x0C gives zero.
+struct MaskSel {
+    uint32_t s0, s1;   // selectors for A dword 0 / dword 1 with c & 3 == 0
+    uint32_t inc0, inc1;  // added (c & 3) times for the other classes
+};
+
+__device__ __forceinline__ MaskSel mask_selectors(int n, bool valid) {
+    // the pair lands in bytes 2 (j % 4) and 2 (j % 4) + 1 of the 8-byte operand
+    const uint32_t pair = 0x0400u;              // (lo: sel 0, hi: sel 4)
+    const uint32_t shift = 16u * (n & 1);
+    const uint32_t placed = (pair << shift) | (0x0C0C0C0Cu & ~(0xFFFFu << shift));
+    const uint32_t inc = 0x0101u << shift;
+    MaskSel m;
+    const bool lo = valid && !(n & 2), hi = valid && (n & 2);
+    m.s0 = lo ? placed : 0x0C0C0C0Cu;
+    m.s1 = hi ? placed : 0x0C0C0C0Cu;
+    m.inc0 = lo ? inc : 0u;
+    m.inc1 = hi ? inc : 0u;
+    return m;
+}
+
+__device__ __forceinline__ long amask_perm(const uint32_t g[4], int c, const MaskSel &m) {
+    const uint32_t lo = g[c >> 2], hi = g[2 + (c >> 2)];
+    const uint32_t a0 = __builtin_amdgcn_perm(hi, lo, m.s0 + (uint32_t)(c & 3) * m.inc0);
+    const uint32_t a1 = __builtin_amdgcn_perm(hi, lo, m.s1 + (uint32_t)(c & 3) * m.inc1);
+    return (long)((uint64_t)a0 | ((uint64_t)a1 << 32));
+}
+
+struct BlockRegs {
+    uint4 q0, q1, q2;
+    uint32_t scw;
+    uint16_t dh;
+    uint4 g;
+    float ad;
+};
+
+__device__ __forceinline__ void load_block(BlockRegs &r, const uint8_t *seg, const int8_t *aq,
+                                           const float *ad, int b, int lane, int n) {
+    r.q0 = *(const uint4 *)(seg + 16 * lane);
+    r.q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
+    r.q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
+    r.scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
+    r.dh = *(const uint16_t *)(seg + SEG_D + 2 * n);
+    r.g = *(const uint4 *)(aq + (size_t)b * QK_K + 16 * n);
+    r.ad = ad[b];
+}
+
+// Butterfly over the 4 lanes of a row (n, n+16, n+32, n+48) with gfx950's
+// half-wave swaps. permlane32_swap(a, b) leaves a = [a_lo, b_lo] and
+// b = [a_hi, b_hi] (halves of 32 lanes), so a + b sums class c over lanes L,
+// L^32 in the low half and class c+4 in the high half; permlane16_swap does
+// the same between 16-lane rows. After both steps lane (n, s) holds the full
+// aux32 of classes 2s and 2s+1.
+__device__ __forceinline__ void reduce_classes(const int acc[8], int &c_even, int &c_odd) {
+    int r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(acc[k], acc[k + 4], false, false);
+        r[k] = (int)sw[0] + (int)sw[1];  // low half: class k, high half: class k + 4
+    }
+    const auto s0 = __builtin_amdgcn_permlane16_swap(r[0], r[2], false, false);
+    const auto s1 = __builtin_amdgcn_permlane16_swap(r[1], r[3], false, false);
+    c_even = (int)s0[0] + (int)s0[1];  // rows 0..3: classes 0, 2, 4, 6
+    c_odd = (int)s1[0] + (int)s1[1];   // rows 0..3: classes 1, 3, 5, 7
+}
+
+// Per-block float terms (f16(d) * a.d) * aux32[c] for this lane's row and its
+// two classes 2s, 2s+1: exactly the products the reference adds into
+// sums[c] (dot.rs:190-193).
+__device__ __forceinline__ void block_terms(const BlockRegs &r, const MaskSel &ms, float &t_even,
+                                            float &t_odd) {
+    const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
+    const uint32_t g[4] = {r.g.x, r.g.y, r.g.z, r.g.w};
+    const v4i zero = {0, 0, 0, 0};
+    long am[8];
+    v4i kc[8], d[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        am[c] = amask_perm(g, c, ms);
+        kc[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(am[c], NEG32_BYTES, zero, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        d[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(am[c], unpack_codes(nib, hb, c), kc[c], 0, 0, 0);
+    // int8 scales of the lane's 4 groups; 24-bit multiplies run at full rate
+    const int sc0 = __builtin_amdgcn_sbfe(r.scw, 0, 8), sc1 = __builtin_amdgcn_sbfe(r.scw, 8, 8);
+    const int sc2 = __builtin_amdgcn_sbfe(r.scw, 16, 8), sc3 = __builtin_amdgcn_sbfe(r.scw, 24, 8);
+    int acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        int v = __mul24(sc0, d[c][0]);
+        v = __mul24(sc1, d[c][1]) + v;
+        v = __mul24(sc2, d[c][2]) + v;
+        acc[c] = __mul24(sc3, d[c][3]) + v;
+    }
+    int ae, ao;
+    reduce_classes(acc, ae, ao);
+    const float dd = f16_bits_to_f32(r.dh) * r.ad;
+    t_even = dd * (float)ae;
+    t_odd = dd * (float)ao;
+}
+
+template <int KS>
+__device__ __forceinline__ void consume_terms(int b, float te, float to, float &se, float &so,
+                                              float (*terms)[TILE_ROWS][8], int n, int s) {
+    if constexpr (KS == 1) {
+        se = se + te;
+        so = so + to;
+    } else {
+        if (b < 16) {
+            terms[b][n][2 * s] = te;
+            terms[b][n][2 * s + 1] = to;
+        }
+    }
+}
+
+// One (slot, 16-row tile) item per KS waves of a 4-wave workgroup; wave kc of
+// the item takes blocks [kc*bpc, (kc+1)*bpc) with the next block's loads in
+// flight while the current one is computed. With KS > 1 the per-block terms
+// meet in LDS and are folded in block order -- the same additions in the same
+// order as a single wave walking every block, so splitting K changes the
+// latency, never the bits.
+template <int KS>
 __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
+    constexpr int IPW = 4 / KS;                 // items per workgroup
+    constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
+    __shared__ float terms[KS > 1 ? IPW : 1][KS > 1 ? MAXB : 1][TILE_ROWS][8];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int item = blockIdx.x * 4 + wave;
-    if (item >= p.n_slots * p.tiles) return;  // whole wave exits together
-    const int slot = item / p.tiles;
-    const int t = item - slot * p.tiles;
+    const int kc = wave % KS;
+    const int local = wave / KS;
+    const int item = blockIdx.x * IPW + local;
+    const bool live = item < p.n_slots * p.tiles;
+    const int slot = live ? item / p.tiles : 0;
+    const int t = live ? item - slot * p.tiles : 0;
     const int n = lane & 15;
     const int s = lane >> 4;
-    const bool valid = (n >> 2) == s;  // this lane carries the mask of group n
+    const MaskSel msel = mask_selectors(n, (n >> 2) == s);  // lane carries group n's mask
 
-    const int expert = p.ids ? p.ids[slot] : 0;
-    const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
+    const bool second = slot >= p.slots_a;
+    const int eslot = second ? slot - p.slots_a : slot;
+    const int expert = (live && p.ids) ? p.ids[eslot] : 0;
     const int act = p.act_per_slot ? slot : 0;
     const int8_t *aq = p.aq + (size_t)act * p.blocks * QK_K;
     const float *ad = p.ad + (size_t)act * p.blocks;
+    const uint8_t *seg0 = (second ? p.w_b : p.w) + (size_t)expert * p.expert_stride +
+                          (size_t)t * p.blocks * SEG_BYTES;
 
-    float sums[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) sums[c] = 0.0f;
+    const int bpc = (p.blocks + KS - 1) / KS;
+    const int b0 = kc * bpc;
+    const int b1 = min(p.blocks, b0 + bpc);
 
-    for (int b = 0; b < p.blocks; ++b, seg += SEG_BYTES) {
-        const uint4 q0 = *(const uint4 *)(seg + 16 * lane);
-        const uint4 q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
-        const uint4 q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
-        const uint32_t scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
-        const uint16_t dh = *(const uint16_t *)(seg + SEG_D + 2 * n);
-        const uint4 gv = *(const uint4 *)(aq + (size_t)b * QK_K + 16 * n);
-        const float adb = ad[b];
-
-        const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
-        const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
-        const int sc0 = (int8_t)(scw & 0xFF), sc1 = (int8_t)((scw >> 8) & 0xFF);
-        const int sc2 = (int8_t)((scw >> 16) & 0xFF), sc3 = (int8_t)(scw >> 24);
-
-        int acc[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const long am = make_amask(g, c, n, valid);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i kc = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, NEG32_BYTES, zero, 0, 0, 0);
-            const long bw = unpack_codes(nib, hb, c);
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, bw, kc, 0, 0, 0);
-            acc[c] = sc0 * d[0] + sc1 * d[1] + sc2 * d[2] + sc3 * d[3];
+    float se = 0.0f, so = 0.0f;  // classes 2s and 2s+1 of row n
+    if (live && b0 < b1) {
+        // two register sets in ping-pong: the next block's loads are in
+        // flight while the current block is computed, with no copies
+        BlockRegs ra, rb;
+        load_block(ra, seg0 + (size_t)b0 * SEG_BYTES, aq, ad, b0, lane, n);
+        for (int b = b0; b < b1; b += 2) {
+            if (b + 1 < b1) load_block(rb, seg0 + (size_t)(b + 1) * SEG_BYTES, aq, ad, b + 1, lane, n);
+            float te, to;
+            block_terms(ra, msel, te, to);
+            consume_terms<KS>(b, te, to, se, so, terms[local], n, s);
+            if (b + 1 >= b1) break;
+            if (b + 2 < b1) load_block(ra, seg0 + (size_t)(b + 2) * SEG_BYTES, aq, ad, b + 2, lane, n);
+            block_terms(rb, msel, te, to);
+            consume_terms<KS>(b + 1, te, to, se, so, terms[local], n, s);
         }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            acc[c] += shfl_xor_i(acc[c], 16);
-            acc[c] += shfl_xor_i(acc[c], 32);
-        }
-        const float dd = f16_bits_to_f32(dh) * adb;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) sums[c] = sums[c] + dd * (float)acc[c];
     }
-
+    if constexpr (KS > 1) {
+        __syncthreads();
+        if (!live || kc != 0) return;
+        // fold in block order, classes 2s and 2s+1 on lane (n, s)
+        for (int b = 0; b < p.blocks; ++b) {
+            se = se + terms[local][b][n][2 * s];
+            so = so + terms[local][b][n][2 * s + 1];
+        }
+    } else {
+        if (!live) return;
+    }
+    // lane (n, 0) adds the eight class sums in class order (dot.rs:195)
+    float cls[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
+        cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
+    }
     if (s == 0) {
         const int row = t * TILE_ROWS + n;
         if (row < p.rows) {
             float tot = -0.0f;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) tot = tot + sums[c];
+            for (int c = 0; c < 8; ++c) tot = tot + cls[c];
             p.y[(size_t)slot * p.rows + row] = tot;
         }
     }
@@ -308,10 +444,16 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
 
 }  // namespace
 
+int g_tune_mv_ks = 0;
+
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st) {
+                     hipStream_t st, const void *w_b) {
     MvParams p;
+    // with a second weight, slots [n_slots, 2 n_slots) repeat the ids on it
+    p.w_b = (const uint8_t *)w_b;
+    p.slots_a = w_b ? n_slots : 0x7FFFFFFF;
+    if (w_b) n_slots *= 2;
     p.w = (const uint8_t *)w;
     p.expert_stride = expert_stride;
     p.ids = ids;
@@ -324,7 +466,26 @@ int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, co
     p.n_slots = n_slots;
     p.act_per_slot = act_per_slot;
     const int items = p.tiles * n_slots;
-    hipLaunchKernelGGL(q6k_mv_b1, dim3((items + 3) / 4), dim3(256), 0, st, p);
+    const int ks = g_tune_mv_ks;
+    if (ks == 1 || ks == 2 || ks == 4) {
+        const int ipw = 4 / ks;
+        if (ks == 1 || blocks <= 16) {
+            if (ks == 1) hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
+            if (ks == 2) hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + ipw - 1) / ipw), dim3(256), 0, st, p);
+            if (ks == 4) hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
+    if (blocks > 16 && items < 2048) {
+        // LDS holds up to 16 block terms per item; longer rows use one wave
+        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
+    } else if (items >= 4096) {
+        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
+    } else if (items >= 1024) {
+        hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + 1) / 2), dim3(256), 0, st, p);
+    } else {
+        hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

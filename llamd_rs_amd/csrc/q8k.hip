@@ -16,59 +16,10 @@
 #include "common.hpp"
 #include "expf_ref.h"
 #include "launch.hpp"
+#include "q8k_wave.hpp"
 
 namespace llamd {
 namespace {
-
-// qs: natural order (the reference's BlockQ8K.qs). qs_cm (optional): the same
-// quants in class-major order, byte 32 * (e % 8) + e / 8 for element e, which
-// is what the batched kernel's MFMA operand loads want.
-__device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t *qs, int8_t *qs_cm,
-                                              float *d, int16_t *bsums) {
-    float amax = 0.0f, mx = 0.0f;
-    int idx = 0x7FFFFFFF;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > amax) { amax = a; mx = v[i]; idx = 4 * lane + i; }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float oa = shfl_xor_f(amax, m);
-        const float om = shfl_xor_f(mx, m);
-        const int oi = shfl_xor_i(idx, m);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
-    int q[4];
-    float dv;
-    if (amax == 0.0f) {
-        q[0] = q[1] = q[2] = q[3] = 0;
-        dv = 0.0f;
-    } else {
-        const float iscale = -127.0f / mx;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = (int)__builtin_rintf(iscale * v[i]);
-            q[i] = r < 127 ? r : 127;
-        }
-        dv = 1.0f / iscale;
-    }
-    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-    if (qs) *(uint32_t *)(qs + 4 * lane) = packed;
-    if (qs_cm) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * lane + i;
-            qs_cm[32 * (e & 7) + (e >> 3)] = (int8_t)q[i];
-        }
-    }
-    int gs = q[0] + q[1] + q[2] + q[3];
-    gs += shfl_xor_i(gs, 1);
-    gs += shfl_xor_i(gs, 2);
-    if (bsums && (lane & 3) == 0) bsums[lane >> 2] = (int16_t)gs;
-    if (lane == 0) *d = dv;
-}
 
 __global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm,
                                                     float *d, int16_t *bsums, int nblocks) {
