@@ -527,12 +527,12 @@ extern "C" {
 void *llamd_hip_moe_create(const float *router, const void *gate, const void *upw,
                            const void *downw, int n_embd, int n_ff, int n_expert, int n_used) {
     if (!router || !gate || !upw || !downw) { fail("moe_create: null weight"); return nullptr; }
-    if (n_embd <= 0 || n_ff <= 0 || n_embd % QK || n_ff % QK || n_embd % 64) {
-        fail("moe_create: n_embd and n_ff must be multiples of 256");
+    if (n_embd <= 0 || n_ff <= 0 || n_embd % QK || n_ff % QK || n_embd > 2048) {
+        fail("moe_create: n_embd and n_ff must be multiples of 256, n_embd <= 2048");
         return nullptr;
     }
-    if (n_expert <= 0 || n_expert > 256 || n_used <= 0 || n_used > n_expert || n_used > 64) {
-        fail("moe_create: need 0 < n_used <= n_expert <= 256, n_used <= 64");
+    if (n_expert <= 0 || n_expert > 256 || n_used <= 0 || n_used > n_expert || n_used > 16) {
+        fail("moe_create: need 0 < n_used <= n_expert <= 256, n_used <= 16");
         return nullptr;
     }
     MoeLayer *m = new MoeLayer();
@@ -608,12 +608,12 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
                            m->xd.as<float>(), m->g.as<float>(), m->n_ff, m->be, m->n_used, 0, st,
                            m->upw);
     rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
-                            nullptr, m->aq.as<int8_t>(), nullptr,
-                            m->ad.as<float>(), nullptr, m->n_used * m->bf, st);
-    rc |= launch_q6k_mv_b1(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
-                           m->ad.as<float>(), m->dn.as<float>(), m->n_embd, m->bf, m->n_used, 1, st);
-    rc |= launch_moe_combine(m->dn.as<float>(), m->weights.as<float>(), d_res, d_out, m->n_used,
-                             m->n_embd, 1, st);
+                            nullptr, m->aq.as<int8_t>(), nullptr, m->ad.as<float>(), nullptr,
+                            m->n_used * m->bf, st);
+    // down projection of the routed experts + weighted combine + residual
+    rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
+                                  m->ad.as<float>(), m->weights.as<float>(), d_res, d_out,
+                                  m->n_embd, m->bf, m->n_used, st);
     return rc ? fail("moe_forward: launch failed") : 0;
 }
 

@@ -19,6 +19,12 @@ extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
                      hipStream_t st, const void *w_b = nullptr);
+// Down projection of n_slots routed experts (activation e for slot e) and the
+// routing-weighted combine (+ residual) into out, one workgroup per 16 rows.
+int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
+                            const int8_t *aq, const float *ad, const float *weights,
+                            const float *res, float *out, int rows, int blocks, int n_slots,
+                            hipStream_t st);
 // Expert-grouped batched matvec (see q6k_mv.hip). sub_start has n_groups+1
 // entries; max_subtiles bounds sub_start[n_groups] and sizes the grid. With
 // grp_expert == nullptr there is a single group (expert 0) of n_groups pairs.

@@ -35,136 +35,189 @@
 namespace llamd {
 namespace {
 
+// Phase timestamps for measurement builds; compiled out otherwise.
+#ifndef LLAMD_PROBE
+#define LLAMD_PROBE(slot) ((void)0)
+#endif
+#ifndef LLAMD_DEBUG_DECIDE
+#define LLAMD_DEBUG_DECIDE(i, v) ((void)0)
+#endif
+
 constexpr int ROUTE_MAX_EXPERTS = 256;
 constexpr int ROUTE_MAX_USED = 64;
 
-// ---- routing core, shared by the kernels below ---------------------------
-// One workgroup (any multiple of 64 threads) routes n_expert <= 256 experts
-// held in LDS. `c`/`r` are the centre and radius of every logit; `l` the
-// float logits the probabilities are computed from.
+// ---- routing core (one wave), shared by the kernels below -----------------
+// n_expert <= 256 experts, lane l owning experts l, l+64, l+128, l+192. Top-k
+// is n_sel rounds of a wave-wide (key desc, index asc) arg-max: exactly the
+// first n_sel entries of Rust's stable sort_by in moe.rs:93-100 (a total
+// order once ties go to the lower index).
+constexpr int RW = ROUTE_MAX_EXPERTS / WAVE;  // experts per lane
+
 struct RouteLds {
-    double c[ROUTE_MAX_EXPERTS];
-    double r[ROUTE_MAX_EXPERTS];
-    float l[ROUTE_MAX_EXPERTS];
     float p[ROUTE_MAX_EXPERTS];
-    int sorted[ROUTE_MAX_EXPERTS];
-    float mx, total;
-    int flag;
+    int sorted[ROUTE_MAX_USED + 1];
 };
 
-// Rank experts by key (descending), ties to the lower index: the order of
-// Rust's stable sort_by in moe.rs:93-100 for a total order.
-template <class T>
-__device__ void rank_desc(const T *key, int n, int *sorted) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const T ki = key[i];
-        int rank = 0;
-        for (int j = 0; j < n; ++j) {
-            const T kj = key[j];
-            rank += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
+__device__ __forceinline__ bool beats(double av, int ai, double bv, int bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+__device__ __forceinline__ void wave_best(double &v, int &i) { wave_argmax(v, i, (double)-INFINITY); }
+
+__device__ __forceinline__ double wave_max_d(double v) {
+    return wave_reduce(v, (double)-INFINITY, [](double a, double b) { return fmax(a, b); });
+}
+
+// Select the n_sel best of key[] (per-lane registers, invalid = -inf with
+// index INT_MAX); marks the chosen in `taken`, writes their indices to sorted.
+__device__ void wave_select(const double key[RW], int n_sel, unsigned &taken, int *sorted) {
+    const int lane = threadIdx.x & 63;
+    for (int r = 0; r < n_sel; ++r) {
+        double bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const bool live = !(taken & (1u << j)) && key[j] != -INFINITY;
+            argmax_step(bv, bi, live ? key[j] : (double)-INFINITY, live ? lane + WAVE * j : 0x7FFFFFFF);
         }
-        sorted[rank] = i;
+        wave_best(bv, bi);
+        taken |= (bi != 0x7FFFFFFF && (bi & 63) == lane) ? 1u << (bi >> 6) : 0u;
+        if (lane == 0) sorted[r] = bi;
     }
-    __syncthreads();
 }
 
-// Workgroup-wide max of a double (order-free), result on every thread.
-__device__ double block_max_d(double v, double *red) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmax(v, shfl_xor_d(v, m));
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    double r = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = fmax(r, red[i]);
-    __syncthreads();
-    return r;
-}
-
-// Sequential f32 sum v[0] + v[1] + ... from -0.0 (Rust's .sum()), on one
-// thread, with the loads batched ahead of the dependent adds.
-__device__ float seq_sum(const float *v, int n) {
-    float acc = -0.0f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        const float4 a = *(const float4 *)(v + i);
-        const float4 b = *(const float4 *)(v + i + 4);
-        acc = acc + a.x; acc = acc + a.y; acc = acc + a.z; acc = acc + a.w;
-        acc = acc + b.x; acc = acc + b.y; acc = acc + b.z; acc = acc + b.w;
+// Is the order of the n_used best centres (and the set) provably the
+// reference's? c/r: this lane's centres and radii. Returns the verdict on
+// every lane and leaves the selection in sh.sorted.
+__device__ bool route_decide(const double c[RW], const double r[RW], int n_expert, int n_used,
+                             int force_exact, RouteLds &sh) {
+    const int lane = threadIdx.x & 63;
+    double key[RW];
+    double bad = 0.0;
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const bool live = lane + WAVE * j < n_expert;
+        if (live && (isnan(c[j]) || isinf(c[j]))) bad = 1.0;
+        key[j] = live && !isnan(c[j]) ? c[j] : -INFINITY;
     }
-    for (; i < n; ++i) acc = acc + v[i];
-    return acc;
-}
-
-// Is the order of the n_used best logits (and the set) provably the
-// reference's? Result in sh.flag (0 = proven, 1 = not), on every thread.
-__device__ void decide(RouteLds &sh, int n_expert, int n_used, int force_exact, double *red) {
-    // every centre finite; the largest (c + r) outside the chosen set
-    double bad = 0.0, mrest = -DBL_MAX;
-    for (int q = threadIdx.x; q < n_expert; q += blockDim.x) {
-        const int j = sh.sorted[q];
-        if (isnan(sh.c[j]) || isinf(sh.c[j])) bad = 1.0;
-        if (q >= n_used) mrest = fmax(mrest, sh.c[j] + sh.r[j]);
+    bad = wave_max_d(bad);
+    LLAMD_PROBE(6);
+    unsigned taken = 0;
+    wave_select(key, n_used, taken, sh.sorted);
+    LLAMD_PROBE(7);
+    // the largest c + r among experts not chosen
+    double mrest = -DBL_MAX;
+#pragma unroll
+    for (int j = 0; j < RW; ++j)
+        if (lane + WAVE * j < n_expert && !(taken & (1u << j))) mrest = fmax(mrest, c[j] + r[j]);
+    mrest = wave_max_d(mrest);
+    __builtin_amdgcn_wave_barrier();
+    // centre and radius of the chosen, in order, gathered by lane 0 via LDS
+    __shared__ double cr[2][ROUTE_MAX_USED];
+    for (int q = 0; q < n_used; ++q) {
+        const int i = sh.sorted[q];
+        if ((i & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < RW; ++j)
+                if ((i >> 6) == j) { cr[0][q] = c[j]; cr[1][q] = r[j]; }
+        }
     }
-    bad = block_max_d(bad, red);
-    mrest = block_max_d(mrest, red);
-    if (threadIdx.x == 0) {
-        bool ok = !force_exact && bad == 0.0;
-        const double cmax = sh.c[sh.sorted[0]];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int ok = 0;
+    if (lane == 0) {
+        bool good = !force_exact && bad == 0.0 && sh.sorted[0] != 0x7FFFFFFF;
+        const double cmax = cr[0][0];
         // Separation required on top of the two radii so the reference's
         // probabilities exp(l - max) / total cannot collapse to equal floats
         // (where its tie rule, index order, would decide): 1e-6 relative
         // keeps well clear of f32 rounding.
         const double rel = 1e-6 * (1.0 + fabs(cmax));
-        for (int q = 0; ok && q + 1 < n_used; ++q) {
-            const int a = sh.sorted[q], b = sh.sorted[q + 1];
-            ok = (sh.c[a] - sh.r[a]) - (sh.c[b] + sh.r[b]) > rel * (1.0 + fabs(sh.c[a]));
-        }
-        if (ok && n_used < n_expert) {
-            const int last = sh.sorted[n_used - 1];
-            ok = (sh.c[last] - sh.r[last]) - mrest > rel * (1.0 + fabs(sh.c[last]));
-        }
+        for (int q = 0; good && q + 1 < n_used; ++q)
+            good = (cr[0][q] - cr[1][q]) - (cr[0][q + 1] + cr[1][q + 1]) > rel * (1.0 + fabs(cr[0][q]));
+        if (good && n_used < n_expert)
+            good = (cr[0][n_used - 1] - cr[1][n_used - 1]) - mrest > rel * (1.0 + fabs(cr[0][n_used - 1]));
         // chosen probabilities must stay far from exp() underflow, where
         // zero-probability ties would fall back to index order
-        if (ok) ok = (sh.c[sh.sorted[n_used - 1]] - cmax) > -80.0;
-        sh.flag = ok ? 0 : 1;
+        if (good) good = cr[0][n_used - 1] - cmax > -80.0;
+        ok = good ? 1 : 0;
+        LLAMD_DEBUG_DECIDE(0, bad);
+        LLAMD_DEBUG_DECIDE(1, mrest);
+        LLAMD_DEBUG_DECIDE(2, (double)sh.sorted[0]);
+        for (int q = 0; q < n_used && q < 8; ++q) {
+            LLAMD_DEBUG_DECIDE(3 + 2 * q, cr[0][q]);
+            LLAMD_DEBUG_DECIDE(4 + 2 * q, cr[1][q]);
+        }
     }
-    __syncthreads();
+    return __shfl(ok, 0, WAVE) != 0;
 }
 
-// softmax over sh.l exactly as moe.rs:82-87 (max fold, exp, sequential
-// total from -0.0, divide), then, if `resort`, rank by probability; then
-// gather, clamp and renormalise (moe.rs:103-105) into ids/weights.
-__device__ void finish_route(RouteLds &sh, int n_expert, int n_used, bool resort, int32_t *ids,
-                             float *weights, float *logits_used, double *red) {
-    const int tid = threadIdx.x;
-    // f32::max fold: NaN-ignoring and order-free
-    double m = -INFINITY;
-    for (int i = tid; i < n_expert; i += blockDim.x)
-        if (!isnan(sh.l[i])) m = fmax(m, (double)sh.l[i]);
-    const float mx = (float)block_max_d(m, red);
-    for (int i = tid; i < n_expert; i += blockDim.x) sh.p[i] = expf_ref(sh.l[i] - mx);
-    __syncthreads();
-    if (tid == 0) sh.total = seq_sum(sh.p, n_expert);
-    __syncthreads();
-    for (int i = tid; i < n_expert; i += blockDim.x) sh.p[i] = sh.p[i] / sh.total;
-    __syncthreads();
-    if (resort) rank_desc(sh.p, n_expert, sh.sorted);
-    if (tid == 0) {
-        float raw[ROUTE_MAX_USED];
-        float wsum = -0.0f;
-        for (int q = 0; q < n_used; ++q) {
-            raw[q] = sh.p[sh.sorted[q]];
-            wsum = wsum + raw[q];
+// softmax of this lane's logits l[] exactly as moe.rs:82-87 (max fold, exp,
+// sequential total from -0.0, divide); if `resort`, select by probability;
+// then gather, clamp and renormalise (moe.rs:103-105).
+__device__ void route_finish(const float l[RW], int n_expert, int n_used, bool resort,
+                             RouteLds &sh, int32_t *ids, float *weights, float *logits_used) {
+    const int lane = threadIdx.x & 63;
+    double m = -INFINITY;  // f32::max fold: NaN-ignoring, order-free
+#pragma unroll
+    for (int j = 0; j < RW; ++j)
+        if (lane + WAVE * j < n_expert && !isnan(l[j])) m = fmax(m, (double)l[j]);
+    const float mx = (float)wave_max_d(m);
+    float p[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int i = lane + WAVE * j;
+        p[j] = 0.0f;
+        if (i < n_expert) {
+            p[j] = expf_ref(l[j] - mx);
+            sh.p[i] = p[j];
+            if (logits_used) logits_used[i] = l[j];
         }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float total = 0.0f;
+    if (lane == 0) {
+        float acc = -0.0f;
+        int i = 0;
+        for (; i + 8 <= n_expert; i += 8) {
+            const float4 u = *(const float4 *)(sh.p + i);
+            const float4 v = *(const float4 *)(sh.p + i + 4);
+            acc = acc + u.x; acc = acc + u.y; acc = acc + u.z; acc = acc + u.w;
+            acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+        }
+        for (; i < n_expert; ++i) acc = acc + sh.p[i];
+        total = acc;
+    }
+    total = __shfl(total, 0, WAVE);
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int i = lane + WAVE * j;
+        if (i < n_expert) {
+            p[j] = p[j] / total;
+            sh.p[i] = p[j];
+        }
+    }
+    if (resort) {
+        double key[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j) key[j] = lane + WAVE * j < n_expert ? (double)p[j] : -INFINITY;
+        // probabilities are >= 0, so -inf only marks absent experts
+        unsigned taken = 0;
+        wave_select(key, n_used, taken, sh.sorted);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane == 0) {
+        // raw = p[chosen]; sum from -0.0, clamped; w = raw / sum (moe.rs:103-105)
+        float wsum = -0.0f;
+        for (int q = 0; q < n_used; ++q) wsum = wsum + sh.p[sh.sorted[q]];
         wsum = fmaxf(wsum, WEIGHT_SUM_FLOOR);
         for (int q = 0; q < n_used; ++q) {
             ids[q] = sh.sorted[q];
-            weights[q] = raw[q] / wsum;
+            weights[q] = sh.p[sh.sorted[q]] / wsum;
         }
     }
-    if (logits_used)
-        for (int i = tid; i < n_expert; i += blockDim.x) logits_used[i] = sh.l[i];
 }
 
 // Loads that must see other workgroups' stores from the same kernel: bypass
@@ -213,6 +266,45 @@ struct RouterArgs {
     int xblocks;
 };
 
+// The reference's fold s = -0.0; s += w[t] * x[t] (model.rs:253-262) for every
+// row, by one 256-thread workgroup: 32-column tiles of all rows are staged in
+// LDS (four tiles in flight) and thread r adds row r's products in order.
+// Results land in sh.p (as scratch) indexed by row.
+__device__ void exact_fold_wg(const RouterArgs &a, RouteLds &sh, float *lds, int lds_floats) {
+    const int tid = threadIdx.x;
+    // columns per tile: two tiles of n_expert x (tc + 1) floats must fit
+    int tc = 32;
+    while (tc > 4 && 2 * a.n_expert * (tc + 1) > lds_floats) tc /= 2;
+    const int ld = tc + 1;
+    const int ntile = a.k / tc;
+    auto stage = [&](int t) {
+        float *dst = lds + (t & 1) * a.n_expert * ld;
+        for (int idx = tid; idx < a.n_expert * (tc / 4); idx += blockDim.x) {
+            const int r = idx / (tc / 4), c4 = idx % (tc / 4);
+            const float4 v = *(const float4 *)(a.w + (size_t)r * a.k + (size_t)t * tc + 4 * c4);
+            float *d = dst + r * ld + 4 * c4;
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+    };
+    stage(0);
+    float acc = -0.0f;
+    for (int t = 0; t < ntile; ++t) {
+        __syncthreads();
+        if (t + 1 < ntile) stage(t + 1);
+        if (tid < a.n_expert) {
+            const float *row = lds + (t & 1) * a.n_expert * ld + tid * ld;
+            const float *xs = a.x + (size_t)t * tc;
+            for (int c = 0; c < tc; ++c) {
+                const float p = row[c] * xs[c];
+                acc = acc + p;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < a.n_expert) sh.p[tid] = acc;
+    __syncthreads();
+}
+
 // ---- 1. router logits with a rigorous error radius, then the fast route ----
 // Workgroups [0, nr): one wave per expert row; lane l owns elements
 // [l*k/64, (l+1)*k/64). Workgroups [nr, nr + nq): Q8_K of x, a wave per block.
@@ -230,36 +322,55 @@ __global__ __launch_bounds__(256) void router_fast(RouterArgs a) {
         }
         return;
     }
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row < a.n_expert) {
-        const int per = a.k / 64;
-        const float *wr = a.w + (size_t)row * a.k + (size_t)lane * per;
-        const float *xr = a.x + (size_t)lane * per;
+    LLAMD_PROBE(0);
+    // Coalesced loads staged through LDS so that each lane then owns 32
+    // CONTIGUOUS elements (the prefix-sum bound needs index order). Rows are
+    // padded by 4 floats every 32 so the per-lane 16-byte reads of a 16-lane
+    // group hit disjoint banks.
+    constexpr int PAD = 36;  // floats per 32-element lane chunk
+    __shared__ float stage_flat[5 * 64 * PAD];  // x, then one row per wave
+    float (*stage)[64 * PAD] = (float (*)[64 * PAD])stage_flat;
+    const int wv = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + wv;
+    const int per = a.k / 64;  // elements per lane (32 at k = 2048)
+    for (int v = wv; v < 5; v += 4) {
+        const float *src = v == 0 ? a.x : a.w + (size_t)(blockIdx.x * 4 + v - 1) * a.k;
+        if (v == 0 || blockIdx.x * 4 + v - 1 < a.n_expert)
+            for (int e4 = lane; e4 < a.k / 4; e4 += 64) {
+                const float4 q = *(const float4 *)(src + 4 * e4);
+                const int e = 4 * e4;
+                *(float4 *)(&stage[v][(e / per) * PAD + e % per]) = q;
+            }
+    }
+    __syncthreads();
+    if (row < a.n_expert && per <= 32) {
+        const float *xs = &stage[0][lane * PAD];
+        const float *ws = &stage[1 + wv][lane * PAD];
+        float pr[32];
         double tot = 0.0, absum = 0.0;
-        for (int i = 0; i < per; i += 4) {
-            const float4 w4 = *(const float4 *)(wr + i);
-            const float4 x4 = *(const float4 *)(xr + i);
-            // the reference's rounded products
-            const float p0 = w4.x * x4.x, p1 = w4.y * x4.y, p2 = w4.z * x4.z, p3 = w4.w * x4.w;
-            tot += (double)p0; tot += (double)p1; tot += (double)p2; tot += (double)p3;
-            absum += fabs((double)p0) + fabs((double)p1) + fabs((double)p2) + fabs((double)p3);
-        }
-        double incl = tot;
-        for (int o = 1; o < 64; o <<= 1) {
-            const double v = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += v;
-        }
-        double pre = __shfl_up(incl, 1, 64);
-        if (lane == 0) pre = 0.0;
-        double sabs = 0.0, run = pre;
-        for (int i = 0; i < per; i += 4) {
-            const float4 w4 = *(const float4 *)(wr + i);
-            const float4 x4 = *(const float4 *)(xr + i);
-            const float pr[4] = {w4.x * x4.x, w4.y * x4.y, w4.z * x4.z, w4.w * x4.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                run += (double)pr[j];
-                if (lane * per + i + j >= 1) sabs += fabs(run);
+        for (int i = 0; i < 32; i += 4) {
+            if (i < per) {
+                const float4 w4 = *(const float4 *)(ws + i);
+                const float4 x4 = *(const float4 *)(xs + i);
+                // the reference's rounded products
+                pr[i] = w4.x * x4.x; pr[i + 1] = w4.y * x4.y;
+                pr[i + 2] = w4.z * x4.z; pr[i + 3] = w4.w * x4.w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    tot += (double)pr[i + j];
+                    absum += fabs((double)pr[i + j]);
+                }
+            }
+        }
+        // exclusive prefix of the lane totals, then |S_k| over this lane's k
+        const double pre = wave_inclusive_sum(tot) - tot;
+        double sabs = 0.0, run = pre;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i < per) {
+                run += (double)pr[i];
+                if (lane * per + i >= 1) sabs += fabs(run);
             }
         }
         const double S = wave_sum_d(tot);
@@ -277,23 +388,47 @@ __global__ __launch_bounds__(256) void router_fast(RouterArgs a) {
             a.logit_f[row] = (float)S;
         }
     }
+    LLAMD_PROBE(1);
     if (!last_arrival(&a.counters[0], nr)) return;
+    LLAMD_PROBE(2);
     __shared__ RouteLds sh;
-    __shared__ double red[4];
-    for (int i = threadIdx.x; i < a.n_expert; i += blockDim.x) {
-        sh.c[i] = load_dev(&a.centre[i]);
-        sh.r[i] = load_dev(&a.radius[i]);
-        sh.l[i] = load_dev(&a.logit_f[i]);
+    __shared__ int verdict;
+    if (threadIdx.x < WAVE) {
+        double c[RW], r[RW];
+        float l[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const int i = lane + WAVE * j;
+            c[j] = i < a.n_expert ? load_dev(&a.centre[i]) : 0.0;
+            r[j] = i < a.n_expert ? load_dev(&a.radius[i]) : 0.0;
+            l[j] = i < a.n_expert ? load_dev(&a.logit_f[i]) : 0.0f;
+        }
+        LLAMD_PROBE(3);
+        const bool ok = route_decide(c, r, a.n_expert, a.n_used, a.force_exact, sh);
+        LLAMD_PROBE(4);
+        if (lane == 0) {
+            verdict = ok ? 0 : 1;
+            *a.flag = a.force_exact ? 1 : 0;  // exact mode: router_exact runs next
+            if (a.stats) a.stats[0] += 1;
+        }
+        if (ok) route_finish(l, a.n_expert, a.n_used, false, sh, a.ids, a.weights, a.logits_used);
+        LLAMD_PROBE(5);
     }
     __syncthreads();
-    rank_desc(sh.c, a.n_expert, sh.sorted);
-    decide(sh, a.n_expert, a.n_used, a.force_exact, red);
-    if (threadIdx.x == 0) {
-        *a.flag = sh.flag;
-        if (a.stats) a.stats[0] += 1;
+    if (verdict == 0 || a.force_exact) return;
+    // The order was not provable (rare): this workgroup computes the
+    // reference's exact sequential fold for every row and routes on it.
+    exact_fold_wg(a, sh, stage_flat, 5 * 64 * PAD);
+    if (threadIdx.x < WAVE) {
+        float l[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const int i = lane + WAVE * j;
+            l[j] = i < a.n_expert ? sh.p[i] : 0.0f;
+        }
+        route_finish(l, a.n_expert, a.n_used, true, sh, a.ids, a.weights, a.logits_used);
+        if (lane == 0 && a.stats) a.stats[1] += 1;
     }
-    if (sh.flag == 0)
-        finish_route(sh, a.n_expert, a.n_used, false, a.ids, a.weights, a.logits_used, red);
 }
 
 // ---- 2. the reference's exact fold, only when router_fast could not prove --
@@ -328,28 +463,33 @@ __global__ __launch_bounds__(64) void router_exact(RouterArgs a) {
     if (lane == 0) a.exact_l[row] = acc;
     if (!last_arrival(&a.counters[1], a.n_expert)) return;
     __shared__ RouteLds sh;
-    __shared__ double red[4];
-    for (int i = threadIdx.x; i < a.n_expert; i += blockDim.x) sh.l[i] = load_dev(&a.exact_l[i]);
-    __syncthreads();
-    finish_route(sh, a.n_expert, a.n_used, true, a.ids, a.weights, a.logits_used, red);
-    if (threadIdx.x == 0 && a.stats) a.stats[1] += 1;
+    float l[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int i = lane + WAVE * j;
+        l[j] = i < a.n_expert ? load_dev(&a.exact_l[i]) : 0.0f;
+    }
+    route_finish(l, a.n_expert, a.n_used, true, sh, a.ids, a.weights, a.logits_used);
+    if (lane == 0 && a.stats) a.stats[1] += 1;
 }
 
 // Routing from given logits (llamd_hip_route / llamd_fwd_router): exact
 // inputs, radius 0; ties or near-collapses go through the reference's sort.
-__global__ __launch_bounds__(256) void route_logits(const float *logits, int n_expert, int n_used,
-                                                    int32_t *ids, float *weights) {
+__global__ __launch_bounds__(64) void route_logits(const float *logits, int n_expert, int n_used,
+                                                   int32_t *ids, float *weights) {
     __shared__ RouteLds sh;
-    __shared__ double red[4];
-    for (int i = threadIdx.x; i < n_expert; i += blockDim.x) {
-        sh.l[i] = logits[i];
-        sh.c[i] = (double)logits[i];
-        sh.r[i] = 0.0;
+    const int lane = threadIdx.x;
+    double c[RW], r[RW];
+    float l[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int i = lane + WAVE * j;
+        l[j] = i < n_expert ? logits[i] : 0.0f;
+        c[j] = (double)l[j];
+        r[j] = 0.0;
     }
-    __syncthreads();
-    rank_desc(sh.c, n_expert, sh.sorted);
-    decide(sh, n_expert, n_used, 0, red);
-    finish_route(sh, n_expert, n_used, sh.flag != 0, ids, weights, nullptr, red);
+    const bool ok = route_decide(c, r, n_expert, n_used, 0, sh);
+    route_finish(l, n_expert, n_used, !ok, sh, ids, weights, nullptr);
 }
 
 // ---- 3. weighted combine + residual (layer.rs:245-258, 281-287) -------------
@@ -387,11 +527,7 @@ __global__ __launch_bounds__(256) void argmax_partial(const float *x, int n, int
         const float v = xs[i];
         if (!isnan(v)) better(bv, bi, v, i);
     }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = shfl_xor_f(bv, m);
-        const int oi = shfl_xor_i(bi, m);
-        better(bv, bi, ov, oi);
-    }
+    wave_argmax(bv, bi, -INFINITY);
     __shared__ float sv[4];
     __shared__ int si[4];
     if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
@@ -411,11 +547,7 @@ __global__ __launch_bounds__(64) void argmax_final(const float *x, int ld, const
     int bi = 0x7FFFFFFF;
     for (int i = lane; i < nparts; i += 64)
         better(bv, bi, pv[(size_t)seq * nparts + i], pi[(size_t)seq * nparts + i]);
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = shfl_xor_f(bv, m);
-        const int oi = shfl_xor_i(bi, m);
-        better(bv, bi, ov, oi);
-    }
+    wave_argmax(bv, bi, -INFINITY);
     if (lane == 0) {
         // the reference's incumbent is index 0: a NaN there is never beaten,
         // and when nothing beats -inf the answer stays 0
@@ -505,13 +637,14 @@ int launch_router(const RouterLaunch &l, hipStream_t st) {
     a.xq = l.xq; a.xd = l.xd; a.xblocks = l.xblocks;
     const int nr = (l.n_expert + 3) / 4, nq = (l.xblocks + 3) / 4;
     hipLaunchKernelGGL(router_fast, dim3(nr + nq), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(router_exact, dim3(l.n_expert), dim3(64), 0, st, a);
+    // exact mode: the reference's fold on every row, one workgroup per row
+    if (l.force_exact) hipLaunchKernelGGL(router_exact, dim3(l.n_expert), dim3(64), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
                         float *weights, hipStream_t st) {
-    hipLaunchKernelGGL(route_logits, dim3(1), dim3(256), 0, st, logits, n_expert, n_used, ids,
+    hipLaunchKernelGGL(route_logits, dim3(1), dim3(64), 0, st, logits, n_expert, n_used, ids,
                        weights);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -28,7 +28,9 @@
 // block; the 16x redundancy of the masked MFMA costs nothing because the
 // matrix cores are >50x faster than HBM can feed this op.
 #include "common.hpp"
+#include "expf_ref.h"
 #include "launch.hpp"
+#include "q8k_wave.hpp"
 
 namespace llamd {
 namespace {
@@ -48,15 +50,8 @@ struct MvParams {
     int slots_a;              // (gate and up of the same experts in one launch)
 };
 
-__device__ __forceinline__ long make_amask(const uint32_t g[4], int c, int n, bool valid) {
-    const uint32_t lo = (g[c >> 2] >> (8 * (c & 3))) & 0xFFu;
-    const uint32_t hi = (g[2 + (c >> 2)] >> (8 * (c & 3))) & 0xFFu;
-    const uint32_t placed = (lo | (hi << 8)) << (16 * (n & 1));
-    const uint32_t a0 = (valid && !(n & 2)) ? placed : 0u;
-    const uint32_t a1 = (valid && (n & 2)) ? placed : 0u;
-    return (long)((uint64_t)a0 | ((uint64_t)a1 << 32));
-}
-
+// 6-bit codes of class c for this lane's 8 weights (B operand, K = 8s..8s+7)
+// from the nibble words and high-bit words of the tiled layout.
 __device__ __forceinline__ long unpack_codes(const uint32_t nib[8], const uint32_t hb[4], int c) {
     const uint32_t N = nib[c];
     const uint32_t H = hb[c >> 1];
@@ -71,10 +66,12 @@ __device__ __forceinline__ long unpack_codes(const uint32_t nib[8], const uint32
     return (long)((uint64_t)b0 | ((uint64_t)b1 << 32));
 }
 
-// v_perm_b32 selectors that build the A-mask dwords (see make_amask) with one
-// permute each: for class c the pair (a[16j + c], a[16j + c + 8]) sits in
-// byte (c & 3) of g[c >> 2] and of g[2 + (c >> 2)]; selector byte values
-// 0..3 pick from the second operand, 4..7 from the first, 0x0C gives zero.
+// The A operand (activation mask) of lane L = n + 16 s for class c holds, if
+// s == n / 4 (the lane carries group j = n), the pair (a[16j + c],
+// a[16j + c + 8]) in bytes 2 (j % 4) and 2 (j % 4) + 1 of its 8 bytes, and
+// zeros otherwise. v_perm_b32 builds each dword in one instruction: the pair
+// sits in byte (c & 3) of g[c >> 2] and of g[2 + (c >> 2)]; selector byte
+// values 0..3 pick from the second operand, 4..7 from the first, 0x0C gives 0.
 struct MaskSel {
     uint32_t s0, s1;   // selectors for A dword 0 / dword 1 with c & 3 == 0
     uint32_t inc0, inc1;  // added (c & 3) times for the other classes
@@ -269,6 +266,74 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) tot = tot + cls[c];
             p.y[(size_t)slot * p.rows + row] = tot;
+        }
+    }
+}
+
+// Down projection and expert combine in one workgroup per 16-row tile: wave e
+// computes the tile for routed expert ids[e] on activation e (all of its
+// blocks, next block's loads in flight), then wave 0 adds the experts in
+// routing order, out = res + (((0 + w0*y0) + w1*y1) + ...) (layer.rs:245-258,
+// 281-287). No cross-workgroup traffic: the combine reads LDS.
+struct DownParams {
+    const uint8_t *w;
+    size_t expert_stride;
+    const int32_t *ids;
+    const int8_t *aq;     // [n_slots][blocks*256]
+    const float *ad;      // [n_slots][blocks]
+    const float *weights; // [n_slots] routing weights
+    const float *res;     // [rows] or nullptr
+    float *out;           // [rows]
+    int rows, tiles, blocks, n_slots;
+};
+
+__global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
+    __shared__ float ys[16][TILE_ROWS];
+    const int lane = threadIdx.x & 63;
+    const int e = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    const int n = lane & 15, s = lane >> 4;
+    const MaskSel msel = mask_selectors(n, (n >> 2) == s);
+    const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
+    const int8_t *aq = p.aq + (size_t)e * p.blocks * QK_K;
+    const float *ad = p.ad + (size_t)e * p.blocks;
+    float se = 0.0f, so = 0.0f;
+    BlockRegs ra, rb;
+    load_block(ra, seg0, aq, ad, 0, lane, n);
+    for (int b = 0; b < p.blocks; b += 2) {
+        if (b + 1 < p.blocks) load_block(rb, seg0 + (size_t)(b + 1) * SEG_BYTES, aq, ad, b + 1, lane, n);
+        float te, to;
+        block_terms(ra, msel, te, to);
+        se = se + te;
+        so = so + to;
+        if (b + 1 >= p.blocks) break;
+        if (b + 2 < p.blocks) load_block(ra, seg0 + (size_t)(b + 2) * SEG_BYTES, aq, ad, b + 2, lane, n);
+        block_terms(rb, msel, te, to);
+        se = se + te;
+        so = so + to;
+    }
+    float cls[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
+        cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
+    }
+    if (s == 0) {
+        float tot = -0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) tot = tot + cls[c];
+        ys[e][n] = tot;
+    }
+    __syncthreads();
+    if (e == 0 && lane < TILE_ROWS) {
+        const int row = t * TILE_ROWS + lane;
+        if (row < p.rows) {
+            float acc = 0.0f;
+            for (int q = 0; q < p.n_slots; ++q) {
+                const float prod = p.weights[q] * ys[q][lane];
+                acc = acc + prod;
+            }
+            p.out[row] = p.res ? p.res[row] + acc : acc;
         }
     }
 }
@@ -476,15 +541,13 @@ int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, co
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
     }
-    if (blocks > 16 && items < 2048) {
-        // LDS holds up to 16 block terms per item; longer rows use one wave
-        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
-    } else if (items >= 4096) {
-        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
-    } else if (items >= 1024) {
-        hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + 1) / 2), dim3(256), 0, st, p);
-    } else {
+    // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four waves per
+    // tile, each on a quarter of the row, beat one wave per tile at every
+    // size -- more loads in flight per tile and shorter per-wave chains.
+    if (blocks <= 16) {
         hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
+    } else {
+        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -516,6 +579,28 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     const long items = (long)p.tiles * max_subtiles;
     if (items <= 0) return 0;
     hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
+                            const int8_t *aq, const float *ad, const float *weights,
+                            const float *res, float *out, int rows, int blocks, int n_slots,
+                            hipStream_t st) {
+    if (n_slots <= 0 || n_slots > 16) return -1;
+    DownParams p;
+    p.w = (const uint8_t *)w;
+    p.expert_stride = expert_stride;
+    p.ids = ids;
+    p.aq = aq;
+    p.ad = ad;
+    p.weights = weights;
+    p.res = res;
+    p.out = out;
+    p.rows = rows;
+    p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    p.blocks = blocks;
+    p.n_slots = n_slots;
+    hipLaunchKernelGGL(q6k_down_combine, dim3(p.tiles), dim3(64 * n_slots), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

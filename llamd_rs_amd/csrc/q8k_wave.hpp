@@ -20,13 +20,13 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
         const float a = fabsf(v[i]);
         if (a > amax) { amax = a; mx = v[i]; idx = 4 * lane + i; }
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float oa = shfl_xor_f(amax, m);
-        const float om = shfl_xor_f(mx, m);
-        const int oi = shfl_xor_i(idx, m);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-    }
+    // (|x|, index) arg-max over the wave; the sign comes from the winning lane
+    int win = idx;
+    float best = amax;
+    wave_argmax(best, win, -1.0f);
+    amax = best;
+    mx = win == 0x7FFFFFFF ? 0.0f
+                           : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), win >> 2));
     int q[4];
     float dv;
     if (amax == 0.0f) {
@@ -52,8 +52,8 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
         }
     }
     int gs = q[0] + q[1] + q[2] + q[3];
-    gs += shfl_xor_i(gs, 1);
-    gs += shfl_xor_i(gs, 2);
+    gs += dpp<DPP_XOR1>(0, gs);
+    gs += dpp<DPP_XOR2>(0, gs);
     if (bsums && (lane & 3) == 0) bsums[lane >> 2] = (int16_t)gs;
     if (lane == 0) *d = dv;
 }
