@@ -286,23 +286,18 @@ def bench_extra(L, rocm, synth, K, W, p):
     X = rocm.DeviceBuffer.from_array(synth.normal(600, 1.0, nx * n_embd))
     R = rocm.DeviceBuffer.from_array(synth.normal(601, 1.0, nx * n_embd))
     O_ = rocm.DeviceBuffer(n_embd * 4)
-    for mode, flag in (("fast", 0), ("exact", 1)):
-        def f(i, flag=flag):
-            xo = X.ptr + (i % nx) * n_embd * 4
-            ro = R.ptr + (i % nx) * n_embd * 4
-            if L.llamd_hip_moe_forward(layers[i % 4].handle, xo, ro, O_.ptr, flag):
-                raise RuntimeError("moe")
-        steps = max(20, K // 2)
-        ms = time_region(L, f, steps, 5)
-        by = n_expert * n_embd * 4 + 24 * q6k_bytes(n_ff, n_embd) + 3 * n_embd * 4
-        out[f"moe_layer_{mode}"] = {"us_per_token": ms / steps * 1e3, "tok_s": steps / (ms * 1e-3),
-                                    "bytes_per_token": by, "gbs": by / (ms / steps * 1e-3) / 1e9}
-        log(f"  moe {mode}: {out[f'moe_layer_{mode}']}")
-    calls, exact_calls = 0, 0
-    for ly in layers:
-        c, e = ly.stats()
-        calls += c; exact_calls += e
-    out["moe_router_exact_fold_calls"] = {"calls": calls, "exact_calls": exact_calls}
+    def f(i):
+        xo = X.ptr + (i % nx) * n_embd * 4
+        ro = R.ptr + (i % nx) * n_embd * 4
+        if L.llamd_hip_moe_forward(layers[i % 4].handle, xo, ro, O_.ptr, 0):
+            raise RuntimeError("moe")
+    steps = max(20, K // 2)
+    ms = time_region(L, f, steps, 5)
+    by = n_expert * n_embd * 4 + 24 * q6k_bytes(n_ff, n_embd) + 3 * n_embd * 4
+    out["moe_layer"] = {"us_per_token": ms / steps * 1e3, "tok_s": steps / (ms * 1e-3),
+                        "bytes_per_token": by, "gbs": by / (ms / steps * 1e-3) / 1e9,
+                        "routing": "bit-exact (sequential router fold every call)"}
+    log(f"  moe layer: {out['moe_layer']}")
 
     # prefill grouped GEMM, configs[3]: 512 tokens, Zipf 1.1
     n_tok = 512

@@ -20,9 +20,10 @@
  * 256 per block), d (f32 per block), bsums (int16, 16 per block).
  *
  * Results: every Q6_K matvec output, Q8_K quantization, dequantization,
- * expert id and argmax id is bit-identical to the reference CPU path
- * (llamd-quant/llamd-models/llamd-runtime); Q8_0/F32 matvecs and, outside
- * exact mode, routing weights are within llamd-core::tolerance::REDUCTION.
+ * expert id, routing weight, MoE decode-layer output and argmax id is
+ * bit-identical to the reference CPU path (llamd-quant/llamd-models/
+ * llamd-runtime); Q8_0/F32 matvecs are within
+ * llamd-core::tolerance::REDUCTION.
  *
  * Threading: all device work is queued on one library-owned stream
  * (llamd_fwd_get_stream). Host-in/host-out calls synchronise that stream and
@@ -163,11 +164,11 @@ void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, 
 void *llamd_hip_moe_create(const float *router, const void *gate, const void *up,
                            const void *down, int n_embd, int n_ff, int n_expert, int n_used);
 void llamd_hip_moe_destroy(void *h);
-/* flags bit 0: exact mode -- always route on the reference's sequential f32
- * router fold (bit-identical weights and layer output). Without it ids are
- * still exact (a rigorous error bound decides when the fold is needed) and
- * weights are within REDUCTION. Device pointers, asynchronous. d_res may be
- * NULL (then out = moe_ffn only). */
+/* router (the reference's sequential f32 fold) -> route -> gate/up -> SwiGLU
+ * -> down -> weighted combine (+ residual), bit-identical to the CPU path on
+ * every call. flags: reserved, pass 0 (bit 0, "exact", is accepted and is
+ * what every call does). Device pointers, asynchronous. d_res may be NULL
+ * (then out = moe_ffn only). */
 int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *d_out, int flags);
 /* Host in/out; ids/weights/logits (optional) receive the routing. */
 int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float *out,
@@ -178,7 +179,8 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
                           float *d_out, int n_tok);
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
                                float *out, int n_tok);
-/* Routing statistics since create: calls, and calls that needed the exact fold. */
+/* Routing statistics since create: calls, and calls routed on the exact
+ * sequential router fold (every call, so the two are equal). */
 int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls);
 
 /* ---- LM head: Q6_K matvec over the vocabulary + argmax -------------------- */

@@ -512,8 +512,7 @@ struct MoeLayer {
     void *gate = nullptr, *upw = nullptr, *downw = nullptr;
     size_t sgu = 0, sd = 0;  // expert strides
     // decode scratch
-    DevBuf xq, xd, logit_f, centre, radius, exact_l, logits_used, ids, weights, stats, flag,
-        counters;
+    DevBuf xq, xd, logits, ids, weights, stats;
     DevBuf g, aq, ad, dn;
     // prefill scratch (grown on demand)
     int cap_tok = 0;
@@ -547,17 +546,14 @@ void *llamd_hip_moe_create(const float *router, const void *gate, const void *up
     if (ok) {
         m->sgu = llamd_hip_q6k_tiled_bytes(n_ff, m->be);
         m->sd = llamd_hip_q6k_tiled_bytes(n_embd, m->bf);
-        ok = m->xq.alloc(n_embd) && m->xd.alloc(m->be * 4) && m->logit_f.alloc(n_expert * 4) &&
-             m->centre.alloc(n_expert * 8) && m->radius.alloc(n_expert * 8) &&
-             m->exact_l.alloc(n_expert * 4) && m->flag.alloc(16) && m->counters.alloc(16) &&
-             m->logits_used.alloc(n_expert * 4) && m->ids.alloc(n_used * 4) &&
+        ok = m->xq.alloc(n_embd) && m->xd.alloc(m->be * 4) &&
+             m->logits.alloc(n_expert * 4) && m->ids.alloc(n_used * 4) &&
              m->weights.alloc(n_used * 4) && m->stats.alloc(16) &&
              m->g.alloc((size_t)2 * n_used * n_ff * 4) &&
              m->aq.alloc((size_t)n_used * n_ff) && m->ad.alloc((size_t)n_used * m->bf * 4) &&
              m->dn.alloc((size_t)n_used * n_embd * 4);
         int zero[4] = {0, 0, 0, 0};
-        ok = ok && up(m->stats.p, zero, sizeof zero) && up(m->counters.p, zero, sizeof zero) &&
-             up(m->flag.p, zero, sizeof zero) && sync();
+        ok = ok && up(m->stats.p, zero, sizeof zero) && sync();
     }
     if (!ok) {
         llamd_hip_moe_destroy(m);
@@ -578,39 +574,35 @@ void llamd_hip_moe_destroy(void *h) {
 }
 
 int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *d_out, int flags) {
+    // every call is bit-exact; flags (bit 0 once asked for that) is accepted
+    // and has no effect
+    (void)flags;
     MoeLayer *m = (MoeLayer *)h;
     if (!m || !d_x || !d_out) return fail("moe_forward: null argument");
     hipStream_t st = stream();
     int rc = 0;
+    // 1. the reference's router logits + Q8_K of x
     RouterLaunch rl;
     rl.w = m->router.as<float>();
     rl.x = d_x;
     rl.n_expert = m->n_expert;
     rl.k = m->n_embd;
-    rl.n_used = m->n_used;
-    rl.force_exact = flags & 1;
-    rl.logit_f = m->logit_f.as<float>();
-    rl.centre = m->centre.as<double>();
-    rl.radius = m->radius.as<double>();
-    rl.exact_l = m->exact_l.as<float>();
-    rl.ids = m->ids.as<int32_t>();
-    rl.weights = m->weights.as<float>();
-    rl.logits_used = m->logits_used.as<float>();
-    rl.flag = m->flag.as<int>();
-    rl.counters = m->counters.as<int>();
-    rl.stats = m->stats.as<int>();
+    rl.logits = m->logits.as<float>();
     rl.xq = m->xq.as<int8_t>();
     rl.xd = m->xd.as<float>();
     rl.xblocks = m->be;
     rc |= launch_router(rl, st);
-    // gate and up in one launch: g holds [gate | up] x n_used x n_ff
-    rc |= launch_q6k_mv_b1(m->gate, m->sgu, m->ids.as<int32_t>(), m->xq.as<int8_t>(),
-                           m->xd.as<float>(), m->g.as<float>(), m->n_ff, m->be, m->n_used, 0, st,
-                           m->upw);
+    // 2. route (prologue) + gate and up of the routed experts in one launch:
+    //    g holds [gate | up] x n_used x n_ff
+    rc |= launch_q6k_mv_routed(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
+                               m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
+                               m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
+                               m->g.as<float>(), m->n_ff, m->be, st);
+    // 3. SwiGLU + Q8_K of the activations
     rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
                             nullptr, m->aq.as<int8_t>(), nullptr, m->ad.as<float>(), nullptr,
                             m->n_used * m->bf, st);
-    // down projection of the routed experts + weighted combine + residual
+    // 4. down projection of the routed experts + weighted combine + residual
     rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
                                   m->ad.as<float>(), m->weights.as<float>(), d_res, d_out,
                                   m->n_embd, m->bf, m->n_used, st);
@@ -633,7 +625,7 @@ int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float 
     if (!down(out, dout.p, nb)) return -1;
     if (ids && !down(ids, m->ids.p, (size_t)m->n_used * 4)) return -1;
     if (weights && !down(weights, m->weights.p, (size_t)m->n_used * 4)) return -1;
-    if (logits && !down(logits, m->logits_used.p, (size_t)m->n_expert * 4)) return -1;
+    if (logits && !down(logits, m->logits.p, (size_t)m->n_expert * 4)) return -1;
     return sync() ? 0 : -1;
 }
 

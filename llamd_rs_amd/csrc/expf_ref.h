@@ -83,13 +83,14 @@ EXPF_REF_FN float expf_ref_asfloat(uint32_t u) { float f; memcpy(&f, &u, 4); ret
 #define EXPF_REF_MADD(a, b, c) EXPF_REF_ADD(EXPF_REF_MUL(a, b), (c))
 #endif
 
-EXPF_REF_FN float expf_ref(float x) {
+// The core with the table passed in: device code keeps a copy in LDS so the
+// lookup is not a dependent global-memory load.
+EXPF_REF_FN float expf_ref_tab(float x, const uint64_t *tab) {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    const uint64_t tab[32] = EXPF_REF_TAB;
 
     const uint32_t ux = expf_ref_asuint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -117,5 +118,23 @@ EXPF_REF_FN float expf_ref(float x) {
     y = EXPF_REF_MUL(y, s);
     return (float)y;
 }
+
+EXPF_REF_FN float expf_ref(float x) {
+    const uint64_t tab[32] = EXPF_REF_TAB;
+    return expf_ref_tab(x, tab);
+}
+
+#if defined(__HIPCC__)
+static __constant__ uint64_t k_expf_ref_tab[32] = EXPF_REF_TAB;
+
+// Copy the table into LDS (32 x 8 B) with this wave; every wave that reads it
+// calls this first (the writes of several waves carry identical values).
+__device__ static inline void expf_ref_tab_fill(uint64_t *lds_tab) {
+    const int lane = threadIdx.x & 63;
+    if (lane < 32) lds_tab[lane] = k_expf_ref_tab[lane];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+#endif
 
 #endif

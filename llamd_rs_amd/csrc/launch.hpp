@@ -11,6 +11,8 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
+extern int g_tune_router;
+extern int g_tune_down_fused;  // 1: SwiGLU in the down kernel's prologue  // router kernel arrangement (see launch_router)
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4
 
 // q6k_mv.hip
@@ -21,6 +23,12 @@ int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, co
                      hipStream_t st, const void *w_b = nullptr);
 // Down projection of n_slots routed experts (activation e for slot e) and the
 // routing-weighted combine (+ residual) into out, one workgroup per 16 rows.
+// Gate and up of the routed experts in one launch, routing (softmax, top-k,
+// renormalise) in the prologue on exact logits; y = [gate | up][n_used][rows].
+int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
+                        const float *logits, int n_expert, int n_used, int32_t *ids_out,
+                        float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
+                        int rows, int blocks, hipStream_t st);
 int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
                             const int8_t *aq, const float *ad, const float *weights,
                             const float *res, float *out, int rows, int blocks, int n_slots,
@@ -51,15 +59,12 @@ int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipSt
 // moe.hip
 // Router + route for one token (moe.hip): router_fast then router_exact
 // (the latter exits at once unless the fast pass could not prove the order).
+// The reference's router logits (sequential f32 fold per expert) and, in the
+// same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.
 struct RouterLaunch {
     const float *w, *x;
-    int n_expert, k, n_used, force_exact;
-    float *logit_f;
-    double *centre, *radius;
-    float *exact_l;
-    int32_t *ids;
-    float *weights, *logits_used;
-    int *flag, *counters, *stats;
+    int n_expert, k;
+    float *logits;
     int8_t *xq;
     float *xd;
     int xblocks;

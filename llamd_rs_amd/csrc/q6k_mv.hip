@@ -31,6 +31,7 @@
 #include "expf_ref.h"
 #include "launch.hpp"
 #include "q8k_wave.hpp"
+#include "route.hpp"
 
 namespace llamd {
 namespace {
@@ -48,6 +49,14 @@ struct MvParams {
     int act_per_slot;         // 1: slot i uses activation i; 0: all use activation 0
     const uint8_t *w_b;       // slots >= slots_a read this weight (ids[slot - slots_a])
     int slots_a;              // (gate and up of the same experts in one launch)
+    // routing prologue (ROUTE): every wave routes on the exact router logits
+    // and takes slot -> expert from its own selection; workgroup 0 publishes
+    // ids / weights for the kernels after it
+    const float *route_l;     // [n_expert]
+    int n_expert, n_used;
+    int32_t *ids_out;
+    float *w_out;
+    int *stats;               // [2] calls (+1 each, both counters)
 };
 
 // 6-bit codes of class c for this lane's 8 weights (B operand, K = 8s..8s+7)
@@ -194,7 +203,7 @@ __device__ __forceinline__ void consume_terms(int b, float te, float to, float &
 // meet in LDS and are folded in block order -- the same additions in the same
 // order as a single wave walking every block, so splitting K changes the
 // latency, never the bits.
-template <int KS>
+template <int KS, bool ROUTE = false>
 __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
     constexpr int IPW = 4 / KS;                 // items per workgroup
     constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
@@ -213,7 +222,30 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
 
     const bool second = slot >= p.slots_a;
     const int eslot = second ? slot - p.slots_a : slot;
-    const int expert = (live && p.ids) ? p.ids[eslot] : 0;
+    int expert;
+    if constexpr (ROUTE) {
+        // wave 0 routes; the workgroup's other waves wait for its choice
+        __shared__ RouteLds rsh;
+        if (wave == 0) {
+            float l[RW];
+#pragma unroll
+            for (int j = 0; j < RW; ++j) {
+                const int i = lane + WAVE * j;
+                l[j] = i < p.n_expert ? p.route_l[i] : 0.0f;
+            }
+            const bool writer = blockIdx.x == 0;
+            route_finish(l, p.n_expert, p.n_used, true, rsh, writer ? p.ids_out : nullptr,
+                         writer ? p.w_out : nullptr, nullptr);
+            if (writer && lane == 0 && p.stats) {
+                p.stats[0] += 1;
+                p.stats[1] += 1;
+            }
+        }
+        __syncthreads();
+        expert = live ? rsh.sorted[eslot] : 0;
+    } else {
+        expert = (live && p.ids) ? p.ids[eslot] : 0;
+    }
     const int act = p.act_per_slot ? slot : 0;
     const int8_t *aq = p.aq + (size_t)act * p.blocks * QK_K;
     const float *ad = p.ad + (size_t)act * p.blocks;
@@ -549,6 +581,35 @@ int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, co
     } else {
         hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
+                        const float *logits, int n_expert, int n_used, int32_t *ids_out,
+                        float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
+                        int rows, int blocks, hipStream_t st) {
+    if (blocks > 16 || n_expert > ROUTE_MAX_EXPERTS || n_used > ROUTE_MAX_USED) return -1;
+    MvParams p;
+    p.w = (const uint8_t *)w;
+    p.w_b = (const uint8_t *)w_b;
+    p.slots_a = n_used;
+    p.expert_stride = expert_stride;
+    p.ids = nullptr;
+    p.aq = aq;
+    p.ad = ad;
+    p.y = y;
+    p.rows = rows;
+    p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    p.blocks = blocks;
+    p.n_slots = 2 * n_used;
+    p.act_per_slot = 0;
+    p.route_l = logits;
+    p.n_expert = n_expert;
+    p.n_used = n_used;
+    p.ids_out = ids_out;
+    p.w_out = w_out;
+    p.stats = stats;
+    hipLaunchKernelGGL((q6k_mv_b1<4, true>), dim3(p.tiles * p.n_slots), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -33,23 +33,24 @@ __global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, 
                   bsums ? bsums + (size_t)blk * 16 : nullptr);
 }
 
-__device__ __forceinline__ float silu_ref(float v) { return v / (1.0f + expf_ref(-v)); }
 
 // act[i] = silu(gate[i]) * up[i], then Q8_K of act. Optionally stores act.
 __global__ __launch_bounds__(256) void swiglu_q8k(const float *gate, const float *up, float *act_out,
                                                   int8_t *qs, int8_t *qs_cm, float *d,
                                                   int16_t *bsums, int nblocks) {
+    __shared__ uint64_t tab[32];
     const int lane = threadIdx.x & 63;
     const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const size_t o = (size_t)blk * QK_K + 4 * lane;
     const float4 gv = *(const float4 *)(gate + o);
     const float4 uv = *(const float4 *)(up + o);
+    expf_ref_tab_fill(tab);
     float v[4];
-    v[0] = silu_ref(gv.x) * uv.x;
-    v[1] = silu_ref(gv.y) * uv.y;
-    v[2] = silu_ref(gv.z) * uv.z;
-    v[3] = silu_ref(gv.w) * uv.w;
+    v[0] = silu_ref(gv.x, tab) * uv.x;
+    v[1] = silu_ref(gv.y, tab) * uv.y;
+    v[2] = silu_ref(gv.z, tab) * uv.z;
+    v[3] = silu_ref(gv.w, tab) * uv.w;
     if (act_out) *(float4 *)(act_out + o) = make_float4(v[0], v[1], v[2], v[3]);
     quantize_wave(v, lane, qs ? qs + (size_t)blk * QK_K : nullptr,
                   qs_cm ? qs_cm + (size_t)blk * QK_K : nullptr, d + blk,
@@ -57,8 +58,10 @@ __global__ __launch_bounds__(256) void swiglu_q8k(const float *gate, const float
 }
 
 __global__ void silu_mul_f32(const float *gate, const float *up, float *out, int n) {
+    __shared__ uint64_t tab[32];
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = silu_ref(gate[i]) * up[i];
+    expf_ref_tab_fill(tab);
+    if (i < n) out[i] = silu_ref(gate[i], tab) * up[i];
 }
 
 }  // namespace

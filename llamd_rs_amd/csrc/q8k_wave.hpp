@@ -5,6 +5,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "expf_ref.h"
 
 namespace llamd {
 
@@ -58,6 +59,11 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
     if (lane == 0) *d = dv;
 }
 
+
+// silu(v) = v / (1 + exp(-v)) with the reference's f32 expf (model.rs silu).
+__device__ __forceinline__ float silu_ref(float v, const uint64_t *tab) {
+    return v / (1.0f + expf_ref_tab(-v, tab));
+}
 
 __device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, int8_t *qs, float *d) {
     quantize_wave(v, lane, qs, nullptr, d, nullptr);

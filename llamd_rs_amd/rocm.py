@@ -333,8 +333,9 @@ class MoeLayer:
     def handle(self):
         return self._h
 
-    def forward(self, x, res=None, exact: bool = False):
-        """Returns (out, Routing, logits_used). out = res + moe_ffn(x) (res optional)."""
+    def forward(self, x, res=None, exact: bool = True):
+        """Returns (out, Routing, logits). out = res + moe_ffn(x) (res optional).
+        Every call is bit-exact; `exact` is accepted for older callers."""
         x = _f32(x)
         if x.size != self.n_embd:
             raise ValueError("x must be [n_embd]")

@@ -1,7 +1,6 @@
 """Routing, the MoE decode layer, prefill grouping and the LM head on the
-MI355X against the CPU oracle. Expert ids and argmax ids: EXACT. Layer
-outputs: EXACT in exact-router mode, within REDUCTION * max(rms, 1) in the
-default mode (routing weights from the parallel router sum)."""
+MI355X against the CPU oracle. Router logits, expert ids, routing weights,
+decode-layer outputs and argmax ids: EXACT (bit-identical)."""
 import numpy as np
 import pytest
 
@@ -81,34 +80,34 @@ def qwen_layer(gpu):
     layer.close()
 
 
-def test_moe_layer_ids_exact_and_output_close(gpu, qwen_layer):
+def test_moe_layer_bit_identical(gpu, qwen_layer):
+    """configs[2] decode layer: logits, expert ids, routing weights and the
+    layer output all equal the CPU path's bits on every call."""
     from llamd_rs_amd import synth
     layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
-    for t in range(6):
+    calls0, _ = layer.stats()
+    for t in range(8):
         x = synth.normal(1000 + t, 1.0, n_embd)
         res = synth.normal(2000 + t, 1.0, n_embd)
         want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
         out, r, lg_used = layer.forward(x, res)
+        assert bits_equal(lg_used, lg), t
         assert list(r.experts) == list(ids), t
-        assert np.max(np.abs(r.weights - w)) <= O.REDUCTION
-        bound = O.REDUCTION * max(H.rms(want), 1.0)
-        assert np.max(np.abs(out - want)) <= bound, t
-
-
-def test_moe_layer_exact_mode_is_bit_identical(gpu, qwen_layer):
-    from llamd_rs_amd import synth
-    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
-    for t in range(3):
-        x = synth.normal(3000 + t, 1.0, n_embd)
-        res = synth.normal(4000 + t, 1.0, n_embd)
-        want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
-        out, r, lg_used = layer.forward(x, res, exact=True)
-        assert bits_equal(lg_used, lg)
-        assert list(r.experts) == list(ids)
-        assert bits_equal(r.weights, w)
+        assert bits_equal(r.weights, w), t
         assert bits_equal(out, want), t
     calls, exact_calls = layer.stats()
-    assert exact_calls >= 3
+    assert calls - calls0 == 8 and exact_calls == calls
+
+
+def test_moe_layer_without_residual(gpu, qwen_layer):
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    x = synth.normal(3000, 1.0, n_embd)
+    zero = np.zeros(n_embd, np.float32)
+    want, lg, ids, w = O.moe_layer(x, zero, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+    out, r, _ = layer.forward(x, None)
+    # res = 0 adds +0.0 to each sum: the same bits except that -0.0 becomes +0.0
+    assert np.array_equal(out, want)
 
 
 def test_moe_layer_near_tied_router_stays_exact(gpu):
@@ -127,8 +126,10 @@ def test_moe_layer_near_tied_router_stays_exact(gpu):
         x = x * np.sign(router[5] @ x)      # make the tied group win
         want, lg, ids, w = O.moe_layer(x, np.zeros(n_embd, np.float32), n_embd, n_ff, n_expert,
                                        n_used, router, gate, up, down)
-        out, r, _ = layer.forward(x)
+        out, r, _ = layer.forward(x, np.zeros(n_embd, np.float32))
         assert list(r.experts) == list(ids), (t, r.experts, ids)
+        assert bits_equal(r.weights, w), t
+        assert bits_equal(out, want), t
     layer.close()
 
 
