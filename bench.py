@@ -36,6 +36,12 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_INT8_TOPS = 5000.0        # dense int8 MFMA
 QK_K = 256
 GIB = 1 << 30
+# HBM bytes per q6k_mv_b1 launch of configs[1] (mean of the step's three
+# launches), from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script
+# scaled by the same counters on a copy of known size (x2.0 fetch, x1.0
+# write); the commands and per-kernel values are in
+# profiles/q6k_mv_b1.configs1.hbm_traffic.txt. Algorithmic: 1,301,504 B.
+TRAFFIC_Q6K_MV_CONFIGS1 = 1396470
 
 
 def log(*a):
@@ -84,19 +90,6 @@ def time_region(L, fn, steps, warmup):
     sync(L)
     t.close()
     return ms
-
-
-def per_launch_ms(L, fn, n):
-    """Average duration of single launches, each bracketed by its own events."""
-    t = Timer(L, 2 * n)
-    for i in range(n):
-        t.rec(2 * i)
-        fn(i)
-        t.rec(2 * i + 1)
-    sync(L)
-    ds = [t.ms(2 * i, 2 * i + 1) for i in range(n)]
-    t.close()
-    return float(np.mean(ds)), float(np.median(ds))
 
 
 def main():
@@ -162,33 +155,34 @@ def main():
     shape_res = {}
     for name, rows, k, _ in shapes:
         msn = time_region(L, lambda i, n=name, r=rows, kk=k: launch(n, r, kk, i), K, W)
-        avg, med = per_launch_ms(L, lambda i, n=name, r=rows, kk=k: launch(n, r, kk, i), min(K, 200))
         shape_res[name] = {
             "rows": rows, "k": k, "bytes": per_shape_bytes[name],
             "us_back_to_back": msn / K * 1e3,
             "gbs_back_to_back": per_shape_bytes[name] * K / (msn * 1e-3) / 1e9,
-            "us_per_launch_events": avg * 1e3, "us_per_launch_median": med * 1e3,
-            "gbs_kernel": per_shape_bytes[name] / (avg * 1e-3) / 1e9,
         }
         log(f"  {name}: {shape_res[name]}")
-    # dominant kernel for the roofline: q6k_mv_b1 over the three shapes
-    avg_all = np.mean([shape_res[n]["us_per_launch_events"] for n in shape_res])
+    # dominant kernel for the roofline: q6k_mv_b1, the three launches of the
+    # timed step; its average launch duration is the HIP-event time of the
+    # timed region over the launches in it (rocprof's kernel average agrees)
+    launches = 3 * K
+    avg_us = ms * 1e3 / launches
     bytes_launch = bytes_step / 3
-    achieved = bytes_launch / (avg_all * 1e-6) / 1e9
+    achieved = bytes_launch / (avg_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_Q6K_MV_CONFIGS1,
                 "kernel": "q6k_mv_b1", "bytes_per_launch": bytes_launch,
-                "avg_launch_us": round(float(avg_all), 3)}
+                "avg_launch_us": round(avg_us, 3),
+                "traffic_source": "profiles/q6k_mv_b1.configs1.hbm_traffic.txt"}
     for lst in copies.values():
         for c in lst:
             c.close()
     copies = None
 
-    extra = {"configs1_per_shape": shape_res}
+    extra = {"configs1_per_shape": shape_res, "copy_calibration": bench_copy(L, rocm)}
 
     # ---- extra configs ---------------------------------------------------------
     if not args.quick:
-        extra.update(bench_extra(L, rocm, synth, K, W, p))
+        extra.update(bench_extra(L, rocm, synth, K, W, p, 0.0 if args.no_cpu else 6.0))
 
     # ---- CPU baseline --------------------------------------------------------------
     cpu = None
@@ -219,7 +213,23 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_extra(L, rocm, synth, K, W, p):
+def bench_copy(L, rocm, mib=512, reps=5):
+    """A plain device copy of known size: the achievable-bandwidth reference
+    and the calibration kernel for the profiler's FETCH_SIZE / WRITE_SIZE."""
+    n = mib << 20
+    a, b = rocm.DeviceBuffer(n), rocm.DeviceBuffer(n)
+    def f(i):
+        if L.llamd_hip_copy_calibration(b.ptr, a.ptr, n):
+            raise RuntimeError("copy")
+    ms = time_region(L, f, reps, 1)
+    a.close(); b.close()
+    res = {"bytes_read": n, "bytes_written": n, "us": ms / reps * 1e3,
+           "gbs_read_plus_write": 2 * n / (ms / reps * 1e-3) / 1e9}
+    log(f"  copy calibration: {res}")
+    return res
+
+
+def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     out = {}
     # Q8_0 matvec, configs[0]
     rows, k = 4096, 2048
@@ -232,11 +242,9 @@ def bench_extra(L, rocm, synth, K, W, p):
     def fq(i):
         L.llamd_hip_fwd_matvec_q8_0(ws[i % nc]._ptr, x.ptr, y.ptr, rows, k)
     ms = time_region(L, fq, K, W)
-    avg, med = per_launch_ms(L, fq, min(K, 100))
     by = len(w) + k * 4 + rows * 4
     out["q8_0_matvec"] = {"rows": rows, "k": k, "bytes": by, "us_back_to_back": ms / K * 1e3,
-                          "gbs_back_to_back": by * K / (ms * 1e-3) / 1e9,
-                          "us_per_launch_events": avg * 1e3, "gbs_kernel": by / (avg * 1e-3) / 1e9}
+                          "gbs_back_to_back": by * K / (ms * 1e-3) / 1e9}
     log(f"  q8_0: {out['q8_0_matvec']}")
     for q in ws:
         q.close()
@@ -262,12 +270,24 @@ def bench_extra(L, rocm, synth, K, W, p):
         steps = max(10, K // 4)
         ms = time_region(L, f, steps, 3)
         by = q6k_bytes(rows, k) + nseq * k * 4 + nseq * rows * 4
-        avg, med = per_launch_ms(L, f, 20)
         out[f"lm_head_b{nseq}"] = {"us_per_call": ms / steps * 1e3, "bytes": by,
                                    "gbs": by / (ms / steps * 1e-3) / 1e9,
                                    "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
-                                   "us_per_call_events": avg * 1e3}
+                                   "call": "Q8_K quantize + Q6_K matvec + argmax"}
         log(f"  lm_head b{nseq}: {out[f'lm_head_b{nseq}']}")
+    # the LM-head matvec kernel alone (activation already quantized)
+    a1 = rocm.quantize_q8k_on_device(synth.normal(31, 1.0, k))
+    q1, d1 = rocm.DeviceBuffer.from_array(a1.qs), rocm.DeviceBuffer.from_array(a1.d)
+    def fm(i):
+        L.llamd_fwd_matvec(heads[i % 4][0].ptr, q1.ptr, d1.ptr, logits.ptr, k // QK_K, rows)
+    steps = max(10, K // 4)
+    ms = time_region(L, fm, steps, 3)
+    by = q6k_bytes(rows, k) + k + (k // QK_K) * 4 + rows * 4
+    out["lm_head_matvec_b1"] = {"us_per_launch": ms / steps * 1e3, "bytes": by,
+                                "gbs": by / (ms / steps * 1e-3) / 1e9,
+                                "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
+    log(f"  lm_head matvec b1: {out['lm_head_matvec_b1']}")
+    q1.close(); d1.close()
     for dw, h in heads:
         h.close(); dw.close()
     xb.close(); logits.close(); ids.close()
@@ -297,6 +317,18 @@ def bench_extra(L, rocm, synth, K, W, p):
     out["moe_layer"] = {"us_per_token": ms / steps * 1e3, "tok_s": steps / (ms * 1e-3),
                         "bytes_per_token": by, "gbs": by / (ms / steps * 1e-3) / 1e9,
                         "routing": "bit-exact (sequential router fold every call)"}
+    if moe_cpu_seconds > 0:
+        # the reference's CPU layer (the oracle, 1 thread) on a bounded sample
+        from oracle import oracle as O
+        xh, rh = synth.normal(600, 1.0, n_embd), synth.normal(601, 1.0, n_embd)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < moe_cpu_seconds:
+            O.moe_layer(xh, rh, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+            n += 1
+        dt = time.perf_counter() - t0
+        out["moe_layer"]["cpu_tok_s"] = n / dt
+        out["moe_layer"]["cpu_sample"] = f"{n} tokens in {dt:.1f}s, oracle on 1 host thread"
+        out["moe_layer"]["vs_cpu"] = out["moe_layer"]["tok_s"] / (n / dt)
     log(f"  moe layer: {out['moe_layer']}")
 
     # prefill grouped GEMM, configs[3]: 512 tokens, Zipf 1.1

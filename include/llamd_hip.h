@@ -63,6 +63,14 @@ void llamd_rocm_release(void *dev);
 /* llamd_forward.hip:711-745 */
 void *llamd_fwd_get_stream(void);
 int llamd_fwd_stream_init(void);
+/* forward.rs:613-617 / llamd_forward.hip:879-910: capture the library
+ * stream into one graph, replay it, query and drop it. Nothing runs between
+ * begin and end; the first results come from the first replay. */
+int llamd_fwd_begin_capture(void);
+int llamd_fwd_end_capture(void);
+int llamd_fwd_graph_launch(void);
+int llamd_fwd_has_graph(void);
+void llamd_fwd_graph_destroy(void);
 void *llamd_fwd_alloc(size_t bytes);
 void llamd_fwd_free(void *p);
 int llamd_fwd_upload(void *dst, const void *src, size_t bytes);
@@ -137,6 +145,28 @@ void llamd_fwd_matvec_grouped(const void *d_w, const int32_t *d_ids, const int8_
 void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
                                  const float *d_ad, float *d_out, int blocks, int rows,
                                  int n_used);
+/* llamd.hip:1400-1411: Q, K, V (any three Q6_K matrices with the same k)
+ * on one activation in ONE launch. */
+void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
+                         const float *d_ad, float *o0, float *o1, float *o2, int blocks, int rows0,
+                         int rows1, int rows2);
+/* llamd.hip:1413-1424: gate and up of the same experts in ONE launch;
+ * oa, ob: [n_used][rows]. */
+void llamd_fwd_matvec_grouped_x2(const void *wa, const void *wb, const int32_t *d_ids,
+                                 const int8_t *d_aq, const float *d_ad, float *oa, float *ob,
+                                 int blocks, int rows, int n_used);
+/* llamd.hip:1426-1466: the split-K variants. nsub is accepted and ignored:
+ * the library chooses the split of K itself (the results do not depend on
+ * it: every split folds the per-block terms in block order). */
+void llamd_fwd_matvec_x3_splitk(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
+                                const float *d_ad, float *o0, float *o1, float *o2, int blocks,
+                                int rows0, int rows1, int rows2, int nsub);
+void llamd_fwd_matvec_grouped_x2_splitk(const void *wa, const void *wb, const int32_t *d_ids,
+                                        const int8_t *d_aq, const float *d_ad, float *oa,
+                                        float *ob, int blocks, int rows, int n_used, int nsub);
+void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                                        const float *d_ad, float *d_out, int blocks, int rows,
+                                        int n_used, int nsub);
 /* llamd.hip:1607-1611 (d_bsums may be NULL) */
 void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks);
 /* llamd_forward.hip:802-805 (exact SiLU: glibc-identical expf) */
@@ -145,6 +175,9 @@ void llamd_fwd_silu_mul(const float *gate, const float *up, float *out, int n);
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs);
 /* llamd_forward.hip:856-861 */
+/* llamd_forward.hip:813-817: out = sum_e w[e] * down[e] (no residual). */
+void llamd_fwd_moe_combine(const float *d_down, const float *d_weights, float *d_out, int n_used,
+                           int n_embd);
 void llamd_fwd_moe_combine_add(const float *down, const float *weights, const float *residual,
                                float *out, int n_used, int n_embd);
 /* llamd_forward.hip:819-825; scratch_v/scratch_i hold nblocks partials. */
@@ -199,6 +232,10 @@ void *llamd_hip_event_create(void);
 void llamd_hip_event_destroy(void *ev);
 int llamd_hip_event_record(void *ev);
 float llamd_hip_event_elapsed_ms(void *start, void *stop);
+/* Not in the reference: a plain 16-byte-vector device copy of `bytes` (a
+ * multiple of 16) on the library stream, asynchronous. Its known traffic
+ * (bytes read, bytes written) calibrates the profiler's HBM counters. */
+int llamd_hip_copy_calibration(void *d_dst, const void *d_src, size_t bytes);
 /* llamd.hip:1101-1148: one warm launch, then iters launches, total ms. */
 int llamd_rocm_matvec_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,
                             int rows, int iters, float *ms_out);

@@ -40,6 +40,11 @@ SIGNATURES = {
     "llamd_rocm_release": (None, [vp]),
     "llamd_fwd_get_stream": (vp, []),
     "llamd_fwd_stream_init": (i32, []),
+    "llamd_fwd_begin_capture": (i32, []),
+    "llamd_fwd_end_capture": (i32, []),
+    "llamd_fwd_graph_launch": (i32, []),
+    "llamd_fwd_has_graph": (i32, []),
+    "llamd_fwd_graph_destroy": (None, []),
     "llamd_fwd_alloc": (vp, [sz]),
     "llamd_fwd_free": (None, [vp]),
     "llamd_fwd_upload": (i32, [vp, vp, sz]),
@@ -68,6 +73,12 @@ SIGNATURES = {
     "llamd_fwd_matvec": (None, [vp, vp, vp, vp, i32, i32]),
     "llamd_fwd_matvec_grouped": (None, [vp, vp, vp, vp, vp, i32, i32, i32]),
     "llamd_fwd_matvec_grouped_pa": (None, [vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_fwd_matvec_x3": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_fwd_matvec_x3_splitk": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "llamd_fwd_matvec_grouped_x2": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_fwd_matvec_grouped_x2_splitk": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_fwd_matvec_grouped_pa_splitk": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_fwd_moe_combine": (None, [vp, vp, vp, i32, i32]),
     "llamd_fwd_quantize": (None, [vp, vp, vp, i32]),
     "llamd_fwd_silu_mul": (None, [vp, vp, vp, i32]),
     "llamd_fwd_router": (None, [vp, i32, i32, vp, vp, vp]),
@@ -89,6 +100,7 @@ SIGNATURES = {
     "llamd_hip_event_destroy": (None, [vp]),
     "llamd_hip_event_record": (i32, [vp]),
     "llamd_hip_event_elapsed_ms": (f, [vp, vp]),
+    "llamd_hip_copy_calibration": (i32, [vp, vp, sz]),
     "llamd_rocm_matvec_bench": (i32, [vp, vp, vp, i32, i32, i32, f32p]),
     "llamd_rocm_matvec_grouped_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32p]),
     # host-side synthetic data (llamd_rs_amd/csrc/host/synth.cpp)

@@ -173,6 +173,45 @@ void llamd_rocm_release(void *dev) {
     (void)hipFree(dev);
 }
 
+// ---- graph capture of the library stream -----------------------------------
+// One graph at a time. Capture records launches without running them; the
+// first results come from the first replay. Everything the captured calls
+// read must be resident (no host copies inside a capture), and no kernel of
+// this library records a memset node.
+static hipGraph_t g_graph = nullptr;
+static hipGraphExec_t g_exec = nullptr;
+
+static void drop_graph() {
+    if (g_exec) { (void)hipGraphExecDestroy(g_exec); g_exec = nullptr; }
+    if (g_graph) { (void)hipGraphDestroy(g_graph); g_graph = nullptr; }
+}
+
+int llamd_fwd_begin_capture(void) {
+    if (!stream()) return fail("stream create failed");
+    drop_graph();
+    return hip_ok(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal), "begin capture")
+               ? 0 : -1;
+}
+
+int llamd_fwd_end_capture(void) {
+    if (!stream()) return fail("stream create failed");
+    if (!hip_ok(hipStreamEndCapture(stream(), &g_graph), "end capture")) return -1;
+    if (!hip_ok(hipGraphInstantiate(&g_exec, g_graph, nullptr, nullptr, 0), "graph instantiate")) {
+        drop_graph();
+        return -1;
+    }
+    return 0;
+}
+
+int llamd_fwd_graph_launch(void) {
+    if (!g_exec) return fail("graph_launch: no graph");
+    return hip_ok(hipGraphLaunch(g_exec, stream()), "graph launch") ? 0 : -1;
+}
+
+int llamd_fwd_has_graph(void) { return g_exec ? 1 : 0; }
+
+void llamd_fwd_graph_destroy(void) { drop_graph(); }
+
 void *llamd_fwd_get_stream(void) { return (void *)stream(); }
 int llamd_fwd_stream_init(void) { return stream() ? 0 : fail("stream create failed"); }
 
@@ -479,6 +518,62 @@ void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *id
                       float *weights, float *probs) {
     (void)probs;
     launch_route_logits(logits, n_expert, n_used, ids, weights, stream());
+}
+
+void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
+                         const float *d_ad, float *o0, float *o1, float *o2, int blocks, int rows0,
+                         int rows1, int rows2) {
+    const void *w[3] = {w0, w1, w2};
+    float *y[3] = {o0, o1, o2};
+    const int rows[3] = {rows0, rows1, rows2};
+    for (int i = 0; i < 3; ++i) {
+        WInfo wi;
+        if (!lookup(w[i], KIND_Q6K, &wi) || wi.blocks != blocks || rows[i] <= 0 ||
+            rows[i] > wi.rows * wi.n_expert) {
+            fail("matvec_x3: weight %d is not a Q6_K handle of that shape", i);
+            return;
+        }
+    }
+    launch_q6k_mv_x3(w, y, rows, 3, d_aq, d_ad, blocks, stream());
+}
+
+void llamd_fwd_matvec_x3_splitk(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
+                                const float *d_ad, float *o0, float *o1, float *o2, int blocks,
+                                int rows0, int rows1, int rows2, int nsub) {
+    (void)nsub;  // the split of K is chosen by the library
+    llamd_fwd_matvec_x3(w0, w1, w2, d_aq, d_ad, o0, o1, o2, blocks, rows0, rows1, rows2);
+}
+
+void llamd_fwd_matvec_grouped_x2(const void *wa, const void *wb, const int32_t *d_ids,
+                                 const int8_t *d_aq, const float *d_ad, float *oa, float *ob,
+                                 int blocks, int rows, int n_used) {
+    size_t sa = 0, sb = 0;
+    int na = 0, nb = 0;
+    if (expert_view(wa, rows, blocks, &sa, &na) || expert_view(wb, rows, blocks, &sb, &nb)) return;
+    if (sa != sb) {
+        fail("matvec_grouped_x2: the two expert tensors differ in shape");
+        return;
+    }
+    launch_q6k_mv_grouped_x2(wa, wb, sa, d_ids, d_aq, d_ad, oa, ob, rows, blocks, n_used, stream());
+}
+
+void llamd_fwd_matvec_grouped_x2_splitk(const void *wa, const void *wb, const int32_t *d_ids,
+                                        const int8_t *d_aq, const float *d_ad, float *oa,
+                                        float *ob, int blocks, int rows, int n_used, int nsub) {
+    (void)nsub;
+    llamd_fwd_matvec_grouped_x2(wa, wb, d_ids, d_aq, d_ad, oa, ob, blocks, rows, n_used);
+}
+
+void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
+                                        const float *d_ad, float *d_out, int blocks, int rows,
+                                        int n_used, int nsub) {
+    (void)nsub;
+    llamd_fwd_matvec_grouped_pa(d_w, d_ids, d_aq, d_ad, d_out, blocks, rows, n_used);
+}
+
+void llamd_fwd_moe_combine(const float *d, const float *weights, float *out, int n_used,
+                           int n_embd) {
+    launch_moe_combine(d, weights, nullptr, out, n_used, n_embd, 1, stream());
 }
 
 void llamd_fwd_moe_combine_add(const float *d, const float *weights, const float *residual,
@@ -829,6 +924,11 @@ static int bench_common(const void *d_w, const int32_t *eid, const int8_t *aq, c
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);
     return rc ? fail("bench: timing failed") : 0;
+}
+
+int llamd_hip_copy_calibration(void *d_dst, const void *d_src, size_t bytes) {
+    if (!d_dst || !d_src || bytes % 16) return fail("copy_calibration: bytes must be a multiple of 16");
+    return launch_copy_calibration(d_dst, d_src, bytes, stream()) ? fail("copy_calibration: launch") : 0;
 }
 
 int llamd_rocm_matvec_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,

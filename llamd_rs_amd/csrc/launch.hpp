@@ -23,6 +23,15 @@ int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, co
                      hipStream_t st, const void *w_b = nullptr);
 // Down projection of n_slots routed experts (activation e for slot e) and the
 // routing-weighted combine (+ residual) into out, one workgroup per 16 rows.
+// One launch over up to three matrices sharing the activation (Q, K, V):
+// y[i] = W[i] x, rows[i] each; n_mat in 1..3.
+int launch_q6k_mv_x3(const void *const w[3], float *const y[3], const int rows[3], int n_mat,
+                     const int8_t *aq, const float *ad, int blocks, hipStream_t st);
+// Two expert tensors (same shape and stride) on the same ids and activation:
+// oa = Wa[ids] x, ob = Wb[ids] x, each [n_used][rows].
+int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_stride,
+                             const int32_t *ids, const int8_t *aq, const float *ad, float *oa,
+                             float *ob, int rows, int blocks, int n_used, hipStream_t st);
 // Gate and up of the routed experts in one launch, routing (softmax, top-k,
 // renormalise) in the prologue on exact logits; y = [gate | up][n_used][rows].
 int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
@@ -61,6 +70,7 @@ int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipSt
 // (the latter exits at once unless the fast pass could not prove the order).
 // The reference's router logits (sequential f32 fold per expert) and, in the
 // same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.
+int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_t st);
 struct RouterLaunch {
     const float *w, *x;
     int n_expert, k;

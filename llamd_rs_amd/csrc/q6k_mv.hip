@@ -38,20 +38,27 @@ namespace {
 
 constexpr long NEG32_BYTES = (long)0xE0E0E0E0E0E0E0E0ull;  // int8 -32 in every byte
 
+// Up to three weight matrices ("segments") share one launch and one
+// activation set: gate and up of the same experts, or Q, K and V. Items are
+// numbered segment by segment; within a segment, item = slot * tiles + tile.
+struct MvSeg {
+    const uint8_t *w;         // tiled Q6_K base (expert 0)
+    float *y;                 // [n_slots][rows]
+    int rows, tiles, first;   // first: index of the segment's first item
+};
+
 struct MvParams {
-    const uint8_t *w;         // tiled Q6_K base
+    MvSeg seg[3];
+    int n_seg, items;         // items over all segments
     size_t expert_stride;     // bytes between experts' tiled matrices
     const int32_t *ids;       // slot -> expert (nullptr: slot -> expert 0)
     const int8_t *aq;         // Q8_K quants, [n_act][blocks*256]
     const float *ad;          // Q8_K scales, [n_act][blocks]
-    float *y;                 // [n_slots][rows]
-    int rows, tiles, blocks, n_slots;
+    int blocks, n_slots;
     int act_per_slot;         // 1: slot i uses activation i; 0: all use activation 0
-    const uint8_t *w_b;       // slots >= slots_a read this weight (ids[slot - slots_a])
-    int slots_a;              // (gate and up of the same experts in one launch)
-    // routing prologue (ROUTE): every wave routes on the exact router logits
-    // and takes slot -> expert from its own selection; workgroup 0 publishes
-    // ids / weights for the kernels after it
+    // routing prologue (ROUTE): wave 0 of every workgroup routes on the exact
+    // router logits and takes slot -> expert from its own selection;
+    // workgroup 0 publishes ids / weights for the kernels after it
     const float *route_l;     // [n_expert]
     int n_expert, n_used;
     int32_t *ids_out;
@@ -213,15 +220,16 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
     const int kc = wave % KS;
     const int local = wave / KS;
     const int item = blockIdx.x * IPW + local;
-    const bool live = item < p.n_slots * p.tiles;
-    const int slot = live ? item / p.tiles : 0;
-    const int t = live ? item - slot * p.tiles : 0;
+    const bool live = item < p.items;
+    const int sg = (p.n_seg > 2 && item >= p.seg[2].first) ? 2 : (p.n_seg > 1 && item >= p.seg[1].first) ? 1 : 0;
+    const MvSeg sgm = p.seg[sg];
+    const int pos = item - sgm.first;
+    const int slot = live ? pos / sgm.tiles : 0;
+    const int t = live ? pos - slot * sgm.tiles : 0;
     const int n = lane & 15;
     const int s = lane >> 4;
     const MaskSel msel = mask_selectors(n, (n >> 2) == s);  // lane carries group n's mask
 
-    const bool second = slot >= p.slots_a;
-    const int eslot = second ? slot - p.slots_a : slot;
     int expert;
     if constexpr (ROUTE) {
         // wave 0 routes; the workgroup's other waves wait for its choice
@@ -242,14 +250,14 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
             }
         }
         __syncthreads();
-        expert = live ? rsh.sorted[eslot] : 0;
+        expert = live ? rsh.sorted[slot] : 0;
     } else {
-        expert = (live && p.ids) ? p.ids[eslot] : 0;
+        expert = (live && p.ids) ? p.ids[slot] : 0;
     }
     const int act = p.act_per_slot ? slot : 0;
     const int8_t *aq = p.aq + (size_t)act * p.blocks * QK_K;
     const float *ad = p.ad + (size_t)act * p.blocks;
-    const uint8_t *seg0 = (second ? p.w_b : p.w) + (size_t)expert * p.expert_stride +
+    const uint8_t *seg0 = sgm.w + (size_t)expert * p.expert_stride +
                           (size_t)t * p.blocks * SEG_BYTES;
 
     const int bpc = (p.blocks + KS - 1) / KS;
@@ -293,11 +301,11 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
     }
     if (s == 0) {
         const int row = t * TILE_ROWS + n;
-        if (row < p.rows) {
+        if (row < sgm.rows) {
             float tot = -0.0f;
 #pragma unroll
             for (int c = 0; c < 8; ++c) tot = tot + cls[c];
-            p.y[(size_t)slot * p.rows + row] = tot;
+            sgm.y[(size_t)slot * sgm.rows + row] = tot;
         }
     }
 }
@@ -543,73 +551,112 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
 
 int g_tune_mv_ks = 0;
 
-int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
-                     const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st, const void *w_b) {
-    MvParams p;
-    // with a second weight, slots [n_slots, 2 n_slots) repeat the ids on it
-    p.w_b = (const uint8_t *)w_b;
-    p.slots_a = w_b ? n_slots : 0x7FFFFFFF;
-    if (w_b) n_slots *= 2;
-    p.w = (const uint8_t *)w;
-    p.expert_stride = expert_stride;
-    p.ids = ids;
-    p.aq = aq;
-    p.ad = ad;
-    p.y = y;
-    p.rows = rows;
-    p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
-    p.blocks = blocks;
-    p.n_slots = n_slots;
-    p.act_per_slot = act_per_slot;
-    const int items = p.tiles * n_slots;
-    const int ks = g_tune_mv_ks;
-    if (ks == 1 || ks == 2 || ks == 4) {
-        const int ipw = 4 / ks;
-        if (ks == 1 || blocks <= 16) {
-            if (ks == 1) hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
-            if (ks == 2) hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + ipw - 1) / ipw), dim3(256), 0, st, p);
-            if (ks == 4) hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
-            return hipGetLastError() == hipSuccess ? 0 : -1;
-        }
+namespace {
+
+// Fills the segment table for n matrices sharing `rows`-independent shapes.
+void set_segments(MvParams &p, int n, const void *const *w, float *const *y, const int *rows,
+                  int n_slots) {
+    int first = 0;
+    p.n_seg = n;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].w = (const uint8_t *)w[i];
+        p.seg[i].y = y[i];
+        p.seg[i].rows = rows[i];
+        p.seg[i].tiles = (rows[i] + TILE_ROWS - 1) / TILE_ROWS;
+        p.seg[i].first = first;
+        first += p.seg[i].tiles * n_slots;
     }
-    // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four waves per
-    // tile, each on a quarter of the row, beat one wave per tile at every
-    // size -- more loads in flight per tile and shorter per-wave chains.
-    if (blocks <= 16) {
-        hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
+    for (int i = n; i < 3; ++i) p.seg[i] = p.seg[0];
+    p.items = first;
+    p.n_slots = n_slots;
+}
+
+int launch_b1(const MvParams &p, hipStream_t st) {
+    const int items = p.items;
+    const int ks = g_tune_mv_ks;
+    if (p.blocks <= 16 && (ks == 2 || ks == 4 || ks == 0)) {
+        if (ks == 2)
+            hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + 1) / 2), dim3(256), 0, st, p);
+        else
+            // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
+            // waves per tile, each on a quarter of the row, beat one wave per
+            // tile at every size -- more loads in flight per tile and shorter
+            // per-wave chains.
+            hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
     } else {
         hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
-                        const float *logits, int n_expert, int n_used, int32_t *ids_out,
-                        float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
-                        int rows, int blocks, hipStream_t st) {
-    if (blocks > 16 || n_expert > ROUTE_MAX_EXPERTS || n_used > ROUTE_MAX_USED) return -1;
-    MvParams p;
-    p.w = (const uint8_t *)w;
-    p.w_b = (const uint8_t *)w_b;
-    p.slots_a = n_used;
+}  // namespace
+
+int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
+                     const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
+                     hipStream_t st, const void *w_b) {
+    MvParams p = {};
+    // with a second weight, its outputs follow the first's: y = [w | w_b]
+    const void *ws[2] = {w, w_b};
+    float *ys[2] = {y, y + (size_t)n_slots * rows};
+    const int rs[2] = {rows, rows};
+    set_segments(p, w_b ? 2 : 1, ws, ys, rs, n_slots);
     p.expert_stride = expert_stride;
-    p.ids = nullptr;
+    p.ids = ids;
     p.aq = aq;
     p.ad = ad;
-    p.y = y;
-    p.rows = rows;
-    p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
     p.blocks = blocks;
-    p.n_slots = 2 * n_used;
-    p.act_per_slot = 0;
+    p.act_per_slot = act_per_slot;
+    return launch_b1(p, st);
+}
+
+int launch_q6k_mv_x3(const void *const w[3], float *const y[3], const int rows[3], int n_mat,
+                     const int8_t *aq, const float *ad, int blocks, hipStream_t st) {
+    if (n_mat < 1 || n_mat > 3) return -1;
+    MvParams p = {};
+    set_segments(p, n_mat, w, y, rows, 1);
+    p.aq = aq;
+    p.ad = ad;
+    p.blocks = blocks;
+    return launch_b1(p, st);
+}
+
+int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_stride,
+                             const int32_t *ids, const int8_t *aq, const float *ad, float *oa,
+                             float *ob, int rows, int blocks, int n_used, hipStream_t st) {
+    MvParams p = {};
+    const void *ws[2] = {wa, wb};
+    float *ys[2] = {oa, ob};
+    const int rs[2] = {rows, rows};
+    set_segments(p, 2, ws, ys, rs, n_used);
+    p.expert_stride = expert_stride;
+    p.ids = ids;
+    p.aq = aq;
+    p.ad = ad;
+    p.blocks = blocks;
+    return launch_b1(p, st);
+}
+
+int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
+                         const float *logits, int n_expert, int n_used, int32_t *ids_out,
+                         float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
+                         int rows, int blocks, hipStream_t st) {
+    if (blocks > 16 || n_expert > ROUTE_MAX_EXPERTS || n_used > ROUTE_MAX_USED) return -1;
+    MvParams p = {};
+    const void *ws[2] = {w, w_b};
+    float *ys[2] = {y, y + (size_t)n_used * rows};
+    const int rs[2] = {rows, rows};
+    set_segments(p, 2, ws, ys, rs, n_used);
+    p.expert_stride = expert_stride;
+    p.aq = aq;
+    p.ad = ad;
+    p.blocks = blocks;
     p.route_l = logits;
     p.n_expert = n_expert;
     p.n_used = n_used;
     p.ids_out = ids_out;
     p.w_out = w_out;
     p.stats = stats;
-    hipLaunchKernelGGL((q6k_mv_b1<4, true>), dim3(p.tiles * p.n_slots), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((q6k_mv_b1<4, true>), dim3(p.items), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

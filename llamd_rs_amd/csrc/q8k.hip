@@ -64,7 +64,22 @@ __global__ void silu_mul_f32(const float *gate, const float *up, float *out, int
     if (i < n) out[i] = silu_ref(gate[i], tab) * up[i];
 }
 
+// Plain grid-stride copy (16-byte vectors), the calibration kernel for the
+// HBM traffic counters: it reads and writes exactly n16 * 16 bytes.
+__global__ __launch_bounds__(256) void copy_calibration(uint4 *dst, const uint4 *src, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}
+
 }  // namespace
+
+int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_t st) {
+    if (bytes % 16) return -1;
+    hipLaunchKernelGGL(copy_calibration, dim3(4096), dim3(256), 0, st, (uint4 *)dst,
+                       (const uint4 *)src, bytes / 16);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm, float *d, int16_t *bsums,
                         int nblocks, hipStream_t st) {
