@@ -77,18 +77,51 @@ def sync(L):
         raise RuntimeError(f"device error: {last_error()}")
 
 
-def time_region(L, fn, steps, warmup):
+def time_region(L, fn, steps, warmup, graph=True):
+    """W eager warm-up steps, then EXACTLY `steps` steps timed with HIP events
+    on the library stream.
+
+    graph=True (loops of short kernels): the timed steps are captured once
+    into a HIP graph (capture records, it does not run) and replayed, so the
+    figure is the device's, not the Python loop's launch rate; every step
+    still runs every kernel on its own (rotating) weights, and one untimed
+    replay first warms the graph's upload. graph=False (kernels long enough
+    that the host keeps ahead): plain launches on the stream."""
     for i in range(warmup):
         fn(i)
     sync(L)
-    t = Timer(L)
-    t.rec(0)
-    for i in range(steps):
-        fn(warmup + i)
-    t.rec(1)
-    ms = t.ms(0, 1)
-    sync(L)
-    t.close()
+    if not graph:
+        t = Timer(L)
+        t.rec(0)
+        for i in range(steps):
+            fn(warmup + i)
+        t.rec(1)
+        sync(L)
+        ms = t.ms(0, 1)
+        t.close()
+        return ms
+    if L.llamd_fwd_begin_capture():
+        raise RuntimeError("graph capture could not start")
+    try:
+        for i in range(steps):
+            fn(warmup + i)
+    finally:
+        if L.llamd_fwd_end_capture():
+            raise RuntimeError("graph capture failed")
+    try:
+        if L.llamd_fwd_graph_launch():
+            raise RuntimeError("graph launch failed")
+        sync(L)
+        t = Timer(L)
+        t.rec(0)
+        if L.llamd_fwd_graph_launch():
+            raise RuntimeError("graph launch failed")
+        t.rec(1)
+        sync(L)
+        ms = t.ms(0, 1)
+        t.close()
+    finally:
+        L.llamd_fwd_graph_destroy()
     return ms
 
 
@@ -221,7 +254,7 @@ def bench_copy(L, rocm, mib=512, reps=5):
     def f(i):
         if L.llamd_hip_copy_calibration(b.ptr, a.ptr, n):
             raise RuntimeError("copy")
-    ms = time_region(L, f, reps, 1)
+    ms = time_region(L, f, reps, 1, graph=False)
     a.close(); b.close()
     res = {"bytes_read": n, "bytes_written": n, "us": ms / reps * 1e3,
            "gbs_read_plus_write": 2 * n / (ms / reps * 1e-3) / 1e9}
@@ -268,7 +301,7 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
             if L.llamd_hip_lmhead_forward(h.handle, xb.ptr, nseq, logits.ptr, ids.ptr):
                 raise RuntimeError("lmhead")
         steps = max(10, K // 4)
-        ms = time_region(L, f, steps, 3)
+        ms = time_region(L, f, steps, 3, graph=False)
         by = q6k_bytes(rows, k) + nseq * k * 4 + nseq * rows * 4
         out[f"lm_head_b{nseq}"] = {"us_per_call": ms / steps * 1e3, "bytes": by,
                                    "gbs": by / (ms / steps * 1e-3) / 1e9,
@@ -281,7 +314,7 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     def fm(i):
         L.llamd_fwd_matvec(heads[i % 4][0].ptr, q1.ptr, d1.ptr, logits.ptr, k // QK_K, rows)
     steps = max(10, K // 4)
-    ms = time_region(L, fm, steps, 3)
+    ms = time_region(L, fm, steps, 3, graph=False)
     by = q6k_bytes(rows, k) + k + (k // QK_K) * 4 + rows * 4
     out["lm_head_matvec_b1"] = {"us_per_launch": ms / steps * 1e3, "bytes": by,
                                 "gbs": by / (ms / steps * 1e-3) / 1e9,
@@ -343,7 +376,7 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
         if L.llamd_hip_moe_prefill(layers[i % 4].handle, xs.ptr, ids_d.ptr, w_d.ptr, po.ptr, n_tok):
             raise RuntimeError("prefill")
     steps = max(5, K // 20)
-    ms = time_region(L, fp, steps, 2)
+    ms = time_region(L, fp, steps, 4, graph=False)  # warm-up touches all 4 layers
     ops = 2 * n_tok * n_used * (2 * n_ff * n_embd + n_embd * n_ff)
     used = len(set(ids_h.ravel().tolist()))
     wbytes = used * 3 * q6k_bytes(n_ff, n_embd)
