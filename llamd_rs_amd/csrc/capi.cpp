@@ -99,16 +99,25 @@ bool down(void *dst, const void *src, size_t n) {
 }
 bool sync() { return hip_ok(hipStreamSynchronize(stream()), "synchronize"); }
 
-int quantize_dev(const float *d_x, int8_t *d_qs, int8_t *d_qs_cm, float *d_d, int16_t *d_bs,
-                 int nblocks) {
-    return launch_q8k_quantize(d_x, d_qs, d_qs_cm, d_d, d_bs, nblocks, stream());
+int quantize_dev(const float *d_x, int8_t *d_qs, float *d_d, int16_t *d_bs, int nblocks) {
+    return launch_q8k_quantize(d_x, d_qs, d_d, d_bs, nblocks, stream());
 }
 
-// Single-group batched matvec (all rows, nseq activations, identity pairs).
-int batched_dev(const void *w, const int8_t *aq_cm, const float *ad, float *y, int blocks,
-                int rows, int nseq) {
-    return launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, aq_cm,
-                                 ad, y, rows, rows, blocks, nseq, (nseq + 15) / 16, stream());
+constexpr int CHUNK = 16;             // tokens per chunk of the batched operand layout
+constexpr size_t CHUNK_BLOCK = 4096;  // bytes per (chunk, block)
+
+size_t chunk_q_bytes(int nseq, int blocks) {
+    return (size_t)((nseq + CHUNK - 1) / CHUNK) * blocks * CHUNK_BLOCK;
+}
+size_t chunk_d_bytes(int nseq, int blocks) {
+    return (size_t)((nseq + CHUNK - 1) / CHUNK) * blocks * CHUNK * 4;
+}
+
+// Single-group batched matvec: all rows, nseq tokens in chunk slots 0..nseq-1.
+int batched_dev(const void *w, const int8_t *cq, const float *cd, float *y, int blocks, int rows,
+                int nseq) {
+    return launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, cq, cd, y, rows,
+                                 rows, blocks, nseq, (nseq + CHUNK - 1) / CHUNK, stream());
 }
 
 }  // namespace
@@ -366,14 +375,22 @@ int llamd_hip_matvec_q6k_batched(const void *d_w, const int8_t *aq, const float 
         !ad || !out)
         return fail("batched: shape mismatch");
     if (wi.n_expert > 1 && rows > wi.rows) return fail("batched: rows span experts");
-    const size_t nq = (size_t)nseq * blocks * QK;
-    std::vector<int8_t> cm(nq);
-    for (size_t b = 0; b < (size_t)nseq * blocks; ++b)
-        for (int e = 0; e < QK; ++e) cm[b * QK + 32 * (e % 8) + e / 8] = aq[b * QK + e];
+    // the reference's BlockQ8K arrays -> the token-chunked operand layout
+    const size_t nq = chunk_q_bytes(nseq, blocks), nd = chunk_d_bytes(nseq, blocks);
+    std::vector<int8_t> cq(nq, 0);
+    std::vector<float> cd(nd / 4, 0.0f);
+    for (int t = 0; t < nseq; ++t)
+        for (int b = 0; b < blocks; ++b) {
+            const size_t base = (size_t)(t / CHUNK) * blocks + b;
+            for (int e = 0; e < QK; ++e)
+                cq[base * CHUNK_BLOCK + (e % 8) * 512 + (t % CHUNK) * 32 + e / 8] =
+                    aq[((size_t)t * blocks + b) * QK + e];
+            cd[base * CHUNK + t % CHUNK] = ad[(size_t)t * blocks + b];
+        }
     std::lock_guard<std::mutex> lk(g_mu);
-    DevBuf q(nq), d((size_t)nseq * blocks * 4), y((size_t)rows * nseq * 4);
+    DevBuf q(nq), d(nd), y((size_t)rows * nseq * 4);
     if (!q.p || !d.p || !y.p) return fail("hipMalloc");
-    if (!up(q.p, cm.data(), nq) || !up(d.p, ad, (size_t)nseq * blocks * 4)) return -1;
+    if (!up(q.p, cq.data(), nq) || !up(d.p, cd.data(), nd)) return -1;
     if (batched_dev(d_w, q.as<int8_t>(), d.as<float>(), y.as<float>(), blocks, rows, nseq))
         return fail("launch");
     if (!down(out, y.p, (size_t)rows * nseq * 4) || !sync()) return -1;
@@ -387,7 +404,7 @@ int llamd_rocm_quantize_q8k(const float *x, int nblocks, int8_t *qs, float *d, i
         db((size_t)nblocks * 32);
     if (!dx.p || !dq.p || !dd.p || !db.p) return fail("hipMalloc");
     if (!up(dx.p, x, (size_t)nblocks * QK * 4)) return -1;
-    if (quantize_dev(dx.as<float>(), dq.as<int8_t>(), nullptr, dd.as<float>(), db.as<int16_t>(),
+    if (quantize_dev(dx.as<float>(), dq.as<int8_t>(), dd.as<float>(), db.as<int16_t>(),
                      nblocks))
         return fail("launch");
     if (!down(qs, dq.p, (size_t)nblocks * QK) || !down(d, dd.p, (size_t)nblocks * 4)) return -1;
@@ -403,7 +420,7 @@ int llamd_hip_swiglu_q8k(const float *gate, const float *upv, int nblocks, float
     DevBuf dg(n * 4), du(n * 4), da(n * 4), dq(n), dd((size_t)nblocks * 4), db((size_t)nblocks * 32);
     if (!dg.p || !du.p || !da.p || !dq.p || !dd.p || !db.p) return fail("hipMalloc");
     if (!up(dg.p, gate, n * 4) || !up(du.p, upv, n * 4)) return -1;
-    if (launch_swiglu_q8k(dg.as<float>(), du.as<float>(), da.as<float>(), dq.as<int8_t>(), nullptr,
+    if (launch_swiglu_q8k(dg.as<float>(), du.as<float>(), da.as<float>(), dq.as<int8_t>(),
                           dd.as<float>(), db.as<int16_t>(), nblocks, stream()))
         return fail("launch");
     if (act && !down(act, da.p, n * 4)) return -1;
@@ -507,7 +524,7 @@ void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const in
 }
 
 void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks) {
-    quantize_dev(d_x, d_qs, nullptr, d_d, nullptr, nblocks);
+    quantize_dev(d_x, d_qs, d_d, nullptr, nblocks);
 }
 
 void llamd_fwd_silu_mul(const float *gate, const float *upv, float *out, int n) {
@@ -611,7 +628,7 @@ struct MoeLayer {
     DevBuf g, aq, ad, dn;
     // prefill scratch (grown on demand)
     int cap_tok = 0;
-    DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_tok, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
+    DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_slot, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
 };
 
 }  // namespace
@@ -695,7 +712,7 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
                                m->g.as<float>(), m->n_ff, m->be, st);
     // 3. SwiGLU + Q8_K of the activations
     rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
-                            nullptr, m->aq.as<int8_t>(), nullptr, m->ad.as<float>(), nullptr,
+                            nullptr, m->aq.as<int8_t>(), m->ad.as<float>(), nullptr,
                             m->n_used * m->bf, st);
     // 4. down projection of the routed experts + weighted combine + residual
     rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
@@ -745,43 +762,48 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
         // kernel still reads the old buffers
         if (!sync()) return -1;
         const size_t NP = (size_t)np;
-        bool ok = m->p_xq.alloc((size_t)n_tok * m->n_embd) && m->p_xd.alloc((size_t)n_tok * m->be * 4) &&
+        const int chunks = np / CHUNK + m->n_expert;  // bound on sum of ceil(count/16)
+        bool ok = m->p_xq.alloc((size_t)chunks * m->be * CHUNK_BLOCK) &&
+                  m->p_xd.alloc((size_t)chunks * m->be * CHUNK * 4) &&
                   m->p_grp_e.alloc(m->n_expert * 4) && m->p_grp_s.alloc(m->n_expert * 4) &&
                   m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc((m->n_expert + 1) * 4) &&
-                  m->p_tok.alloc(NP * 4) && m->p_idx.alloc(NP * 4) &&
+                  m->p_slot.alloc(NP * 4) && m->p_idx.alloc(NP * 4) &&
                   m->p_g.alloc(NP * m->n_ff * 4) && m->p_u.alloc(NP * m->n_ff * 4) &&
-                  m->p_aq.alloc(NP * m->n_ff) && m->p_ad.alloc(NP * m->bf * 4) &&
+                  m->p_aq.alloc((size_t)chunks * m->bf * CHUNK_BLOCK) &&
+                  m->p_ad.alloc((size_t)chunks * m->bf * CHUNK * 4) &&
                   m->p_dn.alloc(NP * m->n_embd * 4);
         if (!ok) { m->cap_tok = 0; return fail("moe_prefill: allocation failed"); }
         m->cap_tok = n_tok;
     }
     hipStream_t st = stream();
-    const int max_sub = np / 16 + m->n_expert;
+    const int max_chunks = np / CHUNK + m->n_expert;
     int rc = 0;
     rc |= launch_moe_group(d_ids, np, m->n_used, m->n_expert, m->p_grp_e.as<int32_t>(),
                            m->p_grp_s.as<int32_t>(), m->p_grp_c.as<int32_t>(),
-                           m->p_sub.as<int32_t>(), m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(), st);
-    rc |= launch_q8k_quantize(d_x, nullptr, m->p_xq.as<int8_t>(), m->p_xd.as<float>(), nullptr,
-                              n_tok * m->be, st);
-    // gate / up: activation = the pair's token, output row = the pair index
+                           m->p_sub.as<int32_t>(), m->p_slot.as<int32_t>(), m->p_idx.as<int32_t>(),
+                           st);
+    // Q8_K of every token, written to the chunk slot of each of its n_used pairs
+    rc |= launch_q8k_quantize_chunks(d_x, n_tok, m->be, m->p_slot.as<int32_t>(), m->n_used,
+                                     m->p_xq.as<int8_t>(), m->p_xd.as<float>(), st);
+    // gate / up: output row = the pair index
     rc |= launch_q6k_mv_batched(m->gate, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
-                                m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(),
-                                m->p_xq.as<int8_t>(), m->p_xd.as<float>(), m->p_g.as<float>(),
-                                m->n_ff, m->n_ff, m->be, m->n_expert, max_sub, st);
+                                m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
+                                m->p_g.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st);
     rc |= launch_q6k_mv_batched(m->upw, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
-                                m->p_tok.as<int32_t>(), m->p_idx.as<int32_t>(),
-                                m->p_xq.as<int8_t>(), m->p_xd.as<float>(), m->p_u.as<float>(),
-                                m->n_ff, m->n_ff, m->be, m->n_expert, max_sub, st);
-    rc |= launch_swiglu_q8k(m->p_g.as<float>(), m->p_u.as<float>(), nullptr, nullptr,
-                            m->p_aq.as<int8_t>(), m->p_ad.as<float>(), nullptr, np * m->bf, st);
-    // down: activation and output are both the pair
+                                m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
+                                m->p_u.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st);
+    // SwiGLU + Q8_K per pair, into the pair's chunk slot
+    rc |= launch_swiglu_q8k_chunks(m->p_g.as<float>(), m->p_u.as<float>(), np, m->bf,
+                                   m->p_slot.as<int32_t>(), m->p_aq.as<int8_t>(),
+                                   m->p_ad.as<float>(), st);
+    // down: output row = the pair index
     rc |= launch_q6k_mv_batched(m->downw, m->sd, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
-                                m->p_idx.as<int32_t>(), m->p_idx.as<int32_t>(),
-                                m->p_aq.as<int8_t>(), m->p_ad.as<float>(), m->p_dn.as<float>(),
-                                m->n_embd, m->n_embd, m->bf, m->n_expert, max_sub, st);
+                                m->p_idx.as<int32_t>(), m->p_aq.as<int8_t>(), m->p_ad.as<float>(),
+                                m->p_dn.as<float>(), m->n_embd, m->n_embd, m->bf, m->n_expert,
+                                max_chunks, st);
     rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, nullptr, d_out, m->n_used, m->n_embd, n_tok, st);
     return rc ? fail("moe_prefill: launch failed") : 0;
 }
@@ -812,7 +834,7 @@ namespace {
 struct LmHead {
     const void *w;
     int rows, blocks, cap;
-    DevBuf xq, xq_cm, xd, pv, pi;
+    DevBuf xq, xd, cq, cd, pv, pi;  // cq, cd: chunked activations for nseq > 1
 };
 }  // namespace
 
@@ -829,7 +851,8 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
     l->w = d_w; l->rows = rows; l->blocks = blocks; l->cap = max_seq;
     const int parts = argmax_parts(rows);
     const size_t nq = (size_t)max_seq * blocks * QK;
-    if (!l->xq.alloc(nq) || !l->xq_cm.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
+    if (!l->xq.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
+        !l->cq.alloc(chunk_q_bytes(max_seq, blocks)) || !l->cd.alloc(chunk_d_bytes(max_seq, blocks)) ||
         !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4)) {
         delete l;
         fail("lmhead_create: allocation failed");
@@ -851,15 +874,14 @@ int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logit
     hipStream_t st = stream();
     int rc = 0;
     if (nseq == 1) {
-        rc |= launch_q8k_quantize(d_x, l->xq.as<int8_t>(), nullptr, l->xd.as<float>(), nullptr,
-                                  l->blocks, st);
+        rc |= launch_q8k_quantize(d_x, l->xq.as<int8_t>(), l->xd.as<float>(), nullptr, l->blocks, st);
         rc |= launch_q6k_mv_b1(l->w, 0, nullptr, l->xq.as<int8_t>(), l->xd.as<float>(), d_logits,
                                l->rows, l->blocks, 1, 0, st);
     } else {
-        rc |= launch_q8k_quantize(d_x, nullptr, l->xq_cm.as<int8_t>(), l->xd.as<float>(), nullptr,
-                                  nseq * l->blocks, st);
-        rc |= batched_dev(l->w, l->xq_cm.as<int8_t>(), l->xd.as<float>(), d_logits, l->blocks,
-                          l->rows, nseq);
+        rc |= launch_q8k_quantize_chunks(d_x, nseq, l->blocks, nullptr, 1, l->cq.as<int8_t>(),
+                                         l->cd.as<float>(), st);
+        rc |= batched_dev(l->w, l->cq.as<int8_t>(), l->cd.as<float>(), d_logits, l->blocks, l->rows,
+                          nseq);
     }
     rc |= launch_argmax(d_logits, l->rows, l->rows, nseq, l->pv.as<float>(), l->pi.as<int>(), d_ids, st);
     return rc ? fail("lmhead_forward: launch failed") : 0;

@@ -12,9 +12,10 @@
 //
 // Outputs (all experts are groups, empty ones included):
 //   grp_expert[e] = e, grp_start[e], grp_count[e],
-//   sub_start[0..n_expert] = prefix sum of ceil(count/16) (16-token MFMA
-//   sub-tiles), pair_tok[i] = token of the i-th sorted pair, pair_idx[i] = its
-//   pair index t * n_used + k.
+//   sub_start[0..n_expert] = prefix sum of ceil(count/16) (16-token chunks
+//   of the batched kernel), slot_of_pair[p] = the chunk slot of pair p
+//   (chunk sub_start[e] + j / 16, token j % 16 for the j-th pair of expert
+//   e), pair_idx[i] = the pair index t * n_used + k at sorted position i.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -26,8 +27,11 @@ constexpr int GROUP_MAX_EXPERTS = 1024;
 __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pairs, int n_used,
                                                   int n_expert, int32_t *grp_expert,
                                                   int32_t *grp_start, int32_t *grp_count,
-                                                  int32_t *sub_start, int32_t *pair_tok,
+                                                  int32_t *sub_start, int32_t *slot_of_pair,
                                                   int32_t *pair_idx) {
+    __shared__ int sub_lds[GROUP_MAX_EXPERTS];
+    __shared__ int start_lds[GROUP_MAX_EXPERTS];
+    (void)n_used;
     __shared__ int hist[GROUP_MAX_EXPERTS];
     __shared__ int cursor[GROUP_MAX_EXPERTS];
     const int tid = threadIdx.x;
@@ -43,6 +47,8 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
             grp_start[e] = start;
             grp_count[e] = c;
             sub_start[e] = sub;
+            sub_lds[e] = sub;
+            start_lds[e] = start;
             cursor[e] = start;
             start += c;
             sub += (c + 15) / 16;
@@ -51,8 +57,10 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     }
     __syncthreads();
     for (int p = tid; p < n_pairs; p += blockDim.x) {
-        const int pos = atomicAdd(&cursor[ids[p]], 1);
-        pair_tok[pos] = p / n_used;
+        const int e = ids[p];
+        const int pos = atomicAdd(&cursor[e], 1);
+        const int j = pos - start_lds[e];
+        slot_of_pair[p] = (sub_lds[e] + j / 16) * 16 + j % 16;
         pair_idx[pos] = p;
     }
 }
@@ -61,10 +69,11 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
 
 int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
                      int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
-                     int32_t *sub_start, int32_t *pair_tok, int32_t *pair_idx, hipStream_t st) {
+                     int32_t *sub_start, int32_t *slot_of_pair, int32_t *pair_idx,
+                     hipStream_t st) {
     if (n_expert > GROUP_MAX_EXPERTS || n_expert <= 0) return -1;
     hipLaunchKernelGGL(moe_group, dim3(1), dim3(1024), 0, st, ids, n_pairs, n_used, n_expert,
-                       grp_expert, grp_start, grp_count, sub_start, pair_tok, pair_idx);
+                       grp_expert, grp_start, grp_count, sub_start, slot_of_pair, pair_idx);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -11,9 +11,7 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
-extern int g_tune_router;
-extern int g_tune_down_fused;  // 1: SwiGLU in the down kernel's prologue  // router kernel arrangement (see launch_router)
-extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4
+extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4 (0: automatic)
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -42,32 +40,41 @@ int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *
                             const int8_t *aq, const float *ad, const float *weights,
                             const float *res, float *out, int rows, int blocks, int n_slots,
                             hipStream_t st);
-// Expert-grouped batched matvec (see q6k_mv.hip). sub_start has n_groups+1
-// entries; max_subtiles bounds sub_start[n_groups] and sizes the grid. With
-// grp_expert == nullptr there is a single group (expert 0) of n_groups pairs.
+// Expert-grouped batched matvec (see q6k_mv.hip). Activations are in the
+// token-chunked layout (q8k_wave.hpp): chunk k holds the 16 tokens of
+// sub-tile k. sub_start has n_groups+1 entries (prefix of ceil(count/16));
+// max_chunks bounds sub_start[n_groups] and sizes the grid. The output of the
+// pair at sorted position i is row pair_out[i] of y (nullptr: row i). With
+// grp_expert == nullptr there is a single group (expert 0) of n_groups tokens.
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
                           const int32_t *grp_start, const int32_t *grp_count,
-                          const int32_t *sub_start, const int32_t *pair_act,
-                          const int32_t *pair_out, const int8_t *aq_cm, const float *ad, float *y,
-                          int ldy, int rows, int blocks, int n_groups, int max_subtiles,
-                          hipStream_t st);
+                          const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
+                          const float *act_d, float *y, int ldy, int rows, int blocks,
+                          int n_groups, int max_chunks, hipStream_t st);
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 
 // q8k.hip
-int launch_q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm, float *d, int16_t *bsums,
-                        int nblocks, hipStream_t st);
-int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs,
-                      int8_t *qs_cm, float *d, int16_t *bsums, int nblocks, hipStream_t st);
-// moe grouping (group.hip): counting sort of (token, slot) pairs by expert
+int launch_q8k_quantize(const float *x, int8_t *qs, float *d, int16_t *bsums, int nblocks,
+                        hipStream_t st);
+// rows of x to the token-chunked layout, each row to `fan` slots slot_of[r*fan+k]
+// (slot_of == nullptr: row r to slot r)
+int launch_q8k_quantize_chunks(const float *x, int rows, int blocks, const int32_t *slot_of,
+                               int fan, int8_t *cq, float *cd, hipStream_t st);
+int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs, float *d,
+                      int16_t *bsums, int nblocks, hipStream_t st);
+int launch_swiglu_q8k_chunks(const float *gate, const float *up, int rows, int blocks,
+                             const int32_t *slot_of, int8_t *cq, float *cd, hipStream_t st);
+// moe grouping (group.hip): counting sort of the (token, k) pairs by expert.
+// Outputs grp_* per expert, sub_start (prefix of ceil(count/16)), for each
+// pair p = token * n_used + k its chunk slot slot_of_pair[p], and for each
+// sorted position its pair index pair_idx.
 int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
                      int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
-                     int32_t *sub_start, int32_t *pair_tok, int32_t *pair_idx,
+                     int32_t *sub_start, int32_t *slot_of_pair, int32_t *pair_idx,
                      hipStream_t st);
 int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipStream_t st);
 
 // moe.hip
-// Router + route for one token (moe.hip): router_fast then router_exact
-// (the latter exits at once unless the fast pass could not prove the order).
 // The reference's router logits (sequential f32 fold per expert) and, in the
 // same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.
 int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_t st);

@@ -439,37 +439,73 @@ struct BatchParams {
     const int32_t *grp_start;    // first pair of the group
     const int32_t *grp_count;    // pairs in the group
     const int32_t *sub_start;    // prefix sum of ceil(count/16) over groups
-    const int32_t *pair_act;     // activation index of each pair (nullptr: identity)
-    const int32_t *pair_out;     // output row of each pair (nullptr: identity)
-    const int8_t *aq_cm;         // class-major Q8_K quants [n_act][blocks*256]
-    const float *ad;             // [n_act][blocks]
+    const int32_t *pair_out;     // output row of each sorted pair (nullptr: identity)
+    const int8_t *act_q;         // token-chunked Q8_K quants (q8k_wave.hpp)
+    const float *act_d;          // their scales
     float *y;                    // y[pair_out * ldy + row]
     int ldy, rows, tiles, blocks, n_groups;
-    int single_count;            // grp_expert == nullptr: one group, expert 0, this many pairs
+    int single_count;            // grp_expert == nullptr: one group, expert 0, this many tokens
 };
 
-__device__ __forceinline__ void fold_digits(uint64_t codes, uint32_t scw, long &lo8, long &hi8) {
-    uint64_t lo = 0, hi = 0;
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Per-block constants of the fold: this lane's 4 scales as int16 pairs, and
+// -32 * scale likewise (so sc * (q - 32) is one packed multiply-add).
+struct FoldScales {
+    s16x2 sc[4], m32[4];
+};
+
+__device__ __forceinline__ FoldScales fold_scales(uint32_t scw) {
+    FoldScales f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-        const int q = (int)((codes >> (8 * kk)) & 0x3F) - 32;
-        const int sc = (int8_t)((scw >> (8 * (kk >> 1))) & 0xFF);
-        const int v = sc * q;
-        lo |= (uint64_t)(v & 63) << (8 * kk);
-        hi |= (uint64_t)((v >> 6) & 0xFF) << (8 * kk);
+    for (int j = 0; j < 4; ++j) {
+        const short v = (short)(int8_t)((scw >> (8 * j)) & 0xFF);
+        f.sc[j] = s16x2{v, v};
+        f.m32[j] = s16x2{(short)(-32 * v), (short)(-32 * v)};
     }
-    lo8 = (long)lo;
-    hi8 = (long)hi;
+    return f;
 }
 
+// w' = sc * (q - 32) for the lane's 8 class-c weights (codes: one byte each,
+// weight kk uses scale kk / 2), split into int8 digits w' = 64 * hi + lo with
+// lo in [0, 63] and hi in [-64, 64]: packed 16-bit arithmetic, two weights
+// per instruction, then byte permutes back to the 8-byte MFMA operands.
+__device__ __forceinline__ void fold_digits(uint64_t codes, const FoldScales &f, long &lo8,
+                                            long &hi8) {
+    const uint32_t c0 = (uint32_t)codes, c1 = (uint32_t)(codes >> 32);
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0u, c0, 0x0C010C00u),
+                           __builtin_amdgcn_perm(0u, c0, 0x0C030C02u),
+                           __builtin_amdgcn_perm(0u, c1, 0x0C010C00u),
+                           __builtin_amdgcn_perm(0u, c1, 0x0C030C02u)};
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const s16x2 v = as_s16x2(w[j]) * f.sc[j] + f.m32[j];
+        lo[j] = as_u32(v) & 0x003F003Fu;
+        hi[j] = as_u32(v >> (s16x2){6, 6});
+    }
+    lo8 = (long)((uint64_t)__builtin_amdgcn_perm(lo[1], lo[0], 0x06040200u) |
+                 ((uint64_t)__builtin_amdgcn_perm(lo[3], lo[2], 0x06040200u) << 32));
+    hi8 = (long)((uint64_t)__builtin_amdgcn_perm(hi[1], hi[0], 0x06040200u) |
+                 ((uint64_t)__builtin_amdgcn_perm(hi[3], hi[2], 0x06040200u) << 32));
+}
+
+
+// One wave per (group, 16-token chunk, 16-row tile). The chunk index is the
+// global sub-tile number, which is also where the activations of its 16
+// tokens sit in the token-chunked layout: each class plane of a block is one
+// contiguous 512-byte load for the wave.
 __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int t = item % p.tiles;
     const int sub = item / p.tiles;
-    int g = 0, st = sub, cnt, start = 0, expert = 0;
+    int st = sub, cnt, start = 0, expert = 0;
     if (p.grp_expert) {
-        // find the group whose sub-tile range holds `sub` (sub_start has
+        // find the group whose chunk range holds `sub` (sub_start has
         // n_groups + 1 entries)
         if (sub >= p.sub_start[p.n_groups]) return;
         int lo = 0, hi = p.n_groups;
@@ -477,23 +513,21 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
             const int mid = (lo + hi) >> 1;
             if (p.sub_start[mid] <= sub) lo = mid; else hi = mid;
         }
-        g = lo;
-        st = sub - p.sub_start[g];
-        cnt = p.grp_count[g];
-        start = p.grp_start[g];
-        expert = p.grp_expert[g];
+        st = sub - p.sub_start[lo];
+        cnt = p.grp_count[lo];
+        start = p.grp_start[lo];
+        expert = p.grp_expert[lo];
     } else {
         cnt = p.single_count;
         if (sub >= (cnt + 15) / 16) return;
     }
     const int n = lane & 15, s = lane >> 4;
     const int tok = 16 * st + n;               // this lane's token (B operand / output column)
-    const bool tok_ok = tok < cnt;
-    const int pair = start + (tok_ok ? tok : 0);
-    const int act = p.pair_act ? p.pair_act[pair] : pair;
+    const bool tok_ok = tok < cnt;             // slots past the last token hold no data;
+                                               // their columns are never stored
     const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
-    const int8_t *aq = p.aq_cm + (size_t)act * p.blocks * QK_K;
-    const float *ad = p.ad + (size_t)act * p.blocks;
+    const int8_t *aq = p.act_q + (size_t)sub * p.blocks * CHUNK_BLOCK_BYTES + n * 32 + 8 * s;
+    const float *ad = p.act_d + (size_t)sub * p.blocks * CHUNK_TOKENS + n;
 
     float sums[8][4];
 #pragma unroll
@@ -506,25 +540,28 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
         const uint4 q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
         const uint4 q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
         const uint32_t scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
+        const uint2 dw = *(const uint2 *)(seg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
+        const float adb = ad[(size_t)b * CHUNK_TOKENS];
+        long act[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            act[c] = *(const long *)(aq + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
         const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
-        // d of rows 4s..4s+3 (the D layout rows this lane holds) times this
-        // lane's token scale
-        const float adb = tok_ok ? ad[b] : 0.0f;
+        const FoldScales fs = fold_scales(scw);
+        // f16(d) of the lane's 4 rows (D rows 4s..4s+3) times the token's scale
         float dd[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-            dd[v] = f16_bits_to_f32(*(const uint16_t *)(seg + SEG_D + 2 * (4 * s + v))) * adb;
-        const int8_t *ab = aq + (size_t)b * QK_K + 8 * s;
+        dd[0] = f16_bits_to_f32((uint16_t)(dw.x & 0xFFFF)) * adb;
+        dd[1] = f16_bits_to_f32((uint16_t)(dw.x >> 16)) * adb;
+        dd[2] = f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)) * adb;
+        dd[3] = f16_bits_to_f32((uint16_t)(dw.y >> 16)) * adb;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            const long bw = unpack_codes(nib, hb, c);
             long a_lo, a_hi;
-            fold_digits((uint64_t)bw, scw, a_lo, a_hi);
-            const long bact = tok_ok ? *(const long *)(ab + 32 * c) : 0;
+            fold_digits((uint64_t)unpack_codes(nib, hb, c), fs, a_lo, a_hi);
             const v4i zero = {0, 0, 0, 0};
-            const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bact, zero, 0, 0, 0);
-            const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bact, zero, 0, 0, 0);
+            const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c], zero, 0, 0, 0);
+            const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c], zero, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int aux = dh[v] * 64 + dl[v];
@@ -533,7 +570,8 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
         }
     }
     if (tok_ok) {
-        const int orow = p.pair_out ? p.pair_out[pair] : pair;
+        const int pos = start + tok;
+        const int orow = p.pair_out ? p.pair_out[pos] : pos;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int row = t * TILE_ROWS + 4 * s + v;
@@ -662,10 +700,9 @@ int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
 
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
                           const int32_t *grp_start, const int32_t *grp_count,
-                          const int32_t *sub_start, const int32_t *pair_act,
-                          const int32_t *pair_out, const int8_t *aq_cm, const float *ad, float *y,
-                          int ldy, int rows, int blocks, int n_groups, int max_subtiles,
-                          hipStream_t st) {
+                          const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
+                          const float *act_d, float *y, int ldy, int rows, int blocks,
+                          int n_groups, int max_chunks, hipStream_t st) {
     BatchParams p;
     p.single_count = n_groups;  // only read when grp_expert == nullptr
     p.w = (const uint8_t *)w;
@@ -674,17 +711,16 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     p.grp_start = grp_start;
     p.grp_count = grp_count;
     p.sub_start = sub_start;
-    p.pair_act = pair_act;
     p.pair_out = pair_out;
-    p.aq_cm = aq_cm;
-    p.ad = ad;
+    p.act_q = act_q;
+    p.act_d = act_d;
     p.y = y;
     p.ldy = ldy;
     p.rows = rows;
     p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
     p.blocks = blocks;
     p.n_groups = n_groups;
-    const long items = (long)p.tiles * max_subtiles;
+    const long items = (long)p.tiles * max_chunks;
     if (items <= 0) return 0;
     hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -21,23 +21,37 @@
 namespace llamd {
 namespace {
 
-__global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm,
-                                                    float *d, int16_t *bsums, int nblocks) {
+__global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, float *d,
+                                                    int16_t *bsums, int nblocks) {
     const int lane = threadIdx.x & 63;
     const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const float4 xv = *(const float4 *)(x + (size_t)blk * QK_K + 4 * lane);
     const float v[4] = {xv.x, xv.y, xv.z, xv.w};
-    quantize_wave(v, lane, qs ? qs + (size_t)blk * QK_K : nullptr,
-                  qs_cm ? qs_cm + (size_t)blk * QK_K : nullptr, d + blk,
-                  bsums ? bsums + (size_t)blk * 16 : nullptr);
+    quantize_wave(v, lane, qs + (size_t)blk * QK_K, d + blk, bsums ? bsums + (size_t)blk * 16 : nullptr);
 }
 
+// Row r of x ([rows][blocks*256]) to the token-chunked layout, once for each
+// of its `fan` slots: slot_of[r * fan + k], or slot r when slot_of is null.
+__global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int rows, int blocks,
+                                                           const int32_t *slot_of, int fan,
+                                                           int8_t *cq, float *cd) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= rows * blocks) return;
+    const int r = item / blocks, b = item - r * blocks;
+    const float4 xv = *(const float4 *)(x + (size_t)item * QK_K + 4 * lane);
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    int q[4];
+    float dv;
+    quantize_wave_q(v, lane, q, dv);
+    for (int k = 0; k < fan; ++k)
+        store_chunk(q, dv, lane, cq, cd, slot_of ? slot_of[(size_t)r * fan + k] : r, b, blocks);
+}
 
 // act[i] = silu(gate[i]) * up[i], then Q8_K of act. Optionally stores act.
 __global__ __launch_bounds__(256) void swiglu_q8k(const float *gate, const float *up, float *act_out,
-                                                  int8_t *qs, int8_t *qs_cm, float *d,
-                                                  int16_t *bsums, int nblocks) {
+                                                  int8_t *qs, float *d, int16_t *bsums, int nblocks) {
     __shared__ uint64_t tab[32];
     const int lane = threadIdx.x & 63;
     const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -52,9 +66,30 @@ __global__ __launch_bounds__(256) void swiglu_q8k(const float *gate, const float
     v[2] = silu_ref(gv.z, tab) * uv.z;
     v[3] = silu_ref(gv.w, tab) * uv.w;
     if (act_out) *(float4 *)(act_out + o) = make_float4(v[0], v[1], v[2], v[3]);
-    quantize_wave(v, lane, qs ? qs + (size_t)blk * QK_K : nullptr,
-                  qs_cm ? qs_cm + (size_t)blk * QK_K : nullptr, d + blk,
-                  bsums ? bsums + (size_t)blk * 16 : nullptr);
+    quantize_wave(v, lane, qs + (size_t)blk * QK_K, d + blk, bsums ? bsums + (size_t)blk * 16 : nullptr);
+}
+
+// The same for rows of pairs, written to the token-chunked layout at
+// slot_of[row] (the expert-sorted position of each pair).
+__global__ __launch_bounds__(256) void swiglu_q8k_chunks(const float *gate, const float *up,
+                                                         int rows, int blocks,
+                                                         const int32_t *slot_of, int8_t *cq,
+                                                         float *cd) {
+    __shared__ uint64_t tab[32];
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= rows * blocks) return;
+    const int r = item / blocks, b = item - r * blocks;
+    const size_t o = (size_t)item * QK_K + 4 * lane;
+    const float4 gv = *(const float4 *)(gate + o);
+    const float4 uv = *(const float4 *)(up + o);
+    expf_ref_tab_fill(tab);
+    const float v[4] = {silu_ref(gv.x, tab) * uv.x, silu_ref(gv.y, tab) * uv.y,
+                        silu_ref(gv.z, tab) * uv.z, silu_ref(gv.w, tab) * uv.w};
+    int q[4];
+    float dv;
+    quantize_wave_q(v, lane, q, dv);
+    store_chunk(q, dv, lane, cq, cd, slot_of[r], b, blocks);
 }
 
 __global__ void silu_mul_f32(const float *gate, const float *up, float *out, int n) {
@@ -81,19 +116,35 @@ int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_q8k_quantize(const float *x, int8_t *qs, int8_t *qs_cm, float *d, int16_t *bsums,
-                        int nblocks, hipStream_t st) {
+int launch_q8k_quantize(const float *x, int8_t *qs, float *d, int16_t *bsums, int nblocks,
+                        hipStream_t st) {
     if (nblocks <= 0) return 0;
-    hipLaunchKernelGGL(q8k_quantize, dim3((nblocks + 3) / 4), dim3(256), 0, st, x, qs, qs_cm, d,
-                       bsums, nblocks);
+    hipLaunchKernelGGL(q8k_quantize, dim3((nblocks + 3) / 4), dim3(256), 0, st, x, qs, d, bsums,
+                       nblocks);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs,
-                      int8_t *qs_cm, float *d, int16_t *bsums, int nblocks, hipStream_t st) {
+int launch_q8k_quantize_chunks(const float *x, int rows, int blocks, const int32_t *slot_of,
+                               int fan, int8_t *cq, float *cd, hipStream_t st) {
+    if (rows <= 0 || blocks <= 0) return 0;
+    hipLaunchKernelGGL(q8k_quantize_chunks, dim3((rows * blocks + 3) / 4), dim3(256), 0, st, x,
+                       rows, blocks, slot_of, fan, cq, cd);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs, float *d,
+                      int16_t *bsums, int nblocks, hipStream_t st) {
     if (nblocks <= 0) return 0;
     hipLaunchKernelGGL(swiglu_q8k, dim3((nblocks + 3) / 4), dim3(256), 0, st, gate, up, act_out,
-                       qs, qs_cm, d, bsums, nblocks);
+                       qs, d, bsums, nblocks);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_swiglu_q8k_chunks(const float *gate, const float *up, int rows, int blocks,
+                             const int32_t *slot_of, int8_t *cq, float *cd, hipStream_t st) {
+    if (rows <= 0 || blocks <= 0) return 0;
+    hipLaunchKernelGGL(swiglu_q8k_chunks, dim3((rows * blocks + 3) / 4), dim3(256), 0, st, gate,
+                       up, rows, blocks, slot_of, cq, cd);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

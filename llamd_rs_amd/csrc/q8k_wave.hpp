@@ -1,7 +1,8 @@
 // q8k_wave.hpp -- one wave quantizes one 256-element block to Q8_K,
 // bit-exactly as quantize_q8_k (crates/llamd-quant/src/dot.rs:89-128); see
 // q8k.hip for the derivation. Shared by the quantize kernels and the fused
-// router kernel.
+// router kernel, with writers for the reference's layout and for the
+// token-chunked layout of the batched matvec.
 #pragma once
 
 #include "common.hpp"
@@ -9,11 +10,9 @@
 
 namespace llamd {
 
-// qs: natural order (the reference's BlockQ8K.qs). qs_cm (optional): the same
-// quants in class-major order, byte 32 * (e % 8) + e / 8 for element e, which
-// is what the batched kernel's MFMA operand loads want.
-__device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t *qs, int8_t *qs_cm,
-                                              float *d, int16_t *bsums) {
+// Q8_K of the wave's 256 values (4 per lane, elements 4*lane .. 4*lane+3):
+// this lane's 4 quants and the block scale d (on every lane).
+__device__ __forceinline__ void quantize_wave_q(const float v[4], int lane, int q[4], float &dv) {
     float amax = 0.0f, mx = 0.0f;
     int idx = 0x7FFFFFFF;
 #pragma unroll
@@ -28,8 +27,6 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
     amax = best;
     mx = win == 0x7FFFFFFF ? 0.0f
                            : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), win >> 2));
-    int q[4];
-    float dv;
     if (amax == 0.0f) {
         q[0] = q[1] = q[2] = q[3] = 0;
         dv = 0.0f;
@@ -42,16 +39,14 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
         }
         dv = 1.0f / iscale;
     }
+}
+
+// The reference's BlockQ8K arrays: qs in natural order, d, bsums (optional).
+__device__ __forceinline__ void store_q8k(const int q[4], float dv, int lane, int8_t *qs, float *d,
+                                          int16_t *bsums) {
     const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                             ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
     if (qs) *(uint32_t *)(qs + 4 * lane) = packed;
-    if (qs_cm) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * lane + i;
-            qs_cm[32 * (e & 7) + (e >> 3)] = (int8_t)q[i];
-        }
-    }
     int gs = q[0] + q[1] + q[2] + q[3];
     gs += dpp<DPP_XOR1>(0, gs);
     gs += dpp<DPP_XOR2>(0, gs);
@@ -59,6 +54,34 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
     if (lane == 0) *d = dv;
 }
 
+__device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t *qs, float *d,
+                                              int16_t *bsums) {
+    int q[4];
+    float dv;
+    quantize_wave_q(v, lane, q, dv);
+    store_q8k(q, dv, lane, qs, d, bsums);
+}
+
+// ---- token-chunked activations (the batched matvec's operand layout) -----
+// 16 token slots form a chunk; block b of chunk k occupies 4 KiB at
+// (k * blocks + b) * 4096, holding class plane c (weights e with e % 8 == c)
+// at c * 512, token n of the chunk at n * 32 within it, and weight 8 m + c
+// at byte m. One MFMA operand load of a class is then one contiguous 512-B
+// read for the whole wave. The scales sit at d[(k * blocks + b) * 16 + n].
+constexpr int CHUNK_TOKENS = 16;
+constexpr int CHUNK_BLOCK_BYTES = 8 * 512;
+
+__device__ __forceinline__ void store_chunk(const int q[4], float dv, int lane, int8_t *cq, float *cd,
+                                            int slot, int b, int blocks) {
+    const size_t base = ((size_t)(slot / CHUNK_TOKENS) * blocks + b);
+    int8_t *dst = cq + base * CHUNK_BLOCK_BYTES + (slot % CHUNK_TOKENS) * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = 4 * lane + i;
+        dst[(e & 7) * 512 + (e >> 3)] = (int8_t)q[i];
+    }
+    if (lane == 0) cd[base * CHUNK_TOKENS + slot % CHUNK_TOKENS] = dv;
+}
 
 // silu(v) = v / (1 + exp(-v)) with the reference's f32 expf (model.rs silu).
 __device__ __forceinline__ float silu_ref(float v, const uint64_t *tab) {
@@ -66,7 +89,7 @@ __device__ __forceinline__ float silu_ref(float v, const uint64_t *tab) {
 }
 
 __device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, int8_t *qs, float *d) {
-    quantize_wave(v, lane, qs, nullptr, d, nullptr);
+    quantize_wave(v, lane, qs, d, nullptr);
 }
 
 }  // namespace llamd
