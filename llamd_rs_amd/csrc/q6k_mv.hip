@@ -555,16 +555,27 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
         dd[1] = f16_bits_to_f32((uint16_t)(dw.x >> 16)) * adb;
         dd[2] = f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)) * adb;
         dd[3] = f16_bits_to_f32((uint16_t)(dw.y >> 16)) * adb;
+        // software-pipelined by one class: the MFMAs of class c+1 are issued
+        // before the epilogue of class c reads its results
+        const v4i zero = {0, 0, 0, 0};
+        v4i dh[2], dl[2];
+        {
+            long a_lo, a_hi;
+            fold_digits((uint64_t)unpack_codes(nib, hb, 0), fs, a_lo, a_hi);
+            dh[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[0], zero, 0, 0, 0);
+            dl[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[0], zero, 0, 0, 0);
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            long a_lo, a_hi;
-            fold_digits((uint64_t)unpack_codes(nib, hb, c), fs, a_lo, a_hi);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c], zero, 0, 0, 0);
-            const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c], zero, 0, 0, 0);
+            if (c + 1 < 8) {
+                long a_lo, a_hi;
+                fold_digits((uint64_t)unpack_codes(nib, hb, c + 1), fs, a_lo, a_hi);
+                dh[(c + 1) & 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c + 1], zero, 0, 0, 0);
+                dl[(c + 1) & 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c + 1], zero, 0, 0, 0);
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int aux = dh[v] * 64 + dl[v];
+                const int aux = dh[c & 1][v] * 64 + dl[c & 1][v];
                 sums[c][v] = sums[c][v] + dd[v] * (float)aux;
             }
         }
