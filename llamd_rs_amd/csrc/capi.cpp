@@ -849,7 +849,8 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
     if (max_seq <= 0) { fail("lmhead_create: max_seq must be positive"); return nullptr; }
     LmHead *l = new LmHead();
     l->w = d_w; l->rows = rows; l->blocks = blocks; l->cap = max_seq;
-    const int parts = argmax_parts(rows);
+    // per-tile arg-max candidates written by the matvec epilogue
+    const int parts = (rows + 15) / 16;
     const size_t nq = (size_t)max_seq * blocks * QK;
     if (!l->xq.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
         !l->cq.alloc(chunk_q_bytes(max_seq, blocks)) || !l->cd.alloc(chunk_d_bytes(max_seq, blocks)) ||
@@ -873,17 +874,23 @@ int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logit
         return fail("lmhead_forward: bad arguments");
     hipStream_t st = stream();
     int rc = 0;
+    // the matvec epilogues leave one arg-max candidate per 16-row tile
+    const int tiles = (l->rows + 15) / 16;
     if (nseq == 1) {
         rc |= launch_q8k_quantize(d_x, l->xq.as<int8_t>(), l->xd.as<float>(), nullptr, l->blocks, st);
         rc |= launch_q6k_mv_b1(l->w, 0, nullptr, l->xq.as<int8_t>(), l->xd.as<float>(), d_logits,
-                               l->rows, l->blocks, 1, 0, st);
+                               l->rows, l->blocks, 1, 0, st, nullptr, l->pv.as<float>(),
+                               l->pi.as<int>());
     } else {
         rc |= launch_q8k_quantize_chunks(d_x, nseq, l->blocks, nullptr, 1, l->cq.as<int8_t>(),
                                          l->cd.as<float>(), st);
-        rc |= batched_dev(l->w, l->cq.as<int8_t>(), l->cd.as<float>(), d_logits, l->blocks, l->rows,
-                          nseq);
+        rc |= launch_q6k_mv_batched(l->w, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                    l->cq.as<int8_t>(), l->cd.as<float>(), d_logits, l->rows,
+                                    l->rows, l->blocks, nseq, (nseq + CHUNK - 1) / CHUNK, st,
+                                    l->pv.as<float>(), l->pi.as<int>());
     }
-    rc |= launch_argmax(d_logits, l->rows, l->rows, nseq, l->pv.as<float>(), l->pi.as<int>(), d_ids, st);
+    rc |= launch_argmax_final(d_logits, l->rows, nseq, l->pv.as<float>(), l->pi.as<int>(), tiles,
+                              d_ids, st);
     return rc ? fail("lmhead_forward: launch failed") : 0;
 }
 

@@ -18,7 +18,8 @@ extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4 (0: a
 // w_b (gate and up in one launch).
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st, const void *w_b = nullptr);
+                     hipStream_t st, const void *w_b = nullptr, float *amax_v = nullptr,
+                     int *amax_i = nullptr);
 // Down projection of n_slots routed experts (activation e for slot e) and the
 // routing-weighted combine (+ residual) into out, one workgroup per 16 rows.
 // One launch over up to three matrices sharing the activation (Q, K, V):
@@ -50,7 +51,8 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *grp_start, const int32_t *grp_count,
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
-                          int n_groups, int max_chunks, hipStream_t st);
+                          int n_groups, int max_chunks, hipStream_t st, float *amax_v = nullptr,
+                          int *amax_i = nullptr);
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 
 // q8k.hip
@@ -92,6 +94,10 @@ int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
                        int n_used, int n_embd, int n_tok, hipStream_t st);
 int argmax_parts(int n);
+// Reduce nparts (value, index) candidates per sequence ([nseq][nparts]) to the
+// reference's arg-max of row x[seq * ld ..] (index 0 wins if x[0] is NaN).
+int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
+                        int nparts, int32_t *out, hipStream_t st);
 int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, int32_t *out,
                   hipStream_t st);
 int launch_q8_0_mv(const void *planar, const float *x, float *y, int rows, int k, hipStream_t st);

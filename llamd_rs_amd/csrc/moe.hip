@@ -155,16 +155,35 @@ __global__ __launch_bounds__(256) void argmax_partial(const float *x, int n, int
     }
 }
 
-__global__ __launch_bounds__(64) void argmax_final(const float *x, int ld, const float *pv,
-                                                   const int *pi, int nparts, int32_t *out) {
+__global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, const float *pv,
+                                                     const int *pi, int nparts, int32_t *out) {
     const int seq = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = lane; i < nparts; i += 64)
-        better(bv, bi, pv[(size_t)seq * nparts + i], pi[(size_t)seq * nparts + i]);
+    // eight independent candidate loads in flight per thread before reducing
+    constexpr int U = 8;
+    const float *sv_in = pv + (size_t)seq * nparts;
+    const int *si_in = pi + (size_t)seq * nparts;
+    for (int base = threadIdx.x; base < nparts; base += U * blockDim.x) {
+        float v[U];
+        int id[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + u * blockDim.x;
+            v[u] = i < nparts ? sv_in[i] : -INFINITY;
+            id[u] = i < nparts ? si_in[i] : 0x7FFFFFFF;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) argmax_step(bv, bi, v[u], id[u]);
+    }
     wave_argmax(bv, bi, -INFINITY);
-    if (lane == 0) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(bv, bi, sv[w], si[w]);
         // the reference's incumbent is index 0: a NaN there is never beaten,
         // and when nothing beats -inf the answer stays 0
         const float v0 = x[(size_t)seq * ld];
@@ -280,6 +299,12 @@ int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, i
     const int parts = argmax_parts(n);
     hipLaunchKernelGGL(argmax_partial, dim3(parts, nseq), dim3(256), 0, st, x, n, ld, pv, pi);
     hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(64), 0, st, x, ld, pv, pi, parts, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
+                        int nparts, int32_t *out, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(1024), 0, st, x, ld, pv, pi, nparts, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

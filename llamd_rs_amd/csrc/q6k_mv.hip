@@ -64,6 +64,9 @@ struct MvParams {
     int32_t *ids_out;
     float *w_out;
     int *stats;               // [2] calls (+1 each, both counters)
+    // optional per-tile arg-max candidates (one segment): [n_slots][tiles]
+    float *amax_v;
+    int *amax_i;
 };
 
 // 6-bit codes of class c for this lane's 8 weights (B operand, K = 8s..8s+7)
@@ -299,13 +302,24 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
         cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
         cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
     }
-    if (s == 0) {
-        const int row = t * TILE_ROWS + n;
-        if (row < sgm.rows) {
-            float tot = -0.0f;
+    const int row = t * TILE_ROWS + n;
+    float tot = -0.0f;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) tot = tot + cls[c];
-            sgm.y[(size_t)slot * sgm.rows + row] = tot;
+    for (int c = 0; c < 8; ++c) tot = tot + cls[c];
+    if (s == 0 && row < sgm.rows) sgm.y[(size_t)slot * sgm.rows + row] = tot;
+    if (p.amax_v) {
+        // this tile's arg-max candidate for the LM head (argmax_final reduces
+        // the tiles): the largest non-NaN logit, lowest row on ties
+        const bool ok = s == 0 && row < sgm.rows && !isnan(tot);
+        float bv = ok ? tot : -INFINITY;
+        int bi = ok ? row : 0x7FFFFFFF;
+        argmax_step(bv, bi, dpp<DPP_XOR1>(-INFINITY, bv), dpp<DPP_XOR1>(0x7FFFFFFF, bi));
+        argmax_step(bv, bi, dpp<DPP_XOR2>(-INFINITY, bv), dpp<DPP_XOR2>(0x7FFFFFFF, bi));
+        argmax_step(bv, bi, dpp<DPP_HALF_MIRROR>(-INFINITY, bv), dpp<DPP_HALF_MIRROR>(0x7FFFFFFF, bi));
+        argmax_step(bv, bi, dpp<DPP_MIRROR>(-INFINITY, bv), dpp<DPP_MIRROR>(0x7FFFFFFF, bi));
+        if (lane == 0) {
+            p.amax_v[(size_t)slot * sgm.tiles + t] = bv;
+            p.amax_i[(size_t)slot * sgm.tiles + t] = bi;
         }
     }
 }
@@ -443,6 +457,8 @@ struct BatchParams {
     const int8_t *act_q;         // token-chunked Q8_K quants (q8k_wave.hpp)
     const float *act_d;          // their scales
     float *y;                    // y[pair_out * ldy + row]
+    float *amax_v;               // optional per-(token, tile) arg-max candidates
+    int *amax_i;                 //   [token][tiles] (single group only)
     int ldy, rows, tiles, blocks, n_groups;
     int single_count;            // grp_expert == nullptr: one group, expert 0, this many tokens
 };
@@ -580,6 +596,8 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
             }
         }
     }
+    float bv = -INFINITY;  // arg-max candidate of this lane's rows (lowest row on ties)
+    int bi = 0x7FFFFFFF;
     if (tok_ok) {
         const int pos = start + tok;
         const int orow = p.pair_out ? p.pair_out[pos] : pos;
@@ -591,7 +609,17 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
 #pragma unroll
                 for (int c = 0; c < 8; ++c) tot = tot + sums[c][v];
                 p.y[(size_t)orow * p.ldy + row] = tot;
+                if (!isnan(tot)) argmax_step(bv, bi, tot, row);
             }
+        }
+    }
+    if (p.amax_v) {
+        // combine the 4 lanes (s = 0..3) of each token: lanes n, n+16, n+32, n+48
+        argmax_step(bv, bi, __shfl_xor(bv, 16, WAVE), __shfl_xor(bi, 16, WAVE));
+        argmax_step(bv, bi, __shfl_xor(bv, 32, WAVE), __shfl_xor(bi, 32, WAVE));
+        if (s == 0 && tok_ok) {
+            p.amax_v[(size_t)tok * p.tiles + t] = bv;
+            p.amax_i[(size_t)tok * p.tiles + t] = bi;
         }
     }
 }
@@ -642,8 +670,11 @@ int launch_b1(const MvParams &p, hipStream_t st) {
 
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st, const void *w_b) {
+                     hipStream_t st, const void *w_b, float *amax_v, int *amax_i) {
+    if (amax_v && w_b) return -1;
     MvParams p = {};
+    p.amax_v = amax_v;
+    p.amax_i = amax_i;
     // with a second weight, its outputs follow the first's: y = [w | w_b]
     const void *ws[2] = {w, w_b};
     float *ys[2] = {y, y + (size_t)n_slots * rows};
@@ -713,7 +744,9 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *grp_start, const int32_t *grp_count,
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
-                          int n_groups, int max_chunks, hipStream_t st) {
+                          int n_groups, int max_chunks, hipStream_t st, float *amax_v,
+                          int *amax_i) {
+    if (amax_v && grp_expert) return -1;
     BatchParams p;
     p.single_count = n_groups;  // only read when grp_expert == nullptr
     p.w = (const uint8_t *)w;
@@ -726,6 +759,8 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     p.act_q = act_q;
     p.act_d = act_d;
     p.y = y;
+    p.amax_v = amax_v;
+    p.amax_i = amax_i;
     p.ldy = ldy;
     p.rows = rows;
     p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;

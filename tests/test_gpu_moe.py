@@ -195,3 +195,34 @@ def test_lm_head_b16_argmax_exact(gpu, lm_head):
     # (identical bits) -- and of the CPU logits for the three checked above
     for s in range(16):
         assert ids[s] == O.argmax(logits[s]), s
+
+
+@pytest.mark.parametrize("nseq", [1, 16])
+def test_lm_head_argmax_ties_and_nan(gpu, nseq):               # device_forward.rs:23-37
+    """The per-tile arg-max candidates of the matvec epilogue, reduced: a
+    duplicated winning row loses to its lower-index copy across tiles, a NaN
+    logit never wins, and a NaN at index 0 makes the answer 0."""
+    rows, k = 64, 256
+    x = H.sample(nseq * k, 5).reshape(nseq, k)
+    w = H.weights(rows, 1, 17).reshape(rows, 210).copy()
+    logits = np.stack([O.matvec_q6k(w.reshape(-1), rows, k, x[s]) for s in range(nseq)])
+    m = int(np.argmax(logits[0]))
+    w[37] = w[m]                        # a copy in a later tile
+    w[3 if m > 3 else 60] = w[m]        # and one in another tile
+    w[50, 208:210] = (0x00, 0x7E)       # f16 NaN scale: logit 50 is NaN
+    for case in ("ties", "nan0"):
+        if case == "nan0":
+            w[0, 208:210] = (0x00, 0x7E)
+        dw = gpu.DeviceWeights.upload(w.reshape(-1), rows, 1)
+        head = gpu.LmHead(dw, max_seq=16)
+        got_logits, ids = head.forward(x)
+        for s in range(nseq):
+            want = O.matvec_q6k(w.reshape(-1), rows, k, x[s])
+            assert bits_equal(got_logits[s], want), (case, s)
+            assert ids[s] == O.argmax(want), (case, s, ids[s], O.argmax(want))
+        if case == "ties":
+            assert ids[0] == min(m, 3 if m > 3 else 60)
+        else:
+            assert list(ids) == [0] * nseq
+        head.close()
+        dw.close()
