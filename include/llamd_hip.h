@@ -175,6 +175,21 @@ void llamd_fwd_silu_mul(const float *gate, const float *up, float *out, int n);
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs);
 /* llamd_forward.hip:856-861 */
+/* llamd_forward.hip:759-763: out = rms_norm(x) * w over one row of n.
+ * Bit-identical to CpuBackend::rms_norm + mul (llamd-cpu/src/lib.rs:55-75,
+ * 112-113): in-order f32 sum of squares, correctly rounded sqrt and divide.
+ * n <= 8192. */
+void llamd_fwd_rms_norm_mul(const float *d_x, const float *d_w, float *d_out, int n, float eps);
+/* llamd_forward.hip:765-770: the same per head (QK-norm, layer.rs:62-79):
+ * n_head rows of hd, each multiplied by w[0..hd). */
+void llamd_fwd_head_rms_norm_mul(const float *d_x, const float *d_w, float *d_out, int n_head,
+                                 int hd, float eps);
+/* llamd_forward.hip:845-855: rms_norm(x) * w, then Q8_K of the result (qs,
+ * d in the reference's layout) for the Q/K/V matvecs; out (the f32 result)
+ * and inv_scratch (the row's scale) are written when non-NULL. n % 256 == 0,
+ * n <= 8192. */
+void llamd_fwd_rms_norm_quant(const float *d_x, const float *d_w, float *d_out, int8_t *d_qs,
+                              float *d_d, float *d_inv_scratch, int n, float eps);
 /* llamd_forward.hip:813-817: out = sum_e w[e] * down[e] (no residual). */
 void llamd_fwd_moe_combine(const float *d_down, const float *d_weights, float *d_out, int n_used,
                            int n_embd);

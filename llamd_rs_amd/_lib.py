@@ -79,6 +79,9 @@ SIGNATURES = {
     "llamd_fwd_matvec_grouped_x2_splitk": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "llamd_fwd_matvec_grouped_pa_splitk": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "llamd_fwd_moe_combine": (None, [vp, vp, vp, i32, i32]),
+    "llamd_fwd_rms_norm_mul": (None, [vp, vp, vp, i32, f]),
+    "llamd_fwd_head_rms_norm_mul": (None, [vp, vp, vp, i32, i32, f]),
+    "llamd_fwd_rms_norm_quant": (None, [vp, vp, vp, vp, vp, vp, i32, f]),
     "llamd_fwd_quantize": (None, [vp, vp, vp, i32]),
     "llamd_fwd_silu_mul": (None, [vp, vp, vp, i32]),
     "llamd_fwd_router": (None, [vp, i32, i32, vp, vp, vp]),

@@ -588,6 +588,23 @@ void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, c
     llamd_fwd_matvec_grouped_pa(d_w, d_ids, d_aq, d_ad, d_out, blocks, rows, n_used);
 }
 
+void llamd_fwd_rms_norm_mul(const float *x, const float *w, float *out, int n, float eps) {
+    if (launch_rms_norm_mul(x, w, out, 1, n, n, eps, stream()))
+        fail("rms_norm_mul: n must be in 1..8192");
+}
+
+void llamd_fwd_head_rms_norm_mul(const float *x, const float *w, float *out, int n_head, int hd,
+                                 float eps) {
+    if (launch_rms_norm_mul(x, w, out, n_head, hd, hd, eps, stream()))
+        fail("head_rms_norm_mul: need n_head > 0 and hd in 1..8192");
+}
+
+void llamd_fwd_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
+                              float *inv_scratch, int n, float eps) {
+    if (launch_rms_norm_quant(x, w, out, qs, d, inv_scratch, n, eps, stream()))
+        fail("rms_norm_quant: n must be a multiple of 256, at most 8192");
+}
+
 void llamd_fwd_moe_combine(const float *d, const float *weights, float *out, int n_used,
                            int n_embd) {
     launch_moe_combine(d, weights, nullptr, out, n_used, n_embd, 1, stream());

@@ -36,6 +36,28 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)v;
 }
 
+// Correctly rounded f32 square root (what Rust's f32::sqrt returns). The
+// hardware estimate is within an ulp or so; the result is then moved to the
+// neighbour whose rounding interval holds sqrt(t), decided exactly in double:
+// a midpoint between two floats has at most 25 significant bits, so its
+// square is exact in double and t < m^2 is an exact comparison (t is never
+// equal to the square of such a midpoint).
+__device__ __forceinline__ float sqrt_rn(float t) {
+    float s = __builtin_sqrtf(t);
+    if (!(t > 0.0f) || __builtin_isinf(t)) return s;  // 0, -0, NaN, negatives, +inf
+    const double td = (double)t;
+    for (int k = 0; k < 4; ++k) {
+        const float dn = __uint_as_float(__float_as_uint(s) - 1u);
+        const double lo = ((double)s + (double)dn) * 0.5;
+        if (s > 0.0f && td < lo * lo) { s = dn; continue; }
+        const float up = __uint_as_float(__float_as_uint(s) + 1u);
+        const double hi = ((double)s + (double)up) * 0.5;
+        if (td > hi * hi) { s = up; continue; }
+        break;
+    }
+    return s;
+}
+
 __device__ __forceinline__ int shfl_xor_i(int v, int mask) { return __shfl_xor(v, mask, WAVE); }
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, WAVE); }
 __device__ __forceinline__ double shfl_xor_d(double v, int mask) { return __shfl_xor(v, mask, WAVE); }

@@ -76,6 +76,14 @@ int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
                      hipStream_t st);
 int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipStream_t st);
 
+// norm.hip: CpuBackend::rms_norm (+ weight), bit-exact. rows of n; the
+// weight repeats every w_len elements (per-head QK norm: w_len = n = hd).
+int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
+                        float eps, hipStream_t st);
+// rms_norm(x) * w, then Q8_K (qs, d natural layout); out and inv_out optional.
+int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
+                          float *inv_out, int n, float eps, hipStream_t st);
+
 // moe.hip
 // The reference's router logits (sequential f32 fold per expert) and, in the
 // same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.

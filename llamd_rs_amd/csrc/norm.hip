@@ -1,0 +1,126 @@
+// norm.hip -- RMSNorm (+ weight, + Q8_K) in front of the attention
+// projections, bit-identical to the reference CPU path.
+//
+// CpuBackend::rms_norm (crates/llamd-cpu/src/lib.rs:55-75) sums the squares
+// of a row in f32, IN ORDER, from 0.0, then scale = 1 / sqrt(sum / n + eps)
+// and out = x * scale; the layer then multiplies by the norm weight as a
+// separate tensor op (be.mul, layer.rs:101-104 and per_head_rms_norm,
+// layer.rs:62-79). The in-order sum is a dependency chain: all lanes form
+// the rounded squares into LDS at once, and one lane adds them in order (the
+// same scheme as the router fold). sqrt and the divide are correctly rounded
+// (sqrt_rn, __fdiv_rn), as Rust's f32 sqrt and `/` are.
+//
+// The fused variant then forms (x * scale) * w for each 256-element block and
+// quantizes it to Q8_K with one wave per block, writing the reference's
+// BlockQ8K arrays for the Q / K / V matvecs.
+#include "common.hpp"
+#include "launch.hpp"
+#include "q8k_wave.hpp"
+
+namespace llamd {
+namespace {
+
+constexpr int NORM_MAX = 8192;  // elements of one row held in LDS
+
+// The sequential sum of squares of src[0..n) by lane 0 of the calling wave,
+// from squares parked in sq[] (all of the wave's lanes write them first).
+// Returns scale on every lane of the wave.
+__device__ float row_scale_wave(const float *src, int n, float eps, float *sq) {
+    const int lane = threadIdx.x & 63;
+    for (int i = lane; i < n; i += WAVE) {
+        const float v = src[i];
+        sq[i] = v * v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float scale = 0.0f;
+    if (lane == 0) {
+        float sum = 0.0f;
+        int i = 0;
+        for (; i + 32 <= n; i += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = *(const float4 *)(sq + i + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                sum = sum + v[j].x;
+                sum = sum + v[j].y;
+                sum = sum + v[j].z;
+                sum = sum + v[j].w;
+            }
+        }
+        for (; i < n; ++i) sum = sum + sq[i];
+        const float mean = __fdiv_rn(sum, (float)n);
+        scale = __fdiv_rn(1.0f, sqrt_rn(mean + eps));
+    }
+    return __shfl(scale, 0, WAVE);
+}
+
+// out[r][i] = (x[r][i] * scale_r) * w[i % w_len], one workgroup per row
+// (rows = heads for the per-head QK norm). w may be null (no multiply).
+__global__ __launch_bounds__(256) void rms_norm_mul(const float *x, const float *w, float *out,
+                                                    int n, int w_len, float eps) {
+    __shared__ __align__(16) float sq[NORM_MAX];
+    __shared__ float sc;
+    const int r = blockIdx.x;
+    const float *src = x + (size_t)r * n;
+    if (threadIdx.x < WAVE) {
+        const float s = row_scale_wave(src, n, eps, sq);
+        if (threadIdx.x == 0) sc = s;
+    }
+    __syncthreads();
+    const float scale = sc;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = src[i] * scale;
+        out[(size_t)r * n + i] = w ? v * w[i % w_len] : v;
+    }
+}
+
+// One row of n = 256 * blocks: wave 0 finds the scale, then wave k forms
+// block k (and k + waves, ...) of (x * scale) * w and quantizes it.
+__global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const float *w, float *out,
+                                                       int8_t *qs, float *d, float *inv_out,
+                                                       int n, float eps) {
+    __shared__ __align__(16) float sq[NORM_MAX];
+    __shared__ float sc;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave == 0) {
+        const float s = row_scale_wave(x, n, eps, sq);
+        if (lane == 0) {
+            sc = s;
+            if (inv_out) *inv_out = s;
+        }
+    }
+    __syncthreads();
+    const float scale = sc;
+    const int blocks = n / QK_K, waves = blockDim.x >> 6;
+    for (int b = wave; b < blocks; b += waves) {
+        const size_t o = (size_t)b * QK_K + 4 * lane;
+        const float4 xv = *(const float4 *)(x + o);
+        const float4 wv = *(const float4 *)(w + o);
+        const float v[4] = {(xv.x * scale) * wv.x, (xv.y * scale) * wv.y, (xv.z * scale) * wv.z,
+                            (xv.w * scale) * wv.w};
+        if (out) *(float4 *)(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+        quantize_wave(v, lane, qs + (size_t)b * QK_K, d + b, nullptr);
+    }
+}
+
+}  // namespace
+
+int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
+                        float eps, hipStream_t st) {
+    if (rows <= 0 || n <= 0 || n > NORM_MAX || (w && w_len <= 0)) return -1;
+    hipLaunchKernelGGL(rms_norm_mul, dim3(rows), dim3(256), 0, st, x, w, out, n, w_len, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
+                          float *inv_out, int n, float eps, hipStream_t st) {
+    if (n <= 0 || n % QK_K || n > NORM_MAX || !w) return -1;
+    const int waves = n / QK_K < 16 ? n / QK_K : 16;
+    hipLaunchKernelGGL(rms_norm_quant, dim3(1), dim3(64 * waves), 0, st, x, w, out, qs, d, inv_out,
+                       n, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace llamd

@@ -17,6 +17,8 @@
  *   orc_matvec_*          composition of the above + float64 bound
  *   orc_route             reference known answers (moe.rs:120-246)
  *   orc_silu/mul/softmax  closed form (float64) within 1 ulp
+ *   orc_rms_norm          reference known answers (llamd-cpu lib.rs:237-259),
+ *                         order probes of the sequential sum, float64 bound
  *   orc_moe_ffn/_layer    composition; float64 restatement bound
  *   orc_argmax            closed form incl. ties
  *   orc_moe_ffn_tokens    composition of orc_moe_ffn per token
@@ -318,6 +320,24 @@ void orc_silu(const float *x, float *y, size_t n) {
     for (size_t i = 0; i < n; ++i) {
         float v = x[i];
         y[i] = v / (1.0f + expf(-v));
+    }
+}
+
+/* CpuBackend::rms_norm: crates/llamd-cpu/src/lib.rs:55-75. Per row: the sum
+ * of squares in f32, in order, from 0.0; scale = 1 / sqrt(sum / n + eps);
+ * out = x * scale. */
+void orc_rms_norm(const float *x, int rows, int n, float eps, float *out) {
+    for (int r = 0; r < rows; ++r) {
+        const float *src = x + (size_t)r * n;
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const float sq = src[i] * src[i];
+            sum = sum + sq;
+        }
+        const float mean = sum / (float)n;
+        const float t = mean + eps;
+        const float scale = 1.0f / sqrtf(t);
+        for (int i = 0; i < n; ++i) out[(size_t)r * n + i] = src[i] * scale;
     }
 }
 

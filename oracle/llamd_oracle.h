@@ -85,6 +85,7 @@ int orc_route(const float *logits, size_t n_expert, size_t n_used, uint32_t *exp
 
 /* CpuBackend::silu / mul / softmax (crates/llamd-cpu/src/lib.rs:81-113). */
 void orc_silu(const float *x, float *y, size_t n);
+void orc_rms_norm(const float *x, int rows, int n, float eps, float *out);
 void orc_mul(const float *a, const float *b, float *y, size_t n);
 void orc_softmax(const float *x, float *y, size_t n);
 

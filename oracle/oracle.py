@@ -46,6 +46,7 @@ def _lib():
             "orc_matvec_q8_0": (C.c_int, [vp, sz, sz, vp, vp]),
             "orc_route": (C.c_int, [vp, sz, sz, vp, vp, vp, vp]),
             "orc_silu": (None, [vp, vp, sz]),
+            "orc_rms_norm": (None, [vp, C.c_int, C.c_int, C.c_float, vp]),
             "orc_mul": (None, [vp, vp, vp, sz]),
             "orc_softmax": (None, [vp, vp, sz]),
             "orc_matvec_expert_q6k": (C.c_int, [vp, sz, sz, sz, sz, vp, vp]),
@@ -168,6 +169,16 @@ def silu(x) -> np.ndarray:
     y = np.empty_like(x)
     _lib().orc_silu(_p(x), _p(y), x.size)
     return y
+
+
+def rms_norm(x, rows: int, n: int, eps: float) -> np.ndarray:
+    """CpuBackend::rms_norm (llamd-cpu/src/lib.rs:55-75) over `rows` rows of n."""
+    x = _f32(x)
+    if x.size != rows * n:
+        raise ValueError("x must be [rows, n]")
+    out = np.empty(rows * n, np.float32)
+    _lib().orc_rms_norm(_p(x), rows, n, eps, _p(out))
+    return out
 
 
 def mul(a, b) -> np.ndarray:
