@@ -29,6 +29,9 @@ constexpr int SEGB = 16 * 210;
 thread_local char g_err[512] = "";
 std::mutex g_mu;             // serialises host-in/host-out calls and the registry
 hipStream_t g_stream = nullptr;
+// 1: gate/up + SwiGLU in one launch and Q8_K in the down kernel (n_ff <= 2048);
+// 0: separate SwiGLU + Q8_K launch.
+int g_tune_moe_fused = 1;
 
 int fail(const char *fmt, ...) {
     va_list ap;
@@ -128,6 +131,11 @@ const char *llamd_hip_last_error(void) { return g_err; }
 
 int llamd_hip_tune(const char *key, int value) {
     if (!key) return fail("tune: null key");
+    if (!strcmp(key, "moe_fused")) {
+        const int prev = g_tune_moe_fused;
+        g_tune_moe_fused = value ? 1 : 0;
+        return prev;
+    }
     if (!strcmp(key, "mv_ks")) {
         const int prev = g_tune_mv_ks;
         g_tune_mv_ks = value;
@@ -634,6 +642,7 @@ void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, 
 // ---- MoE layer -------------------------------------------------------------------
 namespace {
 
+
 struct MoeLayer {
     int n_embd, n_ff, n_expert, n_used;
     int be, bf;  // 256-blocks per row of gate/up (n_embd) and down (n_ff)
@@ -721,20 +730,34 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
     rl.xd = m->xd.as<float>();
     rl.xblocks = m->be;
     rc |= launch_router(rl, st);
-    // 2. route (prologue) + gate and up of the routed experts in one launch:
-    //    g holds [gate | up] x n_used x n_ff
-    rc |= launch_q6k_mv_routed(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
-                               m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
-                               m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
-                               m->g.as<float>(), m->n_ff, m->be, st);
-    // 3. SwiGLU + Q8_K of the activations
-    rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
-                            nullptr, m->aq.as<int8_t>(), m->ad.as<float>(), nullptr,
-                            m->n_used * m->bf, st);
-    // 4. down projection of the routed experts + weighted combine + residual
-    rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
-                                  m->ad.as<float>(), m->weights.as<float>(), d_res, d_out,
-                                  m->n_embd, m->bf, m->n_used, st);
+    if (g_tune_moe_fused && m->bf <= 8) {
+        // 2. route (prologue) + gate and up of each routed expert's tile in
+        //    one workgroup + act = silu(gate) * up
+        rc |= launch_q6k_gateup_silu(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
+                                     m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
+                                     m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
+                                     m->g.as<float>(), m->n_ff, m->be, st);
+        // 3. Q8_K of act in the prologue, down projection, weighted combine,
+        //    residual
+        rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), nullptr, nullptr,
+                                      m->g.as<float>(), m->weights.as<float>(), d_res, d_out,
+                                      m->n_embd, m->bf, m->n_used, st);
+    } else {
+        // 2. route (prologue) + gate and up of the routed experts in one
+        //    launch: g holds [gate | up] x n_used x n_ff
+        rc |= launch_q6k_mv_routed(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
+                                   m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
+                                   m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
+                                   m->g.as<float>(), m->n_ff, m->be, st);
+        // 3. SwiGLU + Q8_K of the activations
+        rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
+                                nullptr, m->aq.as<int8_t>(), m->ad.as<float>(), nullptr,
+                                m->n_used * m->bf, st);
+        // 4. down projection of the routed experts + weighted combine + residual
+        rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
+                                      m->ad.as<float>(), nullptr, m->weights.as<float>(), d_res,
+                                      d_out, m->n_embd, m->bf, m->n_used, st);
+    }
     return rc ? fail("moe_forward: launch failed") : 0;
 }
 

@@ -37,10 +37,18 @@ int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
                         const float *logits, int n_expert, int n_used, int32_t *ids_out,
                         float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
                         int rows, int blocks, hipStream_t st);
+// act non-null: f32 activations [n_slots][blocks*256] quantized to Q8_K in the
+// prologue (aq, ad unused; blocks <= 8).
 int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
-                            const int8_t *aq, const float *ad, const float *weights,
-                            const float *res, float *out, int rows, int blocks, int n_slots,
-                            hipStream_t st);
+                            const int8_t *aq, const float *ad, const float *act,
+                            const float *weights, const float *res, float *out, int rows,
+                            int blocks, int n_slots, hipStream_t st);
+// Routing prologue + gate and up of the routed experts + act = silu(g) * up
+// ([n_used][rows] f32) in one launch.
+int launch_q6k_gateup_silu(const void *w_gate, const void *w_up, size_t expert_stride,
+                           const float *logits, int n_expert, int n_used, int32_t *ids_out,
+                           float *w_out, int *stats, const int8_t *aq, const float *ad, float *act,
+                           int rows, int blocks, hipStream_t st);
 // Expert-grouped batched matvec (see q6k_mv.hip). Activations are in the
 // token-chunked layout (q8k_wave.hpp): chunk k holds the 16 tokens of
 // sub-tile k. sub_start has n_groups+1 entries (prefix of ceil(count/16));
