@@ -262,6 +262,38 @@ def bench_copy(L, rocm, mib=512, reps=5):
     return res
 
 
+def host_threads():
+    try:
+        return len(os.sched_getaffinity(0))
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def cpu_median_ms(fn, seconds, max_iters=10):
+    """1 warm-up call, then up to max_iters timed calls within ~seconds;
+    the median in ms (the reference's CPU timing protocol)."""
+    fn()
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while len(ts) < max_iters and (not ts or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_matvec_q6k_parallel(O, w, rows, k, x, nthreads):
+    """The oracle's matvec split by rows over nthreads host threads (ctypes
+    releases the GIL); rows are independent, so the result is the same bits."""
+    from concurrent.futures import ThreadPoolExecutor
+    per = k // QK_K * 210
+    step = (rows + nthreads - 1) // nthreads
+    chunks = [(r0, min(rows, r0 + step)) for r0 in range(0, rows, step)]
+    with ThreadPoolExecutor(nthreads) as ex:
+        parts = list(ex.map(lambda c: O.matvec_q6k(w[c[0] * per:c[1] * per], c[1] - c[0], k, x), chunks))
+    return np.concatenate(parts)
+
+
 def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     out = {}
     # Q8_0 matvec, configs[0]
@@ -278,6 +310,12 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     by = len(w) + k * 4 + rows * 4
     out["q8_0_matvec"] = {"rows": rows, "k": k, "bytes": by, "us_back_to_back": ms / K * 1e3,
                           "gbs_back_to_back": by * K / (ms * 1e-3) / 1e9}
+    if moe_cpu_seconds > 0:
+        from oracle import oracle as O
+        xh = synth.normal(8, 1.0, k)
+        ms_c, n_c = cpu_median_ms(lambda: O.matvec_q8_0(w, rows, k, xh), 4.0)
+        out["q8_0_matvec"].update({"cpu_1t_ms": ms_c, "cpu_calls": n_c,
+                                   "vs_cpu_1t": ms_c / (out["q8_0_matvec"]["us_back_to_back"] * 1e-3)})
     log(f"  q8_0: {out['q8_0_matvec']}")
     for q in ws:
         q.close()
@@ -319,6 +357,16 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     out["lm_head_matvec_b1"] = {"us_per_launch": ms / steps * 1e3, "bytes": by,
                                 "gbs": by / (ms / steps * 1e-3) / 1e9,
                                 "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)}
+    if moe_cpu_seconds > 0:
+        from oracle import oracle as O
+        xh = synth.normal(31, 1.0, k)
+        ms_1, n_1 = cpu_median_ms(lambda: O.matvec_q6k(w, rows, k, xh), 2.0, 3)
+        nt = min(16, host_threads())
+        ms_n, n_n = cpu_median_ms(lambda: cpu_matvec_q6k_parallel(O, w, rows, k, xh, nt), 2.0, 5)
+        out["lm_head_matvec_b1"].update({
+            "cpu_1t_ms": ms_1, "cpu_nt_ms": ms_n, "cpu_threads": nt,
+            "vs_cpu_1t": ms_1 / (out["lm_head_matvec_b1"]["us_per_launch"] * 1e-3),
+            "vs_cpu_nt": ms_n / (out["lm_head_matvec_b1"]["us_per_launch"] * 1e-3)})
     log(f"  lm_head matvec b1: {out['lm_head_matvec_b1']}")
     q1.close(); d1.close()
     for dw, h in heads:
@@ -384,9 +432,51 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                               "int_tops": ops / (ms / steps * 1e-3) / 1e12,
                               "experts_used": used, "weight_bytes": wbytes,
                               "weight_gbs": wbytes / (ms / steps * 1e-3) / 1e9}
+    if moe_cpu_seconds > 0:
+        # the reference's CPU path runs moe_ffn token by token: time a sample
+        # of 16 tokens (1 thread) and scale to the 512-token pass
+        from oracle import oracle as O
+        xh = synth.normal(700, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+        ns = 16
+        t0 = time.perf_counter()
+        O.moe_ffn_tokens(xh[:ns], n_embd, n_ff, n_expert, gate, up, down, ids_h[:ns], w_h[:ns])
+        dt = time.perf_counter() - t0
+        out["prefill_grouped"].update({
+            "cpu_1t_ms_per_pass_est": dt / ns * n_tok * 1e3,
+            "cpu_sample": f"{ns} tokens of moe_ffn in {dt:.2f}s on 1 host thread, scaled to {n_tok}",
+            "vs_cpu_1t": (dt / ns * n_tok) / (ms / steps * 1e-3)})
     log(f"  prefill: {out['prefill_grouped']}")
     for ly in layers:
         ly.close()
+
+    # attention front end (the adjacent decode step): RMSNorm -> Q8_K -> Q, K,
+    # V (4096 / 512 / 512 rows x 2048) in one launch; 4 weight sets rotate
+    blocks = n_embd // QK_K
+    qkv = [(4096, 801), (512, 802), (512, 803)]
+    mats = [synth.q6k_matrix(sd, 0.02, r, n_embd) for r, sd in qkv]
+    nset = 24  # 24 x 10.3 MB of Q/K/V weights in rotation
+    sets = [[rocm.DeviceWeights.upload(m, r, blocks) for m, (r, _) in zip(mats, qkv)] for _ in range(nset)]
+    xa = rocm.DeviceBuffer.from_array(synth.normal(804, 1.0, n_embd))
+    wn = rocm.DeviceBuffer.from_array((1 + 0.1 * synth.normal(805, 1.0, n_embd)).astype(np.float32))
+    aq, ad = rocm.DeviceBuffer(n_embd), rocm.DeviceBuffer(blocks * 4)
+    oq = [rocm.DeviceBuffer(r * 4) for r, _ in qkv]
+
+    def fa(i):
+        st_ = sets[i % nset]
+        L.llamd_fwd_rms_norm_quant(xa.ptr, wn.ptr, None, aq.ptr, ad.ptr, None, n_embd, 1e-6)
+        L.llamd_fwd_matvec_x3(st_[0].ptr, st_[1].ptr, st_[2].ptr, aq.ptr, ad.ptr, oq[0].ptr, oq[1].ptr,
+                              oq[2].ptr, blocks, qkv[0][0], qkv[1][0], qkv[2][0])
+    steps = max(20, K // 2)
+    ms = time_region(L, fa, steps, 5)
+    by = sum(q6k_bytes(r, n_embd) + r * 4 for r, _ in qkv) + n_embd * 8
+    out["attn_front_end"] = {"us_per_token": ms / steps * 1e3, "bytes": by,
+                             "gbs": by / (ms / steps * 1e-3) / 1e9,
+                             "kernels": "rms_norm_quant + matvec_x3 (Q 4096, K 512, V 512 rows)",
+                             "parity": "bit-exact (tests/test_gpu_norm.py)"}
+    log(f"  attention front end: {out['attn_front_end']}")
+    for st_ in sets:
+        for d_ in st_:
+            d_.close()
     return out
 
 
@@ -407,8 +497,18 @@ def bench_cpu(mats, shapes, xs, seconds):
         aff = len(os.sched_getaffinity(0))
     except Exception:
         aff = os.cpu_count()
+    nt = min(16, host_threads())
+    t0 = time.perf_counter()
+    n_n = 0
+    while time.perf_counter() - t0 < seconds / 4:
+        for name, rows, k, _ in shapes:
+            cpu_matvec_q6k_parallel(O, mats[name], rows, k, xs[k], nt)
+        n_n += 1
+    dt_n = time.perf_counter() - t0
     return {"value": round(bytes_step * n / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
             "kind": "port",
+            "all_cores": {"value": round(bytes_step * n_n / dt_n / 1e9, 4), "threads": nt,
+                          "ms_per_step": round(dt_n / n_n * 1e3, 3)},
             "sample": f"{n} configs[1] steps (gate+up+down Q6_K matvec incl. Q8_K quantize) in "
                       f"{dt:.1f}s on 1 of {aff} host threads",
             "ms_per_step": round(dt / n * 1e3, 3)}
