@@ -41,6 +41,9 @@ struct RouterArgs {
 // the gate/up kernel's prologue.
 template <int RPW>
 __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
+    // all kernarg fields in one batch before the first global load
+    asm volatile("" ::"s"(a.w), "s"(a.x), "s"(a.n_expert), "s"(a.k), "s"(a.logits), "s"(a.xq),
+                 "s"(a.xd), "s"(a.xblocks));
     constexpr int KMAX = 2048;
     __shared__ float4 prod[RPW][KMAX / 4];
     const int nr = (a.n_expert + RPW - 1) / RPW;
@@ -157,6 +160,7 @@ __global__ __launch_bounds__(256) void argmax_partial(const float *x, int n, int
 
 __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, const float *pv,
                                                      const int *pi, int nparts, int32_t *out) {
+    asm volatile("" ::"s"(x), "s"(ld), "s"(pv), "s"(pi), "s"(nparts), "s"(out));
     const int seq = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = -INFINITY;
@@ -201,6 +205,7 @@ constexpr int Q80_ROWS_PER_WAVE = 4;
 
 __global__ __launch_bounds__(256) void q8_0_mv(const int8_t *qs, const uint16_t *dp, const float *x,
                                                float *y, int rows, int k) {
+    asm volatile("" ::"s"(qs), "s"(dp), "s"(x), "s"(y), "s"(rows), "s"(k));
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * Q80_ROWS_PER_WAVE;
     if (r0 >= rows) return;

@@ -47,15 +47,20 @@ struct MvSeg {
     int rows, tiles, first;   // first: index of the segment's first item
 };
 
+// The fields every launch reads come first and together, so the kernel's
+// prologue fetches them from the kernarg segment in one go before the first
+// weight load; the other segments, the routing prologue's and the arg-max
+// fields follow.
 struct MvParams {
-    MvSeg seg[3];
-    int n_seg, items;         // items over all segments
-    size_t expert_stride;     // bytes between experts' tiled matrices
-    const int32_t *ids;       // slot -> expert (nullptr: slot -> expert 0)
+    MvSeg seg0;               // 32 B
     const int8_t *aq;         // Q8_K quants, [n_act][blocks*256]
     const float *ad;          // Q8_K scales, [n_act][blocks]
-    int blocks, n_slots;
-    int act_per_slot;         // 1: slot i uses activation i; 0: all use activation 0
+    const int32_t *ids;       // slot -> expert (nullptr: slot -> expert 0)
+    size_t expert_stride;     // bytes between experts' tiled matrices
+    int items, blocks;        // items over all segments; 256-blocks per row
+    int n_slots, act_per_slot;  // act_per_slot 1: slot i uses activation i
+    MvSeg seg1, seg2;
+    int n_seg;
     // routing prologue (ROUTE): wave 0 of every workgroup routes on the exact
     // router logits and takes slot -> expert from its own selection;
     // workgroup 0 publishes ids / weights for the kernels after it
@@ -213,19 +218,29 @@ __device__ __forceinline__ void consume_terms(int b, float te, float to, float &
 // meet in LDS and are folded in block order -- the same additions in the same
 // order as a single wave walking every block, so splitting K changes the
 // latency, never the bits.
-template <int KS, bool ROUTE = false>
+template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false>
 __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
     constexpr int IPW = 4 / KS;                 // items per workgroup
     constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
     __shared__ float terms[KS > 1 ? IPW : 1][KS > 1 ? MAXB : 1][TILE_ROWS][8];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // every kernarg field the common path reads, fetched in one batch up front
+    asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.y), "s"(p.seg0.rows), "s"(p.seg0.tiles),
+                 "s"(p.aq), "s"(p.ad), "s"(p.ids), "s"(p.expert_stride), "s"(p.items),
+                 "s"(p.blocks), "s"(p.act_per_slot));
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int kc = wave % KS;
     const int local = wave / KS;
     const int item = blockIdx.x * IPW + local;
     const bool live = item < p.items;
-    const int sg = (p.n_seg > 2 && item >= p.seg[2].first) ? 2 : (p.n_seg > 1 && item >= p.seg[1].first) ? 1 : 0;
-    const MvSeg sgm = p.seg[sg];
+    // the item's segment, chosen with scalar selects (no indexed kernarg load)
+    MvSeg sgm = p.seg0;
+    if constexpr (NSEG > 1) {
+        if (item >= p.seg1.first) sgm = p.seg1;
+    }
+    if constexpr (NSEG > 2) {
+        if (item >= p.seg2.first) sgm = p.seg2;
+    }
     const int pos = item - sgm.first;
     const int slot = live ? pos / sgm.tiles : 0;
     const int t = live ? pos - slot * sgm.tiles : 0;
@@ -307,7 +322,7 @@ __global__ __launch_bounds__(256) void q6k_mv_b1(MvParams p) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) tot = tot + cls[c];
     if (s == 0 && row < sgm.rows) sgm.y[(size_t)slot * sgm.rows + row] = tot;
-    if (p.amax_v) {
+    if constexpr (AMAX) {
         // this tile's arg-max candidate for the LM head (argmax_final reduces
         // the tiles): the largest non-NaN logit, lowest row on ties
         const bool ok = s == 0 && row < sgm.rows && !isnan(tot);
@@ -358,6 +373,8 @@ __device__ __forceinline__ void load_weights(BlockRegs &r, const uint8_t *seg, i
 // its first weight blocks are already in flight.
 template <bool QACT>
 __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
+    asm volatile("" ::"s"(p.w), "s"(p.expert_stride), "s"(p.ids), "s"(p.act), "s"(p.aq), "s"(p.ad),
+                 "s"(p.weights), "s"(p.res), "s"(p.out), "s"(p.rows), "s"(p.blocks), "s"(p.n_slots));
     __shared__ float ys[16][TILE_ROWS];
     __shared__ __align__(16) int8_t lq[QACT ? 16 : 1][QACT ? DOWN_ACT_BLOCKS * QK_K : 1];
     __shared__ float ld[QACT ? 16 : 1][QACT ? DOWN_ACT_BLOCKS : 1];
@@ -459,6 +476,9 @@ __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
 // the tile's 16 rows (CpuBackend::silu and mul, llamd-cpu/src/lib.rs:103-113).
 __global__ __launch_bounds__(512) void q6k_gateup_silu(MvParams p, const uint8_t *w_up,
                                                        float *act) {
+    asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.rows), "s"(p.seg0.tiles), "s"(p.aq), "s"(p.ad),
+                 "s"(p.expert_stride), "s"(p.blocks), "s"(p.route_l), "s"(p.n_expert),
+                 "s"(p.n_used), "s"(w_up), "s"(act));
     constexpr int MAXB = 16;
     __shared__ float terms[2][MAXB][TILE_ROWS][8];
     __shared__ float gu[2][TILE_ROWS];
@@ -468,7 +488,7 @@ __global__ __launch_bounds__(512) void q6k_gateup_silu(MvParams p, const uint8_t
     const int wave = threadIdx.x >> 6;
     const int half = wave >> 2;  // 0: gate, 1: up
     const int kc = wave & 3;
-    const int tiles = p.seg[0].tiles, rows = p.seg[0].rows;
+    const int tiles = p.seg0.tiles, rows = p.seg0.rows;
     const int slot = (int)blockIdx.x / tiles;
     const int t = (int)blockIdx.x - slot * tiles;
     const int n = lane & 15, s = lane >> 4;
@@ -491,7 +511,7 @@ __global__ __launch_bounds__(512) void q6k_gateup_silu(MvParams p, const uint8_t
     }
     __syncthreads();
     const int expert = rsh.sorted[slot];
-    const uint8_t *seg0 = (half ? w_up : p.seg[0].w) + (size_t)expert * p.expert_stride +
+    const uint8_t *seg0 = (half ? w_up : p.seg0.w) + (size_t)expert * p.expert_stride +
                           (size_t)t * p.blocks * SEG_BYTES;
     const int bpc = (p.blocks + 3) / 4;
     const int b0 = kc * bpc;
@@ -782,36 +802,45 @@ namespace {
 // Fills the segment table for n matrices sharing `rows`-independent shapes.
 void set_segments(MvParams &p, int n, const void *const *w, float *const *y, const int *rows,
                   int n_slots) {
+    MvSeg *seg[3] = {&p.seg0, &p.seg1, &p.seg2};
     int first = 0;
     p.n_seg = n;
     for (int i = 0; i < n; ++i) {
-        p.seg[i].w = (const uint8_t *)w[i];
-        p.seg[i].y = y[i];
-        p.seg[i].rows = rows[i];
-        p.seg[i].tiles = (rows[i] + TILE_ROWS - 1) / TILE_ROWS;
-        p.seg[i].first = first;
-        first += p.seg[i].tiles * n_slots;
+        seg[i]->w = (const uint8_t *)w[i];
+        seg[i]->y = y[i];
+        seg[i]->rows = rows[i];
+        seg[i]->tiles = (rows[i] + TILE_ROWS - 1) / TILE_ROWS;
+        seg[i]->first = first;
+        first += seg[i]->tiles * n_slots;
     }
-    for (int i = n; i < 3; ++i) p.seg[i] = p.seg[0];
+    for (int i = n; i < 3; ++i) *seg[i] = p.seg0;
     p.items = first;
     p.n_slots = n_slots;
 }
 
-int launch_b1(const MvParams &p, hipStream_t st) {
+template <int NSEG, bool AMAX = false>
+void launch_b1_n(const MvParams &p, hipStream_t st) {
     const int items = p.items;
     const int ks = g_tune_mv_ks;
     if (p.blocks <= 16 && (ks == 2 || ks == 4 || ks == 0)) {
         if (ks == 2)
-            hipLaunchKernelGGL(q6k_mv_b1<2>, dim3((items + 1) / 2), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<2, false, NSEG, AMAX>), dim3((items + 1) / 2), dim3(256), 0, st, p);
         else
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
             // tile at every size -- more loads in flight per tile and shorter
             // per-wave chains.
-            hipLaunchKernelGGL(q6k_mv_b1<4>, dim3(items), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX>), dim3(items), dim3(256), 0, st, p);
     } else {
-        hipLaunchKernelGGL(q6k_mv_b1<1>, dim3((items + 3) / 4), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX>), dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
+}
+
+int launch_b1(const MvParams &p, hipStream_t st) {
+    if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
+    else if (p.n_seg == 1) launch_b1_n<1>(p, st);
+    else if (p.n_seg == 2) launch_b1_n<2>(p, st);
+    else launch_b1_n<3>(p, st);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -910,7 +939,7 @@ int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
     p.ids_out = ids_out;
     p.w_out = w_out;
     p.stats = stats;
-    hipLaunchKernelGGL((q6k_mv_b1<4, true>), dim3(p.items), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((q6k_mv_b1<4, true, 2>), dim3(p.items), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -23,6 +23,7 @@ namespace {
 
 __global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, float *d,
                                                     int16_t *bsums, int nblocks) {
+    asm volatile("" ::"s"(x), "s"(qs), "s"(d), "s"(bsums), "s"(nblocks));
     const int lane = threadIdx.x & 63;
     const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;
