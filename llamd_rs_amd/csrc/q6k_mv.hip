@@ -383,18 +383,25 @@ __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
     const int t = blockIdx.x;
     const int n = lane & 15, s = lane >> 4;
     const MaskSel msel = mask_selectors(n, (n >> 2) == s);
-    const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
     float se = 0.0f, so = 0.0f;
     BlockRegs ra, rb;
     if constexpr (QACT) {
+        // the activations do not depend on the routed ids: their loads go
+        // out first, then the ids, then the weights
+        const float *a = p.act + (size_t)e * p.blocks * QK_K;
+        float4 av[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (j < p.blocks) av[j] = *(const float4 *)(a + (size_t)j * QK_K + 4 * lane);
+        const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
         load_weights(ra, seg0, lane, n);
         if (p.blocks > 1) load_weights(rb, seg0 + SEG_BYTES, lane, n);
-        const float *a = p.act + (size_t)e * p.blocks * QK_K;
         for (int c0 = 0; c0 < p.blocks; c0 += 4) {
-            float4 av[4];
+            if (c0 > 0) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (c0 + j < p.blocks) av[j] = *(const float4 *)(a + (size_t)(c0 + j) * QK_K + 4 * lane);
+                for (int j = 0; j < 4; ++j)
+                    if (c0 + j < p.blocks) av[j] = *(const float4 *)(a + (size_t)(c0 + j) * QK_K + 4 * lane);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 if (c0 + j < p.blocks) {
@@ -426,6 +433,7 @@ __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
             if (b + 3 < p.blocks) load_weights(rb, seg0 + (size_t)(b + 3) * SEG_BYTES, lane, n);
         }
     } else {
+        const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
         const int8_t *aq = p.aq + (size_t)e * p.blocks * QK_K;
         const float *ad = p.ad + (size_t)e * p.blocks;
         load_block(ra, seg0, aq, ad, 0, lane, n);
