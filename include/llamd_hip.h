@@ -222,7 +222,10 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
 int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float *out,
                                int32_t *ids, float *weights, float *logits, int flags);
 /* Prefill / grouped path: n_tok tokens with GIVEN routing ids/weights
- * [n_tok][n_used] (device pointers), out [n_tok][n_embd] = moe_ffn per token. */
+ * [n_tok][n_used] (device pointers), out [n_tok][n_embd] = moe_ffn per token.
+ * Device ids are not read by the host: a pair whose id is outside
+ * [0, n_expert) adds no term to its token (no memory outside the layer's
+ * buffers is touched). The _host variant refuses such ids with an error. */
 int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
                           float *d_out, int n_tok);
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,

@@ -844,7 +844,8 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
                                 m->p_idx.as<int32_t>(), m->p_aq.as<int8_t>(), m->p_ad.as<float>(),
                                 m->p_dn.as<float>(), m->n_embd, m->n_embd, m->bf, m->n_expert,
                                 max_chunks, st);
-    rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, nullptr, d_out, m->n_used, m->n_embd, n_tok, st);
+    rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, nullptr, d_out, m->n_used, m->n_embd, n_tok, st,
+                             m->p_slot.as<int32_t>());
     return rc ? fail("moe_prefill: launch failed") : 0;
 }
 

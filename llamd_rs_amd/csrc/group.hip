@@ -37,7 +37,12 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     const int tid = threadIdx.x;
     for (int e = tid; e < n_expert; e += blockDim.x) hist[e] = 0;
     __syncthreads();
-    for (int p = tid; p < n_pairs; p += blockDim.x) atomicAdd(&hist[ids[p]], 1);
+    // a pair whose id is outside [0, n_expert) joins no group: its slot is -1,
+    // which the chunk quantizers skip and the combine counts as no term
+    for (int p = tid; p < n_pairs; p += blockDim.x) {
+        const int e = ids[p];
+        if ((unsigned)e < (unsigned)n_expert) atomicAdd(&hist[e], 1);
+    }
     __syncthreads();
     if (tid == 0) {
         int start = 0, sub = 0;
@@ -58,6 +63,10 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     __syncthreads();
     for (int p = tid; p < n_pairs; p += blockDim.x) {
         const int e = ids[p];
+        if ((unsigned)e >= (unsigned)n_expert) {
+            slot_of_pair[p] = -1;
+            continue;
+        }
         const int pos = atomicAdd(&cursor[e], 1);
         const int j = pos - start_lds[e];
         slot_of_pair[p] = (sub_lds[e] + j / 16) * 16 + j % 16;

@@ -107,8 +107,11 @@ struct RouterLaunch {
 int launch_router(const RouterLaunch &l, hipStream_t st);
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
                         float *weights, hipStream_t st);
+// out[t] = res[t] + sum_e weights[t][e] * down[t][e] in e order; with skip,
+// pairs whose skip entry is negative add nothing.
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
-                       int n_used, int n_embd, int n_tok, hipStream_t st);
+                       int n_used, int n_embd, int n_tok, hipStream_t st,
+                       const int32_t *skip = nullptr);
 int argmax_parts(int n);
 // Reduce nparts (value, index) candidates per sequence ([nseq][nparts]) to the
 // reference's arg-max of row x[seq * ld ..] (index 0 wins if x[0] is NaN).

@@ -114,17 +114,21 @@ __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_ex
 // ---- 3. weighted combine + residual (layer.rs:245-258, 281-287) -------------
 // out[i] = res[i] + (((0 + w0*d0[i]) + w1*d1[i]) + ...), experts in routing order.
 // blockIdx.y = token (prefill); down is [n_tok][n_used][n_embd].
+// skip (optional): pair slots of the grouped prefill; a pair with slot < 0
+// had an out-of-range expert id and adds no term.
 __global__ void moe_combine(const float *down, const float *weights, const float *res, float *out,
-                            int n_used, int n_embd) {
+                            int n_used, int n_embd, const int32_t *skip) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_embd) return;
     const size_t tok = blockIdx.y;
     down += tok * n_used * n_embd;
     weights += tok * n_used;
+    if (skip) skip += tok * n_used;
     if (res) res += tok * n_embd;
     out += tok * n_embd;
     float acc = 0.0f;
     for (int e = 0; e < n_used; ++e) {
+        if (skip && skip[e] < 0) continue;
         const float p = weights[e] * down[(size_t)e * n_embd + i];
         acc = acc + p;
     }
@@ -286,9 +290,9 @@ int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *
 }
 
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
-                       int n_used, int n_embd, int n_tok, hipStream_t st) {
+                       int n_used, int n_embd, int n_tok, hipStream_t st, const int32_t *skip) {
     hipLaunchKernelGGL(moe_combine, dim3((n_embd + 255) / 256, n_tok), dim3(256), 0, st, down,
-                       weights, res, out, n_used, n_embd);
+                       weights, res, out, n_used, n_embd, skip);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -73,6 +73,7 @@ constexpr int CHUNK_BLOCK_BYTES = 8 * 512;
 
 __device__ __forceinline__ void store_chunk(const int q[4], float dv, int lane, int8_t *cq, float *cd,
                                             int slot, int b, int blocks) {
+    if (slot < 0) return;  // a pair with no expert (out-of-range id)
     const size_t base = ((size_t)(slot / CHUNK_TOKENS) * blocks + b);
     int8_t *dst = cq + base * CHUNK_BLOCK_BYTES + (slot % CHUNK_TOKENS) * 32;
 #pragma unroll

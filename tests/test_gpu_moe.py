@@ -226,3 +226,22 @@ def test_lm_head_argmax_ties_and_nan(gpu, nseq):               # device_forward.
             assert list(ids) == [0] * nseq
         head.close()
         dw.close()
+
+
+def test_prefill_full_config_512_tokens(gpu, qwen_layer):
+    """configs[3] at full size: 512 tokens, top-8 of 128, Zipf 1.1 (about 4096
+    pairs, the most popular experts far above 16 tokens). Every token is
+    computed on the device; a sample of 32 (every 16th, plus the tokens of the
+    most popular expert) is checked bit for bit against the CPU's moe_ffn."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    n_tok = 512
+    x = synth.normal(700, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+    ids, w = synth.zipf_routing(701, 1.1, n_tok, n_expert, n_used)
+    got = layer.prefill(x, ids.astype(np.int32), w)
+    counts = np.bincount(ids.ravel(), minlength=n_expert)
+    assert counts.max() > 64
+    top = int(np.argmax(counts))
+    sample = sorted(set(range(0, n_tok, 16)) | set(np.flatnonzero((ids == top).any(axis=1))[:8].tolist()))
+    want = O.moe_ffn_tokens(x[sample], n_embd, n_ff, n_expert, gate, up, down, ids[sample], w[sample])
+    assert bits_equal(got[sample], want)
