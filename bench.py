@@ -77,6 +77,9 @@ def sync(L):
         raise RuntimeError(f"device error: {last_error()}")
 
 
+EAGER_ONLY = False  # --eager: every region on plain launches (profiler runs)
+
+
 def time_region(L, fn, steps, warmup, graph=True):
     """W eager warm-up steps, then EXACTLY `steps` steps timed with HIP events
     on the library stream.
@@ -90,7 +93,7 @@ def time_region(L, fn, steps, warmup, graph=True):
     for i in range(warmup):
         fn(i)
     sync(L)
-    if not graph:
+    if not graph or EAGER_ONLY:
         t = Timer(L)
         t.rec(0)
         for i in range(steps):
@@ -133,7 +136,12 @@ def main():
     ap.add_argument("--quick", action="store_true", help="skip the large extra configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="plain launches everywhere, no graph replay: for rocprofv3 kernel traces, "
+                         "which space graph-replayed kernels tens of microseconds apart")
     args = ap.parse_args()
+    global EAGER_ONLY
+    EAGER_ONLY = args.eager
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no "
               "multi-GPU path; see DESIGN.md for how the path would shard.", file=sys.stderr)

@@ -233,6 +233,12 @@ int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, cons
 /* Routing statistics since create: calls, and calls routed on the exact
  * sequential router fold (every call, so the two are equal). */
 int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls);
+/* Diagnostics, no counterpart in the reference: counters[4] = {calls,
+ * exact calls, calls whose top-k set was certified from the logit estimates
+ * (gate/up started before the exact fold ended), 1 if a wait inside the
+ * decode kernel ever timed out}; estimates (optional) [2][n_expert] = the
+ * last call's estimates T and bounds E, |logit - T| <= E. Synchronous. */
+int llamd_hip_moe_counters(void *h, int *counters, double *estimates);
 
 /* ---- LM head: Q6_K matvec over the vocabulary + argmax -------------------- */
 /* Not in the reference as one call (device.rs:640-655 queues the same ops).

@@ -96,6 +96,7 @@ SIGNATURES = {
     "llamd_hip_moe_prefill": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_prefill_host": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_stats": (i32, [vp, i32p, i32p]),
+    "llamd_hip_moe_counters": (i32, [vp, i32p, vp]),
     "llamd_hip_lmhead_create": (vp, [vp, i32, i32, i32]),
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),

@@ -31,7 +31,7 @@ std::mutex g_mu;             // serialises host-in/host-out calls and the regist
 hipStream_t g_stream = nullptr;
 // 1: gate/up + SwiGLU in one launch and Q8_K in the down kernel (n_ff <= 2048);
 // 0: separate SwiGLU + Q8_K launch.
-int g_tune_moe_fused = 1;
+int g_tune_moe_fused = 2;  // 2: router+gate/up in one launch, 1: three launches, 0: unfused
 
 int fail(const char *fmt, ...) {
     va_list ap;
@@ -133,7 +133,7 @@ int llamd_hip_tune(const char *key, int value) {
     if (!key) return fail("tune: null key");
     if (!strcmp(key, "moe_fused")) {
         const int prev = g_tune_moe_fused;
-        g_tune_moe_fused = value ? 1 : 0;
+        g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
         return prev;
     }
     if (!strcmp(key, "mv_ks")) {
@@ -652,6 +652,7 @@ struct MoeLayer {
     // decode scratch
     DevBuf xq, xd, logits, ids, weights, stats;
     DevBuf g, aq, ad, dn;
+    DevBuf est, slots, spec_ids;  // decode: logit estimates, hand-off words, act-row experts
     // prefill scratch (grown on demand)
     int cap_tok = 0;
     DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_slot, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
@@ -689,9 +690,13 @@ void *llamd_hip_moe_create(const float *router, const void *gate, const void *up
              m->weights.alloc(n_used * 4) && m->stats.alloc(16) &&
              m->g.alloc((size_t)2 * n_used * n_ff * 4) &&
              m->aq.alloc((size_t)n_used * n_ff) && m->ad.alloc((size_t)n_used * m->bf * 4) &&
-             m->dn.alloc((size_t)n_used * n_embd * 4);
+             m->dn.alloc((size_t)n_used * n_embd * 4) &&
+             m->est.alloc((size_t)n_expert * 16) && m->slots.alloc((size_t)n_expert * 16) &&
+             m->spec_ids.alloc(n_used * 4);
         int zero[4] = {0, 0, 0, 0};
-        ok = ok && up(m->stats.p, zero, sizeof zero) && sync();
+        std::vector<unsigned long long> empty((size_t)2 * n_expert, ~0ull);
+        ok = ok && up(m->stats.p, zero, sizeof zero) &&
+             up(m->slots.p, empty.data(), empty.size() * 8) && sync();
     }
     if (!ok) {
         llamd_hip_moe_destroy(m);
@@ -729,6 +734,33 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
     rl.xq = m->xq.as<int8_t>();
     rl.xd = m->xd.as<float>();
     rl.xblocks = m->be;
+    if (g_tune_moe_fused == 2 && m->bf <= 8 && m->be <= 8) {
+        // router and gate/up overlapped, then down + combine (moe_decode.hip)
+        MoeDecodeLaunch dl;
+        dl.w_gate = m->gate;
+        dl.w_up = m->upw;
+        dl.w_down = m->downw;
+        dl.gu_stride = m->sgu;
+        dl.down_stride = m->sd;
+        dl.router = m->router.as<float>();
+        dl.x = d_x;
+        dl.res = d_res;
+        dl.out = d_out;
+        dl.logits = m->logits.as<float>();
+        dl.est = m->est.as<double>();
+        dl.slots = m->slots.as<unsigned long long>();
+        dl.act = m->g.as<float>();
+        dl.spec_ids = m->spec_ids.as<int32_t>();
+        dl.ids_out = m->ids.as<int32_t>();
+        dl.w_out = m->weights.as<float>();
+        dl.stats = m->stats.as<int>();
+        dl.k = m->n_embd;
+        dl.n_expert = m->n_expert;
+        dl.n_used = m->n_used;
+        dl.n_ff = m->n_ff;
+        rc |= launch_moe_decode(dl, st);
+        return rc ? fail("moe_forward: launch failed") : 0;
+    }
     rc |= launch_router(rl, st);
     if (g_tune_moe_fused && m->bf <= 8) {
         // 2. route (prologue) + gate and up of each routed expert's tile in
@@ -778,6 +810,15 @@ int llamd_hip_moe_forward_host(void *h, const float *x, const float *res, float 
     if (ids && !down(ids, m->ids.p, (size_t)m->n_used * 4)) return -1;
     if (weights && !down(weights, m->weights.p, (size_t)m->n_used * 4)) return -1;
     if (logits && !down(logits, m->logits.p, (size_t)m->n_expert * 4)) return -1;
+    return sync() ? 0 : -1;
+}
+
+int llamd_hip_moe_counters(void *h, int *counters, double *estimates) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !counters) return fail("moe_counters: null argument");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!down(counters, m->stats.p, 16)) return -1;
+    if (estimates && !down(estimates, m->est.p, (size_t)m->n_expert * 16)) return -1;
     return sync() ? 0 : -1;
 }
 

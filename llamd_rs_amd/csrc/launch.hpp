@@ -11,7 +11,7 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
-extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2 or 4 (0: automatic)
+extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -55,6 +55,23 @@ int launch_q6k_gateup_silu(const void *w_gate, const void *w_up, size_t expert_s
 // max_chunks bounds sub_start[n_groups] and sizes the grid. The output of the
 // pair at sorted position i is row pair_out[i] of y (nullptr: row i). With
 // grp_expert == nullptr there is a single group (expert 0) of n_groups tokens.
+// moe_decode.hip: one MoE decode layer (router, top-k, gate, up, SwiGLU,
+// down, combine, residual) in two launches, bit-identical to the reference.
+struct MoeDecodeLaunch {
+    const void *w_gate, *w_up, *w_down;
+    size_t gu_stride, down_stride;
+    const float *router, *x, *res;  // res may be null
+    float *out, *logits;            // [k], [n_expert]
+    double *est;                    // [2 * n_expert] diagnostic copy of the estimates
+    unsigned long long *slots;      // [2 * n_expert] all ones before the first call (every call leaves them so)
+    float *act;                     // [n_used * n_ff]
+    int32_t *spec_ids;              // [n_used]
+    int32_t *ids_out;
+    float *w_out;
+    int *stats;                     // [4]
+    int k, n_expert, n_used, n_ff;
+};
+int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st);
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
                           const int32_t *grp_start, const int32_t *grp_count,
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,

@@ -77,25 +77,7 @@ __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
                                                   wr[j].z * xr[j].z, wr[j].w * xr[j].w);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (lane == 0) {
-        // 128 products per step: the 16-byte LDS reads are issued together
-        // and retire in order, so the adds start on the first while the
-        // rest are still arriving (k is a multiple of 256)
-        float acc = -0.0f;
-        for (int i = 0; i < n4; i += 32) {
-            float4 v[32];
-#pragma unroll
-            for (int j = 0; j < 32; ++j) v[j] = prod[wv][i + j];
-#pragma unroll
-            for (int j = 0; j < 32; ++j) {
-                acc = acc + v[j].x;
-                acc = acc + v[j].y;
-                acc = acc + v[j].z;
-                acc = acc + v[j].w;
-            }
-        }
-        a.logits[row] = acc;
-    }
+    if (lane == 0) a.logits[row] = seq_fold(prod[wv], n4);
 }
 // Routing from given logits (llamd_hip_route / llamd_fwd_router).
 __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_expert, int n_used,

@@ -134,5 +134,94 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
     }
 }
 
+// ---- the router fold and its certified estimate ------------------------------
+//
+// The reference's logit is a sequential f32 fold of the row's products from
+// -0.0 (moe.rs:73-80 via the f32 matvec). seq_fold is that fold, run by one
+// lane over products parked in LDS (n4 float4s, a multiple of 32).
+__device__ __forceinline__ float seq_fold(const float4 *prod, int n4) {
+    // 128 products per step: the 16-byte LDS reads are issued together and
+    // retire in order, so the adds start on the first while the rest arrive
+    float acc = -0.0f;
+    for (int i = 0; i < n4; i += 32) {
+        float4 v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = prod[i + j];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            acc = acc + v[j].x;
+            acc = acc + v[j].y;
+            acc = acc + v[j].z;
+            acc = acc + v[j].w;
+        }
+    }
+    return acc;
+}
+
+// The exact sum T of the same products (in double) and a bound E with
+// |seq_fold - T| <= E, from the whole wave in ~1 us instead of the fold's ~7.
+//
+// Recursive summation S_k = fl(S_{k-1} + p_k) commits an error of at most
+// u |S_{k-1} + p_k| per step (u = 2^-24, round to nearest; additions whose
+// result is subnormal are exact). With D_k = |S_k - T_k| (T_k the exact
+// prefix sums) this gives D_k <= (1 + u) D_{k-1} + u |T_k|, hence
+// D_n <= u (1 + u)^n sum_k |T_k| (Higham, Accuracy and Stability of Numerical
+// Algorithms, 2nd ed., section 4.2). The prefix sums are formed in double
+// (each lane a contiguous run of n/64 products, then a wave scan); the slack
+// factor 1 + 2^-10 covers (1 + u)^2048 and the double roundings, and
+// 2^-40 sum |p| covers the error of T itself. Non-finite products make T or
+// E non-finite, which callers treat as "no estimate".
+__device__ __forceinline__ void fold_estimate(const float *prod, int n, double &T, double &E) {
+    const int lane = threadIdx.x & 63;
+    const int len = n / WAVE;  // n is a multiple of 256: len is a multiple of 4
+    const float4 *seg = (const float4 *)(prod + lane * len);
+    double s = 0.0, a = 0.0;
+    for (int j = 0; j < len / 4; ++j) {
+        const float4 v = seg[j];
+        s += (double)v.x; s += (double)v.y; s += (double)v.z; s += (double)v.w;
+        a += fabs((double)v.x) + fabs((double)v.y) + fabs((double)v.z) + fabs((double)v.w);
+    }
+    const double incl = wave_inclusive_sum(s);
+    double run = incl - s;  // exclusive prefix: the sum of the products before this run
+    double pabs = 0.0;
+    for (int j = 0; j < len / 4; ++j) {
+        const float4 v = seg[j];
+        run += (double)v.x; pabs += fabs(run);
+        run += (double)v.y; pabs += fabs(run);
+        run += (double)v.z; pabs += fabs(run);
+        run += (double)v.w; pabs += fabs(run);
+    }
+    T = readlane63(incl);
+    const double sum_prefix = wave_sum_d(pabs), sum_abs = wave_sum_d(a);
+    E = 0x1p-24 * (1.0 + 0x1p-10) * sum_prefix + 0x1p-40 * sum_abs;
+}
+
+// Publication of one value per expert between workgroups of one launch, with
+// no cache-wide fences: the value and its "ready" mark travel in ONE 64-bit
+// word written with a relaxed agent-scope atomic store and polled with
+// relaxed agent-scope atomic loads (coherent across the XCDs' L2s; an
+// agent-scope release or acquire would write back or invalidate a whole L2
+// per use). A slot holds SLOT_EMPTY until its word is stored; the consumer of
+// the last call resets the slots to SLOT_EMPTY for the next.
+constexpr unsigned long long SLOT_EMPTY = ~0ull;
+
+__device__ __forceinline__ void slot_store(unsigned long long *slot, unsigned lo, unsigned hi) {
+    __hip_atomic_store(slot, ((unsigned long long)hi << 32) | lo, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait for a slot to be filled. Only ever waits on workgroups with
+// lower indices, which the dispatcher has already placed; the bound (about a
+// quarter of a second) guarantees every wave exits even if that ever fails.
+// Returns SLOT_EMPTY on timeout.
+__device__ __forceinline__ unsigned long long slot_wait(const unsigned long long *slot) {
+    for (int it = 0; it < (1 << 18); ++it) {
+        const unsigned long long v =
+            __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v != SLOT_EMPTY) return v;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return SLOT_EMPTY;
+}
 
 }  // namespace llamd

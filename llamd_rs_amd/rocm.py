@@ -365,6 +365,15 @@ class MoeLayer:
         check(lib().llamd_hip_moe_stats(self._h, C.byref(a), C.byref(b)), "moe_stats")
         return a.value, b.value
 
+    def counters(self) -> tuple[np.ndarray, np.ndarray]:
+        """([calls, exact calls, certified calls, wait timed out], the last
+        call's logit estimates T [n_expert] and bounds E [n_expert])."""
+        c = np.zeros(4, np.int32)
+        est = np.zeros(2 * self.n_expert, np.float64)
+        check(lib().llamd_hip_moe_counters(self._h, c.ctypes.data_as(C.POINTER(C.c_int)), _ptr(est)),
+              "moe_counters")
+        return c, est.reshape(2, self.n_expert)
+
     def close(self):
         if self._h:
             lib().llamd_hip_moe_destroy(self._h)

@@ -177,3 +177,24 @@ def test_q8_0_matvec_within_reduction(gpu):
     cpu = O.matvec_q8_0(w, rows, k, x)
     idx, dev_ = O.max_deviation(got, cpu)
     assert dev_ <= O.REDUCTION, (idx, got[idx], cpu[idx])
+
+
+@pytest.mark.parametrize("rows,blocks", [(48, 8), (768, 8), (40, 5), (64, 16), (33, 3)])
+def test_every_k_split_is_bit_identical(gpu, rows, blocks):
+    """The matvec splits K over 1, 2, 4 or 8 waves per 16-row tile (chosen by
+    grid size); every split folds the per-block terms in block order, so all
+    of them give the reference's bits (dot.rs:190-195)."""
+    from llamd_rs_amd._lib import lib
+    w = H.weights(rows, blocks, 70 + blocks)
+    x = H.sample(blocks * QK_K, 71 + rows)
+    act = gpu.quantize_q8k_on_device(x)
+    want = cpu_rows(w, rows, blocks, act)
+    dw = gpu.DeviceWeights.upload(w, rows, blocks)
+    L = lib()
+    try:
+        for ks in (1, 2, 4, 8, 0):
+            L.llamd_hip_tune(b"mv_ks", ks)
+            assert bits_equal(dw.matvec(act), want), ks
+    finally:
+        L.llamd_hip_tune(b"mv_ks", 0)
+        dw.close()

@@ -1,6 +1,8 @@
 """Routing, the MoE decode layer, prefill grouping and the LM head on the
 MI355X against the CPU oracle. Router logits, expert ids, routing weights,
 decode-layer outputs and argmax ids: EXACT (bit-identical)."""
+import math
+
 import numpy as np
 import pytest
 
@@ -245,3 +247,80 @@ def test_prefill_full_config_512_tokens(gpu, qwen_layer):
     sample = sorted(set(range(0, n_tok, 16)) | set(np.flatnonzero((ids == top).any(axis=1))[:8].tolist()))
     want = O.moe_ffn_tokens(x[sample], n_embd, n_ff, n_expert, gate, up, down, ids[sample], w[sample])
     assert bits_equal(got[sample], want)
+
+
+def _host_bound(router, x):
+    """Exact prefix-sum bound of the f32 sequential fold, on the host."""
+    p = (router.astype(np.float32) * x.astype(np.float32)[None, :]).astype(np.float64)
+    T = np.array([math.fsum(r) for r in p])
+    pre = np.cumsum(p, axis=1)
+    return T, 2.0 ** -24 * np.abs(pre).sum(axis=1), np.abs(p).sum(axis=1)
+
+
+def test_decode_logit_estimates_bound_the_sequential_fold(gpu, qwen_layer):
+    """The decode kernel starts gate/up on a top-k set certified from
+    estimates T, E of the logits (|logit - T| <= E, Higham's recursive
+    summation bound over the prefix sums). The published estimates must bound
+    the reference's fold on every expert and match the host's bound."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    for t in range(6):
+        x = synth.normal(4000 + t, 1.0 + 3 * t, n_embd)
+        out, r, lg = layer.forward(x)
+        _, est = layer.counters()
+        T, E = est
+        Th, Eh, pabs = _host_bound(router, x)
+        assert np.all(np.abs(T - Th) <= 1e-12 * pabs), t
+        assert np.all(np.abs(lg.astype(np.float64) - T) <= E), t
+        assert np.all(E >= Eh) and np.all(E <= Eh * 1.01 + 2.0 ** -39 * pabs), t
+
+
+def test_decode_certified_and_fallback_paths_both_exact(gpu):
+    """Well-separated logits take the certified path, logits tied at the
+    k-th place take the wait-for-exact path; both give the CPU's bits."""
+    n_embd, n_ff, n_expert, n_used = 256, 256, 16, 4
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 910)
+    router = router.copy()
+    for e in (5, 7, 9, 11):
+        router[e] = router[2]               # five experts tied exactly ...
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    rng = np.random.default_rng(5)
+    try:
+        c0, _ = layer.counters()
+        n_cert = 0
+        for t in range(12):
+            x = rng.standard_normal(n_embd).astype(np.float32)
+            if t % 2:
+                x = x * np.sign(router[2] @ x) * 4  # ... on top: the tie straddles k = 4
+            want, lg, ids, w = O.moe_layer(x, np.zeros(n_embd, np.float32), n_embd, n_ff, n_expert,
+                                           n_used, router, gate, up, down)
+            out, r, lgd = layer.forward(x)
+            assert bits_equal(lgd, lg) and list(r.experts) == list(ids), t
+            assert bits_equal(r.weights, w) and np.array_equal(out, want), t
+        c1, _ = layer.counters()
+        certified = c1[2] - c0[2]
+        assert c1[3] == 0                       # no wait ever timed out
+        assert c1[0] - c0[0] == 12 and c1[1] == c1[0]
+        assert 0 < certified < 12, certified    # both paths were taken
+    finally:
+        layer.close()
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_decode_modes_bit_identical(gpu, qwen_layer, mode):
+    """The three decode schedules (unfused; router, gate/up and down in three
+    launches; router with gate/up in one) give the same bits."""
+    from llamd_rs_amd import synth
+    from llamd_rs_amd._lib import lib
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    prev = lib().llamd_hip_tune(b"moe_fused", mode)
+    try:
+        for t in range(3):
+            x = synth.normal(5000 + t, 1.0, n_embd)
+            res = synth.normal(5100 + t, 1.0, n_embd)
+            want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+            out, r, lgd = layer.forward(x, res)
+            assert bits_equal(lgd, lg) and list(r.experts) == list(ids), (mode, t)
+            assert bits_equal(r.weights, w) and bits_equal(out, want), (mode, t)
+    finally:
+        lib().llamd_hip_tune(b"moe_fused", prev)
