@@ -41,7 +41,7 @@ GIB = 1 << 30
 # scaled by the same counters on a copy of known size (x2.0 fetch, x1.0
 # write); the commands and per-kernel values are in
 # profiles/q6k_mv_b1.configs1.hbm_traffic.txt. Algorithmic: 1,301,504 B.
-TRAFFIC_Q6K_MV_CONFIGS1 = 1396470
+TRAFFIC_Q6K_MV_CONFIGS1 = 1386959
 
 
 def log(*a):
@@ -204,7 +204,10 @@ def main():
         log(f"  {name}: {shape_res[name]}")
     # dominant kernel for the roofline: q6k_mv_b1, the three launches of the
     # timed step; its average launch duration is the HIP-event time of the
-    # timed region over the launches in it (rocprof's kernel average agrees)
+    # timed region over the launches in it -- the back-to-back interval.
+    # rocprofv3's per-dispatch average for the same kernels reads ~9% longer
+    # (traced dispatches run alone, their start-up and drain exposed):
+    # profiles/q6k_mv_b1.configs1.kernel_trace.txt
     launches = 3 * K
     avg_us = ms * 1e3 / launches
     bytes_launch = bytes_step / 3

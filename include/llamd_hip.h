@@ -231,7 +231,9 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
                                float *out, int n_tok);
 /* Routing statistics since create: calls, and calls routed on the exact
- * sequential router fold (every call, so the two are equal). */
+ * sequential router fold (every call, so the two are equal). Returns -1 if a
+ * bounded wait inside the decode kernel ever timed out (never observed; it
+ * would mean workgroups were not placed in index order). */
 int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls);
 /* Diagnostics, no counterpart in the reference: counters[4] = {calls,
  * exact calls, calls whose top-k set was certified from the logit estimates

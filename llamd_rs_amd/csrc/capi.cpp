@@ -830,6 +830,9 @@ int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls) {
     if (!down(s, m->stats.p, sizeof s) || !sync()) return -1;
     if (calls) *calls = s[0];
     if (exact_calls) *exact_calls = s[1];
+    // a bounded wait inside the decode kernel ran out (workgroups not placed
+    // in index order): that call's results are not to be trusted
+    if (s[3]) return fail("moe_stats: a wait inside the decode kernel timed out");
     return 0;
 }
 
