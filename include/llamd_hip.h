@@ -270,6 +270,39 @@ int llamd_rocm_matvec_grouped_bench(const void *d_w, const int32_t *eid, const i
                                     const float *ad, int blocks, int rows, int n_used, int iters,
                                     float *ms_out);
 
+/* ---- GGUF: the model file in front of the path --------------------------- */
+/* crates/llamd-gguf/src/lib.rs (Gguf::open / get / tensor / tensor_data) and
+ * the upload side of crates/llamd-runtime/src/device.rs:224-256. Host-only
+ * except the two uploads; the file is memory-mapped read-only and every
+ * length in it is checked before use (lib.rs:141-236). NULL / -1 on failure,
+ * with the reason in llamd_hip_last_error(). Pointers returned by
+ * llamd_gguf_tensor_data stay valid until llamd_gguf_close. */
+void *llamd_gguf_open(const char *path);
+void llamd_gguf_close(void *g);
+int llamd_gguf_header(void *g, uint32_t *version, uint64_t *n_tensors, uint64_t *n_kv,
+                      uint64_t *alignment, uint64_t *data_offset, uint64_t *file_size);
+/* metadata entry i, keys in byte order (lib.rs:118 BTreeMap); types are
+ * ggml's gguf_type (0 u8 .. 12 f64, 8 string, 9 array) */
+int llamd_gguf_kv(void *g, uint64_t i, char *key, size_t cap, uint32_t *type,
+                  uint32_t *arr_type, uint64_t *arr_len);
+int64_t llamd_gguf_find_kv(void *g, const char *key);          /* -1 if absent */
+int llamd_gguf_kv_bits(void *g, uint64_t i, uint64_t elem, uint64_t *bits);
+int llamd_gguf_kv_str(void *g, uint64_t i, uint64_t elem, char *buf, size_t cap, uint64_t *len);
+int llamd_gguf_get_u64(void *g, const char *key, uint64_t *out); /* Value::as_u64, lib.rs:55-67 */
+int llamd_gguf_get_f32(void *g, const char *key, float *out);    /* Value::as_f32, lib.rs:68-74 */
+/* tensor i in file order; dims in ggml order (dims[0] fastest), unused = 1 */
+int llamd_gguf_tensor(void *g, uint64_t i, char *name, size_t cap, uint32_t *n_dims,
+                      uint64_t dims[4], uint32_t *type, uint64_t *offset);
+int64_t llamd_gguf_find_tensor(void *g, const char *name);     /* -1 if absent */
+/* Gguf::tensor_data (lib.rs:256-278): F32, F16, Q8_0, Q6_K only */
+const void *llamd_gguf_tensor_data(void *g, uint64_t i, uint64_t *nbytes);
+/* A Q6_K tensor to the device, tiled (device.rs:236-248): 2D [k, rows] as
+ * llamd_rocm_upload_q6k, 3D [k, rows, n_expert] as llamd_rocm_upload_q6k_experts. */
+void *llamd_gguf_upload_q6k(void *g, const char *name);
+/* blk.<layer>'s MoE FFN (ffn_gate_inp F32 router, ffn_{gate,up,down}_exps
+ * Q6_K) as llamd_hip_moe_create, n_used from <arch>.expert_used_count. */
+void *llamd_gguf_moe_create(void *g, int layer);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,6 +97,20 @@ SIGNATURES = {
     "llamd_hip_moe_prefill_host": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_stats": (i32, [vp, i32p, i32p]),
     "llamd_hip_moe_counters": (i32, [vp, i32p, vp]),
+    "llamd_gguf_open": (vp, [cp]),
+    "llamd_gguf_close": (None, [vp]),
+    "llamd_gguf_header": (i32, [vp, vp, vp, vp, vp, vp, vp]),
+    "llamd_gguf_kv": (i32, [vp, u64, vp, sz, vp, vp, vp]),
+    "llamd_gguf_find_kv": (C.c_int64, [vp, cp]),
+    "llamd_gguf_kv_bits": (i32, [vp, u64, u64, vp]),
+    "llamd_gguf_kv_str": (i32, [vp, u64, u64, vp, sz, vp]),
+    "llamd_gguf_get_u64": (i32, [vp, cp, vp]),
+    "llamd_gguf_get_f32": (i32, [vp, cp, vp]),
+    "llamd_gguf_tensor": (i32, [vp, u64, vp, sz, vp, vp, vp, vp]),
+    "llamd_gguf_find_tensor": (C.c_int64, [vp, cp]),
+    "llamd_gguf_tensor_data": (vp, [vp, u64, vp]),
+    "llamd_gguf_upload_q6k": (vp, [vp, cp]),
+    "llamd_gguf_moe_create": (vp, [vp, i32]),
     "llamd_hip_lmhead_create": (vp, [vp, i32, i32, i32]),
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/llamd_hip.h"
+#include "errors.hpp"
 #include "launch.hpp"
 
 using namespace llamd;
@@ -29,9 +30,9 @@ constexpr int SEGB = 16 * 210;
 thread_local char g_err[512] = "";
 std::mutex g_mu;             // serialises host-in/host-out calls and the registry
 hipStream_t g_stream = nullptr;
-// 1: gate/up + SwiGLU in one launch and Q8_K in the down kernel (n_ff <= 2048);
-// 0: separate SwiGLU + Q8_K launch.
-int g_tune_moe_fused = 2;  // 2: router+gate/up in one launch, 1: three launches, 0: unfused
+// MoE decode schedule: 2 router fold beside gate/up, then down (moe_decode.hip);
+// 1 router, gate/up + SwiGLU, down + combine; 0 unfused (separate SwiGLU).
+int g_tune_moe_fused = 2;
 
 int fail(const char *fmt, ...) {
     va_list ap;
@@ -40,6 +41,20 @@ int fail(const char *fmt, ...) {
     va_end(ap);
     return -1;
 }
+
+}  // namespace
+
+// The error text of the calling thread, for the other host files of the
+// library (errors.hpp).
+int llamd::set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+namespace {
 
 bool hip_ok(hipError_t e, const char *what) {
     if (e == hipSuccess) return true;

@@ -329,6 +329,14 @@ class MoeLayer:
         self._h = check_ptr(lib().llamd_hip_moe_create(_ptr(router), _ptr(gate), _ptr(up), _ptr(down),
                                                        n_embd, n_ff, n_expert, n_used), "moe_create")
 
+    @classmethod
+    def from_handle(cls, h, n_embd: int, n_ff: int, n_expert: int, n_used: int) -> "MoeLayer":
+        """Wrap a layer the library built elsewhere (e.g. llamd_gguf_moe_create)."""
+        m = cls.__new__(cls)
+        m.n_embd, m.n_ff, m.n_expert, m.n_used = n_embd, n_ff, n_expert, n_used
+        m._h = check_ptr(h, "moe layer")
+        return m
+
     @property
     def handle(self):
         return self._h
