@@ -423,6 +423,22 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
         out["moe_layer"]["vs_cpu"] = out["moe_layer"]["tok_s"] / (n / dt)
     log(f"  moe layer: {out['moe_layer']}")
 
+    # batched decode: 16 sequences, each routed by its own logits, experts
+    # grouped across the batch (one layer call per 16 tokens)
+    OB = rocm.DeviceBuffer(16 * n_embd * 4)
+    def fb(i):
+        xo = X.ptr + (i % 4) * 16 * n_embd * 4
+        ro = R.ptr + (i % 4) * 16 * n_embd * 4
+        if L.llamd_hip_moe_forward_batch(layers[i % 4].handle, xo, ro, OB.ptr, 16):
+            raise RuntimeError("moe batch")
+    bsteps = max(10, K // 10)
+    ms = time_region(L, fb, bsteps, 4, graph=False)  # warm-up sizes every layer's scratch
+    out["moe_layer_batch16"] = {"us_per_batch": ms / bsteps * 1e3,
+                                "us_per_token": ms / bsteps * 1e3 / 16,
+                                "tok_s": 16 * bsteps / (ms * 1e-3),
+                                "routing": "bit-exact per sequence"}
+    log(f"  moe layer batch 16: {out['moe_layer_batch16']}")
+
     # prefill grouped GEMM, configs[3]: 512 tokens, Zipf 1.1
     n_tok = 512
     xs = rocm.DeviceBuffer.from_array(synth.normal(700, 1.0, n_tok * n_embd))

@@ -230,6 +230,18 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
                           float *d_out, int n_tok);
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
                                float *out, int n_tok);
+/* Batched decode (device.rs:741-962, forward_batch's MoE block): nseq
+ * sequences x [nseq][n_embd], each routed by ITS OWN router logits (the
+ * reference's sequential fold, all nseq x n_expert folds at once; then
+ * softmax / top-k / renormalise per sequence), then the experts grouped
+ * across the sequences so an expert's weights are read once per 16 tokens
+ * routed to it; out = res + moe_ffn per sequence (res optional).
+ * Bit-identical to nseq calls of llamd_hip_moe_forward. Device pointers. */
+int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, float *d_out,
+                                int nseq);
+/* Host in/out; ids / weights [nseq][n_used] and logits [nseq][n_expert] optional. */
+int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, float *out,
+                                     int32_t *ids, float *weights, float *logits, int nseq);
 /* Routing statistics since create: calls, and calls routed on the exact
  * sequential router fold (every call, so the two are equal). Returns -1 if a
  * bounded wait inside the decode kernel ever timed out (never observed; it

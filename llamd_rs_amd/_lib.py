@@ -96,6 +96,8 @@ SIGNATURES = {
     "llamd_hip_moe_prefill": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_prefill_host": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_stats": (i32, [vp, i32p, i32p]),
+    "llamd_hip_moe_forward_batch": (i32, [vp, vp, vp, vp, i32]),
+    "llamd_hip_moe_forward_batch_host": (i32, [vp, vp, vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_counters": (i32, [vp, i32p, vp]),
     "llamd_gguf_open": (vp, [cp]),
     "llamd_gguf_close": (None, [vp]),

@@ -669,7 +669,8 @@ struct MoeLayer {
     DevBuf g, aq, ad, dn;
     DevBuf est, slots, spec_ids;  // decode: logit estimates, hand-off words, act-row experts
     // prefill scratch (grown on demand)
-    int cap_tok = 0;
+    int cap_tok = 0, cap_seq = 0;
+    DevBuf b_logits, b_ids, b_w;  // batched decode routing
     DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_slot, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
 };
 
@@ -851,10 +852,14 @@ int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls) {
     return 0;
 }
 
-int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
-                          float *d_out, int n_tok) {
-    MoeLayer *m = (MoeLayer *)h;
-    if (!m || !d_x || !d_ids || !d_w || !d_out || n_tok <= 0) return fail("moe_prefill: bad arguments");
+}  // extern "C"
+
+namespace {
+
+// The expert-grouped FFN of n_tok tokens with routing ids / weights
+// [n_tok][n_used] on the device; out = res + moe_ffn (res optional).
+int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float *d_w,
+                const float *d_res, float *d_out, int n_tok) {
     const int np = n_tok * m->n_used;
     if (n_tok > m->cap_tok) {
         // grown outside any capture; the stream is drained first so no queued
@@ -903,9 +908,76 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
                                 m->p_idx.as<int32_t>(), m->p_aq.as<int8_t>(), m->p_ad.as<float>(),
                                 m->p_dn.as<float>(), m->n_embd, m->n_embd, m->bf, m->n_expert,
                                 max_chunks, st);
-    rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, nullptr, d_out, m->n_used, m->n_embd, n_tok, st,
+    rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, d_res, d_out, m->n_used, m->n_embd, n_tok, st,
                              m->p_slot.as<int32_t>());
     return rc ? fail("moe_prefill: launch failed") : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
+                          float *d_out, int n_tok) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !d_x || !d_ids || !d_w || !d_out || n_tok <= 0) return fail("moe_prefill: bad arguments");
+    return moe_grouped(m, d_x, d_ids, d_w, nullptr, d_out, n_tok);
+}
+
+int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, float *d_out,
+                                int nseq) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !d_x || !d_out || nseq <= 0) return fail("moe_forward_batch: bad arguments");
+    if (nseq > m->cap_seq) {
+        if (!sync()) return -1;
+        if (!m->b_logits.alloc((size_t)nseq * m->n_expert * 4) ||
+            !m->b_ids.alloc((size_t)nseq * m->n_used * 4) ||
+            !m->b_w.alloc((size_t)nseq * m->n_used * 4)) {
+            m->cap_seq = 0;
+            return fail("moe_forward_batch: allocation failed");
+        }
+        m->cap_seq = nseq;
+    }
+    hipStream_t st = stream();
+    // 1. the reference's router logits for every (sequence, expert), all folds at once
+    RouterLaunch rl;
+    rl.w = m->router.as<float>();
+    rl.x = d_x;
+    rl.n_expert = m->n_expert;
+    rl.k = m->n_embd;
+    rl.logits = m->b_logits.as<float>();
+    rl.xq = nullptr;
+    rl.xd = nullptr;
+    rl.xblocks = 0;
+    rl.nseq = nseq;
+    int rc = launch_router(rl, st);
+    // 2. softmax / top-k / renormalise per sequence
+    rc |= launch_route_logits(m->b_logits.as<float>(), m->n_expert, m->n_used, m->b_ids.as<int32_t>(),
+                              m->b_w.as<float>(), st, nseq);
+    if (rc) return fail("moe_forward_batch: launch failed");
+    // 3. the experts, grouped across the sequences (weights read once per
+    //    16 tokens of an expert), combine + residual
+    return moe_grouped(m, d_x, m->b_ids.as<int32_t>(), m->b_w.as<float>(), d_res, d_out, nseq);
+}
+
+int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, float *out,
+                                     int32_t *ids, float *weights, float *logits, int nseq) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !x || !out || nseq <= 0) return fail("moe_forward_batch_host: bad arguments");
+    std::lock_guard<std::mutex> lk(g_mu);
+    const size_t nb = (size_t)nseq * m->n_embd * 4;
+    DevBuf dx(nb), dr(nb), dout(nb);
+    if (!dx.p || !dr.p || !dout.p) return fail("hipMalloc");
+    if (!up(dx.p, x, nb)) return -1;
+    if (res && !up(dr.p, res, nb)) return -1;
+    if (llamd_hip_moe_forward_batch(m, dx.as<float>(), res ? dr.as<float>() : nullptr,
+                                    dout.as<float>(), nseq))
+        return -1;
+    if (!down(out, dout.p, nb)) return -1;
+    if (ids && !down(ids, m->b_ids.p, (size_t)nseq * m->n_used * 4)) return -1;
+    if (weights && !down(weights, m->b_w.p, (size_t)nseq * m->n_used * 4)) return -1;
+    if (logits && !down(logits, m->b_logits.p, (size_t)nseq * m->n_expert * 4)) return -1;
+    return sync() ? 0 : -1;
 }
 
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,

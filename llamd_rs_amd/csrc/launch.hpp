@@ -120,10 +120,12 @@ struct RouterLaunch {
     int8_t *xq;
     float *xd;
     int xblocks;
+    int nseq = 1;  // x [nseq][k] -> logits [nseq][n_expert]; xblocks only with nseq = 1
 };
 int launch_router(const RouterLaunch &l, hipStream_t st);
+// nseq sequences: logits [nseq][n_expert] -> ids, weights [nseq][n_used]
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
-                        float *weights, hipStream_t st);
+                        float *weights, hipStream_t st, int nseq = 1);
 // out[t] = res[t] + sum_e weights[t][e] * down[t][e] in e order; with skip,
 // pairs whose skip entry is negative add nothing.
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,

@@ -23,9 +23,9 @@ namespace {
 
 struct RouterArgs {
     const float *w;          // f32 router [n_expert][k]
-    const float *x;          // [k]
+    const float *x;          // [nseq][k] (blockIdx.y = sequence)
     int n_expert, k;
-    float *logits;           // [n_expert] the reference's logits, bit for bit
+    float *logits;           // [nseq][n_expert] the reference's logits, bit for bit
     // fused Q8_K quantisation of x for the expert matvecs
     int8_t *xq;
     float *xd;
@@ -50,6 +50,7 @@ __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     if ((int)blockIdx.x >= nr) {
+        // (xblocks > 0 only with one sequence)
         const int blk = ((int)blockIdx.x - nr) * RPW + wv;
         if (blk < a.xblocks) {
             const float4 xv = *(const float4 *)(a.x + (size_t)blk * QK_K + 4 * lane);
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
     const int row = blockIdx.x * RPW + wv;
     if (row >= a.n_expert) return;
     const float4 *w4 = (const float4 *)(a.w + (size_t)row * a.k);
-    const float4 *x4 = (const float4 *)a.x;
+    const float4 *x4 = (const float4 *)(a.x + (size_t)blockIdx.y * a.k);
     const int n4 = a.k / 4;  // a multiple of 64 (k is a multiple of 256)
     float4 wr[KMAX / 256], xr[KMAX / 256];
 #pragma unroll
@@ -77,13 +78,18 @@ __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
                                                   wr[j].z * xr[j].z, wr[j].w * xr[j].w);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (lane == 0) a.logits[row] = seq_fold(prod[wv], n4);
+    if (lane == 0) a.logits[(size_t)blockIdx.y * a.n_expert + row] = seq_fold(prod[wv], n4);
 }
 // Routing from given logits (llamd_hip_route / llamd_fwd_router).
+// One workgroup per sequence (blockIdx.x): logits [nseq][n_expert] -> ids,
+// weights [nseq][n_used].
 __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_expert, int n_used,
                                                    int32_t *ids, float *weights) {
     __shared__ RouteLds sh;
     const int lane = threadIdx.x;
+    logits += (size_t)blockIdx.x * n_expert;
+    ids += (size_t)blockIdx.x * n_used;
+    weights += (size_t)blockIdx.x * n_used;
     float l[RW];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
@@ -258,15 +264,16 @@ int launch_router(const RouterLaunch &l, hipStream_t st) {
     RouterArgs a;
     a.w = l.w; a.x = l.x; a.n_expert = l.n_expert; a.k = l.k; a.logits = l.logits;
     a.xq = l.xq; a.xd = l.xd; a.xblocks = l.xblocks;
-    if (l.k % QK_K || l.k > 2048) return -1;
+    if (l.k % QK_K || l.k > 2048 || l.nseq <= 0 || (l.nseq > 1 && l.xblocks)) return -1;
     // one row per workgroup spreads the sequential folds over the most CUs
-    hipLaunchKernelGGL(router_logits<1>, dim3(l.n_expert + l.xblocks), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(router_logits<1>, dim3(l.n_expert + l.xblocks, l.nseq), dim3(64), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
-                        float *weights, hipStream_t st) {
-    hipLaunchKernelGGL(route_logits, dim3(1), dim3(64), 0, st, logits, n_expert, n_used, ids,
+                        float *weights, hipStream_t st, int nseq) {
+    if (nseq <= 0) return -1;
+    hipLaunchKernelGGL(route_logits, dim3(nseq), dim3(64), 0, st, logits, n_expert, n_used, ids,
                        weights);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

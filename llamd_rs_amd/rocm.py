@@ -357,6 +357,21 @@ class MoeLayer:
               "moe_forward")
         return out, Routing(ids, w), lg
 
+    def forward_batch(self, x, res=None):
+        """nseq sequences at once, each routed by its own logits; returns
+        (out [nseq, n_embd], ids [nseq, n_used], weights [nseq, n_used],
+        logits [nseq, n_expert]). Bit-identical to forward() per row."""
+        x = _f32(x).reshape(-1, self.n_embd)
+        nseq = x.shape[0]
+        r = None if res is None else _f32(res).reshape(nseq, self.n_embd)
+        out = np.empty((nseq, self.n_embd), np.float32)
+        ids = np.empty((nseq, self.n_used), np.int32)
+        w = np.empty((nseq, self.n_used), np.float32)
+        lg = np.empty((nseq, self.n_expert), np.float32)
+        check(lib().llamd_hip_moe_forward_batch_host(self._h, _ptr(x), _ptr(r), _ptr(out), _ptr(ids),
+                                                     _ptr(w), _ptr(lg), nseq), "moe_forward_batch")
+        return out, ids, w, lg
+
     def prefill(self, x, ids, weights) -> np.ndarray:
         """moe_ffn for n_tok tokens with the given routing [n_tok, n_used]."""
         x = _f32(x).reshape(-1, self.n_embd)

@@ -324,3 +324,46 @@ def test_decode_modes_bit_identical(gpu, qwen_layer, mode):
             assert bits_equal(r.weights, w) and bits_equal(out, want), (mode, t)
     finally:
         lib().llamd_hip_tune(b"moe_fused", prev)
+
+
+@pytest.mark.parametrize("nseq", [1, 2, 5, 16])
+def test_batched_decode_equals_per_sequence_decode(gpu, qwen_layer, nseq):
+    """forward_batch: every sequence routed by its own exact logits, experts
+    grouped across the batch; each row bit-identical to the CPU's layer."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    x = synth.normal(900 + nseq, 1.0, nseq * n_embd).reshape(nseq, n_embd)
+    res = synth.normal(950 + nseq, 1.0, nseq * n_embd).reshape(nseq, n_embd)
+    out, ids, w, lg = layer.forward_batch(x, res)
+    for s in range(nseq):
+        want, lgc, idc, wc = O.moe_layer(x[s], res[s], n_embd, n_ff, n_expert, n_used, router, gate,
+                                         up, down)
+        assert bits_equal(lg[s], lgc), s
+        assert list(ids[s]) == list(idc), s
+        assert bits_equal(w[s], wc), s
+        assert bits_equal(out[s], want), s
+
+
+def test_batched_decode_shared_experts_and_ties(gpu):
+    """A batch whose sequences share experts (same x twice), tie at the k-th
+    place (identical router rows) and run without a residual."""
+    from llamd_rs_amd import synth
+    n_embd, n_ff, n_expert, n_used = 256, 256, 16, 4
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 930)
+    router = router.copy()
+    for e in (5, 7, 9, 11):
+        router[e] = router[2]
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    try:
+        x = synth.normal(931, 1.0, 6 * n_embd).reshape(6, n_embd)
+        x[3] = x[0]
+        x[4] = x[4] * np.sign(router[2] @ x[4]) * 4
+        out, ids, w, lg = layer.forward_batch(x)
+        for s in range(6):
+            want, lgc, idc, wc = O.moe_layer(x[s], np.zeros(n_embd, np.float32), n_embd, n_ff,
+                                             n_expert, n_used, router, gate, up, down)
+            assert list(ids[s]) == list(idc) and bits_equal(w[s], wc), s
+            assert np.array_equal(out[s], want), s   # no residual: +0.0 vs -0.0 aside
+        assert bits_equal(out[3], out[0])
+    finally:
+        layer.close()
