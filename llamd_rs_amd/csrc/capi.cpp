@@ -33,6 +33,9 @@ hipStream_t g_stream = nullptr;
 // MoE decode schedule: 2 router fold beside gate/up, then down (moe_decode.hip);
 // 1 router, gate/up + SwiGLU, down + combine; 0 unfused (separate SwiGLU).
 int g_tune_moe_fused = 2;
+// batched decode: up to this many sequences through the decode kernels, more
+// through the expert-grouped (prefill) kernels
+int g_tune_batch_decode_max = 16;
 
 int fail(const char *fmt, ...) {
     va_list ap;
@@ -149,6 +152,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "moe_fused")) {
         const int prev = g_tune_moe_fused;
         g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
+        return prev;
+    }
+    if (!strcmp(key, "batch_decode_max")) {
+        const int prev = g_tune_batch_decode_max;
+        g_tune_batch_decode_max = value;
         return prev;
     }
     if (!strcmp(key, "mv_ks")) {
@@ -668,11 +676,61 @@ struct MoeLayer {
     DevBuf xq, xd, logits, ids, weights, stats;
     DevBuf g, aq, ad, dn;
     DevBuf est, slots, spec_ids;  // decode: logit estimates, hand-off words, act-row experts
+    // logits [cap_seq][n_expert], ids / weights / spec_ids [cap_seq][n_used],
+    // g [cap_seq][2][n_used][n_ff], est / slots [cap_seq][2][n_expert]
     // prefill scratch (grown on demand)
-    int cap_tok = 0, cap_seq = 0;
-    DevBuf b_logits, b_ids, b_w;  // batched decode routing
+    int cap_tok = 0, cap_seq = 1;  // prefill tokens; decode sequences (logits .. slots below)
     DevBuf p_xq, p_xd, p_grp_e, p_grp_s, p_grp_c, p_sub, p_slot, p_idx, p_g, p_u, p_aq, p_ad, p_dn;
 };
+
+// The decode kernels' arguments for this layer's scratch.
+MoeDecodeLaunch decode_launch(MoeLayer *m, const float *d_x, const float *d_res, float *d_out) {
+    MoeDecodeLaunch dl;
+    dl.w_gate = m->gate;
+    dl.w_up = m->upw;
+    dl.w_down = m->downw;
+    dl.gu_stride = m->sgu;
+    dl.down_stride = m->sd;
+    dl.router = m->router.as<float>();
+    dl.x = d_x;
+    dl.res = d_res;
+    dl.out = d_out;
+    dl.logits = m->logits.as<float>();
+    dl.est = m->est.as<double>();
+    dl.slots = m->slots.as<unsigned long long>();
+    dl.act = m->g.as<float>();
+    dl.spec_ids = m->spec_ids.as<int32_t>();
+    dl.ids_out = m->ids.as<int32_t>();
+    dl.w_out = m->weights.as<float>();
+    dl.stats = m->stats.as<int>();
+    dl.k = m->n_embd;
+    dl.n_expert = m->n_expert;
+    dl.n_used = m->n_used;
+    dl.n_ff = m->n_ff;
+    return dl;
+}
+
+// Decode scratch for nseq sequences (the stream is drained first: no queued
+// kernel still reads the old buffers). The hand-off words start empty.
+bool grow_decode(MoeLayer *m, int nseq) {
+    if (nseq <= m->cap_seq) return true;
+    if (!sync()) return false;
+    const size_t n = (size_t)nseq;
+    bool ok = m->logits.alloc(n * m->n_expert * 4) && m->ids.alloc(n * m->n_used * 4) &&
+              m->weights.alloc(n * m->n_used * 4) && m->spec_ids.alloc(n * m->n_used * 4) &&
+              m->g.alloc(n * 2 * m->n_used * m->n_ff * 4) && m->est.alloc(n * 2 * m->n_expert * 8) &&
+              m->slots.alloc(n * 2 * m->n_expert * 8);
+    if (ok) {
+        std::vector<unsigned long long> empty(n * 2 * m->n_expert, ~0ull);
+        ok = up(m->slots.p, empty.data(), empty.size() * 8) && sync();
+    }
+    if (!ok) {
+        m->cap_seq = 0;
+        return fail("moe: decode scratch for %d sequences could not be allocated", nseq) == 0;
+    }
+    m->cap_seq = nseq;
+    return true;
+}
 
 }  // namespace
 
@@ -752,28 +810,7 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
     rl.xblocks = m->be;
     if (g_tune_moe_fused == 2 && m->bf <= 8 && m->be <= 8) {
         // router and gate/up overlapped, then down + combine (moe_decode.hip)
-        MoeDecodeLaunch dl;
-        dl.w_gate = m->gate;
-        dl.w_up = m->upw;
-        dl.w_down = m->downw;
-        dl.gu_stride = m->sgu;
-        dl.down_stride = m->sd;
-        dl.router = m->router.as<float>();
-        dl.x = d_x;
-        dl.res = d_res;
-        dl.out = d_out;
-        dl.logits = m->logits.as<float>();
-        dl.est = m->est.as<double>();
-        dl.slots = m->slots.as<unsigned long long>();
-        dl.act = m->g.as<float>();
-        dl.spec_ids = m->spec_ids.as<int32_t>();
-        dl.ids_out = m->ids.as<int32_t>();
-        dl.w_out = m->weights.as<float>();
-        dl.stats = m->stats.as<int>();
-        dl.k = m->n_embd;
-        dl.n_expert = m->n_expert;
-        dl.n_used = m->n_used;
-        dl.n_ff = m->n_ff;
+        MoeDecodeLaunch dl = decode_launch(m, d_x, d_res, d_out);
         rc |= launch_moe_decode(dl, st);
         return rc ? fail("moe_forward: launch failed") : 0;
     }
@@ -928,36 +965,34 @@ int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, f
                                 int nseq) {
     MoeLayer *m = (MoeLayer *)h;
     if (!m || !d_x || !d_out || nseq <= 0) return fail("moe_forward_batch: bad arguments");
-    if (nseq > m->cap_seq) {
-        if (!sync()) return -1;
-        if (!m->b_logits.alloc((size_t)nseq * m->n_expert * 4) ||
-            !m->b_ids.alloc((size_t)nseq * m->n_used * 4) ||
-            !m->b_w.alloc((size_t)nseq * m->n_used * 4)) {
-            m->cap_seq = 0;
-            return fail("moe_forward_batch: allocation failed");
-        }
-        m->cap_seq = nseq;
-    }
+    if (!grow_decode(m, nseq)) return -1;
     hipStream_t st = stream();
+    if (nseq <= g_tune_batch_decode_max && m->bf <= 8 && m->be <= 8) {
+        // the decode kernels over the batch: per sequence, router fold beside
+        // gate/up, then down + ordered combine (two launches for the batch)
+        MoeDecodeLaunch dl = decode_launch(m, d_x, d_res, d_out);
+        dl.nseq = nseq;
+        return launch_moe_decode(dl, st) ? fail("moe_forward_batch: launch failed") : 0;
+    }
     // 1. the reference's router logits for every (sequence, expert), all folds at once
     RouterLaunch rl;
     rl.w = m->router.as<float>();
     rl.x = d_x;
     rl.n_expert = m->n_expert;
     rl.k = m->n_embd;
-    rl.logits = m->b_logits.as<float>();
+    rl.logits = m->logits.as<float>();
     rl.xq = nullptr;
     rl.xd = nullptr;
     rl.xblocks = 0;
     rl.nseq = nseq;
     int rc = launch_router(rl, st);
     // 2. softmax / top-k / renormalise per sequence
-    rc |= launch_route_logits(m->b_logits.as<float>(), m->n_expert, m->n_used, m->b_ids.as<int32_t>(),
-                              m->b_w.as<float>(), st, nseq);
+    rc |= launch_route_logits(m->logits.as<float>(), m->n_expert, m->n_used, m->ids.as<int32_t>(),
+                              m->weights.as<float>(), st, nseq);
     if (rc) return fail("moe_forward_batch: launch failed");
-    // 3. the experts, grouped across the sequences (weights read once per
-    //    16 tokens of an expert), combine + residual
-    return moe_grouped(m, d_x, m->b_ids.as<int32_t>(), m->b_w.as<float>(), d_res, d_out, nseq);
+    // 3. the experts grouped across the sequences (an expert's weights read
+    //    once per 16 tokens routed to it), combine + residual
+    return moe_grouped(m, d_x, m->ids.as<int32_t>(), m->weights.as<float>(), d_res, d_out, nseq);
 }
 
 int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, float *out,
@@ -974,9 +1009,9 @@ int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, 
                                     dout.as<float>(), nseq))
         return -1;
     if (!down(out, dout.p, nb)) return -1;
-    if (ids && !down(ids, m->b_ids.p, (size_t)nseq * m->n_used * 4)) return -1;
-    if (weights && !down(weights, m->b_w.p, (size_t)nseq * m->n_used * 4)) return -1;
-    if (logits && !down(logits, m->b_logits.p, (size_t)nseq * m->n_expert * 4)) return -1;
+    if (ids && !down(ids, m->ids.p, (size_t)nseq * m->n_used * 4)) return -1;
+    if (weights && !down(weights, m->weights.p, (size_t)nseq * m->n_used * 4)) return -1;
+    if (logits && !down(logits, m->logits.p, (size_t)nseq * m->n_expert * 4)) return -1;
     return sync() ? 0 : -1;
 }
 

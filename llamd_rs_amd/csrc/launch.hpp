@@ -70,6 +70,7 @@ struct MoeDecodeLaunch {
     float *w_out;
     int *stats;                     // [4]
     int k, n_expert, n_used, n_ff;
+    int nseq = 1;  // a batch: every per-token array holds nseq rows (moe_decode.hip for_seq)
 };
 int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st);
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,

@@ -58,8 +58,27 @@ struct DecodeParams {
     float *w_out;
     int *stats;                  // [4] calls, exact calls, certified calls, timed out
     size_t gu_stride, down_stride;
-    int k, n_expert, n_used, n_ff, gu_tiles, bf, down_tiles, n_chain, n_gu;
+    int k, n_expert, n_used, n_ff, gu_tiles, bf, down_tiles, n_chain, n_gu, nseq;
 };
+
+// The parameters of sequence `seq` of a batch: every per-token array offset
+// to that sequence's row (x, res, out [nseq][k]; logits [nseq][n_expert];
+// est, slots [nseq][2][n_expert]; act [nseq][n_used][n_ff]; spec_ids, ids_out,
+// w_out [nseq][n_used]).
+__device__ __forceinline__ DecodeParams for_seq(const DecodeParams &p, int seq) {
+    DecodeParams q = p;
+    q.x += (size_t)seq * p.k;
+    if (q.res) q.res += (size_t)seq * p.k;
+    q.out += (size_t)seq * p.k;
+    q.logits += (size_t)seq * p.n_expert;
+    q.est += (size_t)seq * 2 * p.n_expert;
+    q.slots += (size_t)seq * 2 * p.n_expert;
+    q.act += (size_t)seq * p.n_used * p.n_ff;
+    q.spec_ids += (size_t)seq * p.n_used;
+    q.ids_out += (size_t)seq * p.n_used;
+    q.w_out += (size_t)seq * p.n_used;
+    return q;
+}
 
 union DecodeLds {
     float4 prod[CHAIN_EXPERTS][KMAX / 4];
@@ -146,9 +165,9 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     return certain;
 }
 
-__device__ void chain_workgroup(const DecodeParams &p, DecodeLds &sm, int lane, int wave) {
+__device__ void chain_workgroup(const DecodeParams &p, DecodeLds &sm, int blk, int lane, int wave) {
     const int e = wave & 3;
-    const int row = (int)blockIdx.x * CHAIN_EXPERTS + e;
+    const int row = blk * CHAIN_EXPERTS + e;
     const int n4 = p.k / 4;
     if (wave < CHAIN_EXPERTS && row < p.n_expert) {
         const float4 *w4 = (const float4 *)(p.rw + (size_t)row * p.k);
@@ -194,8 +213,7 @@ __device__ void chain_workgroup(const DecodeParams &p, DecodeLds &sm, int lane, 
 // Gate and up of one (slot, tile): waves 0-3 split the gate row's blocks four
 // ways, waves 4-7 the up row's; the per-block terms meet in LDS and are folded
 // in block order (the same bits as one wave walking the row).
-__device__ void gateup_workgroup(const DecodeParams &p, DecodeLds &sm, int lane, int wave) {
-    const int g = (int)blockIdx.x - p.n_chain;
+__device__ void gateup_workgroup(const DecodeParams &p, DecodeLds &sm, int g, int lane, int wave) {
     const int slot = g / p.gu_tiles;
     const int t = g - slot * p.gu_tiles;
     const int half = wave >> 2, kc = wave & 3;
@@ -215,7 +233,7 @@ __device__ void gateup_workgroup(const DecodeParams &p, DecodeLds &sm, int lane,
         __builtin_amdgcn_s_setprio(0);
         if (g == 0 && lane < p.n_used) p.spec_ids[lane] = sm.g.rsh.sorted[lane];
         if (lane == 0 && p.stats) {
-            if (g == 0 && certain) p.stats[2] += 1;
+            if (g == 0 && certain) atomicAdd(&p.stats[2], 1);
             if (timed_out) p.stats[3] = 1;
         }
     }
@@ -288,8 +306,14 @@ __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
     __shared__ DecodeLds sm;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if ((int)blockIdx.x < p.n_chain) chain_workgroup(p, sm, lane, wave);
-    else gateup_workgroup(p, sm, lane, wave);
+    // all sequences' chain workgroups first (the gate/up ones wait on them)
+    const int b = blockIdx.x, chains = p.n_chain * p.nseq;
+    if (b < chains) {
+        chain_workgroup(for_seq(p, b / p.n_chain), sm, b % p.n_chain, lane, wave);
+    } else {
+        const int g = b - chains;
+        gateup_workgroup(for_seq(p, g / p.n_gu), sm, g % p.n_gu, lane, wave);
+    }
 }
 
 // Launch 2: wave e < n_used computes the tile for expert spec_ids[e] on act
@@ -298,7 +322,8 @@ __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
 // are combined in the reference's order:
 // out = res + (((0 + w0*y[ids0]) + w1*y[ids1]) + ...). Workgroup 0 writes the
 // routing out, counts the call and empties the hand-off words.
-__global__ __launch_bounds__(1024) void moe_down_route(DecodeParams p) {
+__global__ __launch_bounds__(1024) void moe_down_route(DecodeParams pb) {
+    const DecodeParams p = for_seq(pb, blockIdx.y);
     asm volatile("" ::"s"(p.w_down), "s"(p.down_stride), "s"(p.spec_ids), "s"(p.act), "s"(p.n_ff),
                  "s"(p.bf), "s"(p.n_used));
     __shared__ float ys[MAX_USED][TILE_ROWS];
@@ -393,8 +418,8 @@ __global__ __launch_bounds__(1024) void moe_down_route(DecodeParams p) {
                 p.w_out[lane] = rwt[lane];
             }
             if (lane == 0 && p.stats) {
-                p.stats[0] += 1;
-                p.stats[1] += 1;
+                atomicAdd(&p.stats[0], 1);
+                atomicAdd(&p.stats[1], 1);
             }
             for (int i = lane; i < 2 * p.n_expert; i += WAVE) p.slots[i] = SLOT_EMPTY;
         }
@@ -421,7 +446,7 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     if (l.k <= 0 || l.k % QK_K || l.k > KMAX || l.k / QK_K > GU_MAX_BLOCKS) return -1;
     if (l.n_ff <= 0 || l.n_ff % QK_K || l.n_ff / QK_K > DOWN_ACT_BLOCKS) return -1;
     if (l.n_expert <= 0 || l.n_expert > ROUTE_MAX_EXPERTS || l.n_used <= 0 ||
-        l.n_used > MAX_USED || l.n_used > l.n_expert)
+        l.n_used > MAX_USED || l.n_used > l.n_expert || l.nseq <= 0)
         return -1;
     DecodeParams p;
     p.w_gate = (const uint8_t *)l.w_gate;
@@ -450,9 +475,10 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     p.down_tiles = (l.k + TILE_ROWS - 1) / TILE_ROWS;
     p.n_chain = (l.n_expert + CHAIN_EXPERTS - 1) / CHAIN_EXPERTS;
     p.n_gu = l.n_used * p.gu_tiles;
-    hipLaunchKernelGGL(moe_router_gateup, dim3(p.n_chain + p.n_gu), dim3(512), 0, st, p);
+    p.nseq = l.nseq;
+    hipLaunchKernelGGL(moe_router_gateup, dim3((p.n_chain + p.n_gu) * l.nseq), dim3(512), 0, st, p);
     const int waves = l.n_used < MAX_USED ? l.n_used + 1 : MAX_USED;
-    hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles), dim3(64 * waves), 0, st, p);
+    hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles, l.nseq), dim3(64 * waves), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

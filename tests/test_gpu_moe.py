@@ -326,15 +326,22 @@ def test_decode_modes_bit_identical(gpu, qwen_layer, mode):
         lib().llamd_hip_tune(b"moe_fused", prev)
 
 
-@pytest.mark.parametrize("nseq", [1, 2, 5, 16])
-def test_batched_decode_equals_per_sequence_decode(gpu, qwen_layer, nseq):
-    """forward_batch: every sequence routed by its own exact logits, experts
-    grouped across the batch; each row bit-identical to the CPU's layer."""
+@pytest.mark.parametrize("path", ["decode", "grouped"])
+@pytest.mark.parametrize("nseq", [1, 2, 5, 16, 24])
+def test_batched_decode_equals_per_sequence_decode(gpu, qwen_layer, nseq, path):
+    """forward_batch: every sequence routed by its own exact logits -- through
+    the decode kernels (router fold beside gate/up, per sequence) or through
+    the expert-grouped kernels; each row bit-identical to the CPU's layer."""
     from llamd_rs_amd import synth
+    from llamd_rs_amd._lib import lib
     layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
     x = synth.normal(900 + nseq, 1.0, nseq * n_embd).reshape(nseq, n_embd)
     res = synth.normal(950 + nseq, 1.0, nseq * n_embd).reshape(nseq, n_embd)
-    out, ids, w, lg = layer.forward_batch(x, res)
+    prev = lib().llamd_hip_tune(b"batch_decode_max", 64 if path == "decode" else 0)
+    try:
+        out, ids, w, lg = layer.forward_batch(x, res)
+    finally:
+        lib().llamd_hip_tune(b"batch_decode_max", prev)
     for s in range(nseq):
         want, lgc, idc, wc = O.moe_layer(x[s], res[s], n_embd, n_ff, n_expert, n_used, router, gate,
                                          up, down)
@@ -344,7 +351,8 @@ def test_batched_decode_equals_per_sequence_decode(gpu, qwen_layer, nseq):
         assert bits_equal(out[s], want), s
 
 
-def test_batched_decode_shared_experts_and_ties(gpu):
+@pytest.mark.parametrize("path", ["decode", "grouped"])
+def test_batched_decode_shared_experts_and_ties(gpu, path):
     """A batch whose sequences share experts (same x twice), tie at the k-th
     place (identical router rows) and run without a residual."""
     from llamd_rs_amd import synth
@@ -358,7 +366,17 @@ def test_batched_decode_shared_experts_and_ties(gpu):
         x = synth.normal(931, 1.0, 6 * n_embd).reshape(6, n_embd)
         x[3] = x[0]
         x[4] = x[4] * np.sign(router[2] @ x[4]) * 4
-        out, ids, w, lg = layer.forward_batch(x)
+        from llamd_rs_amd._lib import lib
+        prev = lib().llamd_hip_tune(b"batch_decode_max", 64 if path == "decode" else 0)
+        try:
+            c0, _ = layer.counters()
+            out, ids, w, lg = layer.forward_batch(x)
+            c1, _ = layer.counters()
+        finally:
+            lib().llamd_hip_tune(b"batch_decode_max", prev)
+        if path == "decode":
+            assert c1[0] - c0[0] == 6 and c1[3] == 0
+            assert 0 < c1[2] - c0[2] < 6        # sequence 4 is not certified
         for s in range(6):
             want, lgc, idc, wc = O.moe_layer(x[s], np.zeros(n_embd, np.float32), n_embd, n_ff,
                                              n_expert, n_used, router, gate, up, down)
