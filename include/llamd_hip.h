@@ -315,6 +315,20 @@ void *llamd_gguf_upload_q6k(void *g, const char *name);
  * Q6_K) as llamd_hip_moe_create, n_used from <arch>.expert_used_count. */
 void *llamd_gguf_moe_create(void *g, int layer);
 
+/* ---- resident whole-token decode (Qwen3-MoE) ------------------------------ */
+/* DeviceModel::load / forward (crates/llamd-runtime/src/device.rs:262-722):
+ * every weight of a qwen3moe GGUF uploaded once (Q6_K attention, experts and
+ * output; F32 norms and router), a KV cache of max_kv positions (<= 16384),
+ * and one synchronisation per token. A step is bit-identical to the
+ * reference CPU composition (crates/llamd-runtime/src/layer.rs: forward).
+ * The GGUF handle may be closed after create. */
+void *llamd_hip_model_create(void *gguf, int max_kv);
+void llamd_hip_model_destroy(void *m);
+int llamd_hip_model_info(void *m, int *n_layer, int *n_embd, int *n_vocab, int *max_kv);
+/* One token at position pos (positions 0..pos-1 already in the cache):
+ * logits [n_vocab] and next = argmax (lowest index on ties), both optional. */
+int llamd_hip_model_forward(void *m, int token, int pos, float *logits, int32_t *next);
+
 #ifdef __cplusplus
 }
 #endif

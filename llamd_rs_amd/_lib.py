@@ -113,6 +113,10 @@ SIGNATURES = {
     "llamd_gguf_tensor_data": (vp, [vp, u64, vp]),
     "llamd_gguf_upload_q6k": (vp, [vp, cp]),
     "llamd_gguf_moe_create": (vp, [vp, i32]),
+    "llamd_hip_model_create": (vp, [vp, i32]),
+    "llamd_hip_model_destroy": (None, [vp]),
+    "llamd_hip_model_info": (i32, [vp, i32p, i32p, i32p, i32p]),
+    "llamd_hip_model_forward": (i32, [vp, i32, i32, vp, vp]),
     "llamd_hip_lmhead_create": (vp, [vp, i32, i32, i32]),
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),

@@ -46,8 +46,9 @@ DEVICE_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", f"-I{ROOT / 'include'}",
               f"-I{CSRC}"]
 
-HIP_SOURCES = ["q6k_mv.hip", "q8k.hip", "moe.hip", "moe_decode.hip", "group.hip", "norm.hip"]
-HOST_HIP_SOURCES = ["capi.cpp"]          # host code that calls the HIP runtime
+HIP_SOURCES = ["q6k_mv.hip", "q8k.hip", "moe.hip", "moe_decode.hip", "group.hip", "norm.hip",
+               "decode.hip"]
+HOST_HIP_SOURCES = ["capi.cpp", "model.cpp"]  # host code that calls the HIP runtime
 HOST_SOURCES = ["host/layout.cpp", "host/synth.cpp", "host/gguf.cpp"]
 
 

@@ -110,6 +110,18 @@ int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, in
 int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
                           float *inv_out, int n, float eps, hipStream_t st);
 
+// decode.hip: the whole-token step around the matvecs (token / position read
+// from device memory)
+int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st);
+int launch_rope_store(float *q, const float *k, const float *v, const float2 *cs,
+                      const int32_t *pos, int n_head, int n_head_kv, int hd, float *kc, float *vc,
+                      hipStream_t st);
+int attend_max_kv();
+int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
+                         int n_head, int n_head_kv, int hd, float scale, float *out,
+                         hipStream_t st);
+int launch_add_f32(const float *a, const float *b, float *out, int n, hipStream_t st);
+
 // moe.hip
 // The reference's router logits (sequential f32 fold per expert) and, in the
 // same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.

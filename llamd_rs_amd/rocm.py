@@ -492,3 +492,35 @@ __all__ = [
     "DeviceBuffer", "available", "device_count", "device_info", "quantize_q8k_on_device",
     "swiglu_q8k_on_device", "matvec_q6k", "route", "argmax", "HipError", "HipUnavailable",
 ]
+
+
+class DeviceModel:
+    """A resident Qwen3-MoE decode loop from a GGUF (DeviceModel::load /
+    forward, crates/llamd-runtime/src/device.rs:262-722): weights uploaded
+    once, KV cache for max_kv positions, one synchronisation per token."""
+
+    def __init__(self, gguf, max_kv: int):
+        self._h = check_ptr(lib().llamd_hip_model_create(gguf._h, max_kv), "model_create")
+        a, b, c, d = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        check(lib().llamd_hip_model_info(self._h, C.byref(a), C.byref(b), C.byref(c), C.byref(d)),
+              "model_info")
+        self.n_layer, self.n_embd, self.n_vocab, self.max_kv = a.value, b.value, c.value, d.value
+
+    def forward(self, token: int, pos: int):
+        """(logits [n_vocab], next token = argmax) for `token` at `pos`."""
+        logits = np.empty(self.n_vocab, np.float32)
+        nxt = np.zeros(1, np.int32)
+        check(lib().llamd_hip_model_forward(self._h, int(token), int(pos), _ptr(logits), _ptr(nxt)),
+              "model_forward")
+        return logits, int(nxt[0])
+
+    def close(self):
+        if self._h:
+            lib().llamd_hip_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -22,6 +22,13 @@
  *   orc_moe_ffn/_layer    composition; float64 restatement bound
  *   orc_argmax            closed form incl. ties
  *   orc_moe_ffn_tokens    composition of orc_moe_ffn per token
+ *   orc_rope              reference known answers (llamd-cpu lib.rs:313-357:
+ *                         position 0 identity, pairs across the half boundary,
+ *                         pair norms kept) + float64 rotation bound
+ *   orc_attend            reference known answers (attention.rs tests: one
+ *                         position returns v, convex combination, GQA by
+ *                         integer division, scale 1/sqrt(hd), no overflow) +
+ *                         float64 restatement bound
  * Nothing here is "parity unpinned"; the Q6_K/Q8_0 weight QUANTIZERS (input
  * generators, not part of the reference) live with the synthetic-data code.
  */
@@ -452,4 +459,65 @@ int orc_close(float a, float b, float tol) {
     float diff = fabsf(a - b);
     float scale = fmaxf(fmaxf(fabsf(a), fabsf(b)), 1.0f);
     return diff / scale <= tol;
+}
+
+/* CpuBackend::rope (crates/llamd-cpu/src/lib.rs:158-209), NeoX pairing, in
+ * place over `heads` heads of `hd` values at position `pos`:
+ *   theta = (pos * freq_scale) / powf(base, (2 * i) / hd)
+ *   x[i] = a*cos - b*sin,  x[i + hd/2] = a*sin + b*cos   (a = x[i], b = x[i+hd/2])
+ * with Rust's f32 powf / sin / cos, i.e. glibc's powf, sinf, cosf. */
+void orc_rope(float *x, int heads, int hd, uint32_t pos, float base) {
+    const int half = hd / 2;
+    const float p = (float)pos * 1.0f;
+    for (int h = 0; h < heads; ++h) {
+        float *v = x + (size_t)h * hd;
+        for (int i = 0; i < half; ++i) {
+            const float exponent = 2.0f * (float)i / (float)hd;
+            const float theta = p / powf(base, exponent);
+            const float sn = sinf(theta), cs = cosf(theta);
+            const float a = v[i], b = v[i + half];
+            v[i] = a * cs - b * sn;
+            v[i + half] = a * sn + b * cs;
+        }
+    }
+}
+
+/* attend (crates/llamd-runtime/src/attention.rs:73-125): for each head h
+ * (kv head h / (n_head / n_head_kv)):
+ *   logit_t = (sum_d q[d] * k_t[d], in order from 0.0) * (1 / sqrt(hd))
+ *   max fold; e_t = expf(logit_t - max); sum in order from 0.0; inv = 1 / sum
+ *   out[d] = sum_t (e_t * inv) * v_t[d], in order from 0.0
+ * k, v: [n_kv][n_head_kv * hd]; q, out: [n_head * hd]. */
+int orc_attend(const float *q, const float *k, const float *v, int n_kv, int n_head,
+               int n_head_kv, int hd, float *out) {
+    if (n_head_kv <= 0 || n_head % n_head_kv || hd <= 0 || n_kv <= 0) return -1;
+    const int kv_dim = n_head_kv * hd, ratio = n_head / n_head_kv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *logits = (float *)malloc((size_t)n_kv * sizeof(float));
+    if (!logits) return -1;
+    for (int i = 0; i < n_head * hd; ++i) out[i] = 0.0f;
+    for (int h = 0; h < n_head; ++h) {
+        const int kvh = h / ratio, qo = h * hd;
+        for (int t = 0; t < n_kv; ++t) {
+            const float *kr = k + (size_t)t * kv_dim + (size_t)kvh * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot += q[qo + d] * kr[d];
+            logits[t] = dot * scale;
+        }
+        float mx = -INFINITY;
+        for (int t = 0; t < n_kv; ++t) mx = fmaxf(mx, logits[t]);
+        float sum = 0.0f;
+        for (int t = 0; t < n_kv; ++t) {
+            logits[t] = expf(logits[t] - mx);
+            sum += logits[t];
+        }
+        const float inv = 1.0f / sum;
+        for (int t = 0; t < n_kv; ++t) {
+            const float w = logits[t] * inv;
+            const float *vr = v + (size_t)t * kv_dim + (size_t)kvh * hd;
+            for (int d = 0; d < hd; ++d) out[qo + d] += w * vr[d];
+        }
+    }
+    free(logits);
+    return 0;
 }

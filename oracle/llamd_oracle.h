@@ -126,6 +126,12 @@ int orc_moe_ffn_tokens(const float *x, size_t n_tok, size_t n_embd, size_t n_ff,
 /* tolerance.rs:116-151 */
 int orc_close(float a, float b, float tol);
 
+/* CpuBackend::rope, in place (llamd-cpu/src/lib.rs:158-209) */
+void orc_rope(float *x, int heads, int hd, uint32_t pos, float base);
+/* attend (llamd-runtime/src/attention.rs:73-125) */
+int orc_attend(const float *q, const float *k, const float *v, int n_kv, int n_head,
+               int n_head_kv, int hd, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,8 @@ def _lib():
             "orc_argmax": (u32, [vp, sz]),
             "orc_moe_ffn_tokens": (C.c_int, [vp, sz, sz, sz, sz, vp, vp, vp, vp, vp, sz, vp]),
             "orc_close": (C.c_int, [f, f, f]),
+            "orc_rope": (None, [vp, C.c_int, C.c_int, u32, f]),
+            "orc_attend": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -261,3 +263,22 @@ def max_deviation(a, b):
         if d[i] > 0:
             worst = (i, float(d[i]))
     return worst
+
+
+def rope(x, heads: int, hd: int, pos: int, base: float) -> np.ndarray:
+    """CpuBackend::rope (llamd-cpu/src/lib.rs:158-209), NeoX pairs (i, i + hd/2)."""
+    y = np.array(_f32(x), np.float32, copy=True)
+    if y.size != heads * hd or hd % 2:
+        raise ValueError("x must be [heads, hd] with hd even")
+    _lib().orc_rope(_p(y), heads, hd, pos, base)
+    return y
+
+
+def attend(q, k, v, n_kv: int, n_head: int, n_head_kv: int, hd: int) -> np.ndarray:
+    """attend (llamd-runtime/src/attention.rs:73-125); k, v [n_kv][n_head_kv*hd]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.empty(n_head * hd, np.float32)
+    if (q.size != n_head * hd or k.size != n_kv * n_head_kv * hd or v.size != k.size or
+            _lib().orc_attend(_p(q), _p(k), _p(v), n_kv, n_head, n_head_kv, hd, _p(out))):
+        raise ValueError("attend: shape or grouping violation")
+    return out

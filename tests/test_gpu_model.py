@@ -1,0 +1,54 @@
+"""The resident whole-token decode loop (llamd_hip_model_*) on a small
+Qwen3-MoE written as GGUF: every token's logits and argmax bit-identical to
+the reference CPU forward (crates/llamd-runtime/src/layer.rs:268-304)
+composed from the oracle."""
+import numpy as np
+import pytest
+
+import model_fixture as MF
+
+pytestmark = pytest.mark.gpu
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path):
+    from llamd_rs_amd.gguf import Gguf
+    p = tmp_path / "tiny.gguf"
+    w = MF.make(p, seed=3)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=32)
+    ref = MF.OracleModel(w)
+    try:
+        assert (dm.n_layer, dm.n_embd, dm.n_vocab) == (2, 512, 768)
+        tok = 5
+        for pos in range(10):
+            logits, nxt = dm.forward(tok, pos)
+            want, want_next = ref.forward(tok, pos)
+            assert bits_equal(logits, want), pos
+            assert nxt == want_next, pos
+            tok = nxt if pos % 3 else (tok * 37 + 11) % 768   # greedy, with some forced tokens
+    finally:
+        dm.close()
+
+
+def test_decode_loop_refuses_bad_tokens_and_positions(gpu, tmp_path):
+    from llamd_rs_amd._lib import HipError
+    from llamd_rs_amd.gguf import Gguf
+    p = tmp_path / "tiny.gguf"
+    MF.make(p, seed=4)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=8)
+    try:
+        with pytest.raises(HipError, match="vocabulary"):
+            dm.forward(768, 0)
+        with pytest.raises(HipError, match="beyond"):
+            dm.forward(1, 8)
+        logits, nxt = dm.forward(1, 0)
+        assert np.all(np.isfinite(logits)) and 0 <= nxt < 768
+    finally:
+        dm.close()
