@@ -504,6 +504,38 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     for st_ in sets:
         for d_ in st_:
             d_.close()
+    # resident whole-token decode, Qwen3-30B-A3B shapes (48 layers, 128
+    # experts, 151936 vocab): a synthetic GGUF whose layers share one copy of
+    # their data in the file; each layer is a separate ~0.49 GB upload
+    import tempfile
+    from llamd_rs_amd import synth_model
+    from llamd_rs_amd.gguf import Gguf
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        t0 = time.time()
+        synth_model.write_model(path)
+        with Gguf(path) as g:
+            dm = rocm.DeviceModel(g, max_kv=1024)
+        t_load = time.time() - t0
+    finally:
+        os.unlink(path)
+    tok = 1
+    for pos in range(3):
+        _, tok = dm.forward(tok, pos)
+    n = 64
+    t0 = time.perf_counter()
+    for pos in range(3, 3 + n):
+        _, tok = dm.forward(tok, pos)
+    dt = time.perf_counter() - t0
+    out["decode_token"] = {"model": "Qwen3-30B-A3B-shaped (48 layers, 128 experts top-8, vocab 151936), "
+                                    "synthetic Q6_K weights",
+                           "us_per_token": dt / n * 1e6, "tok_s": n / dt, "tokens": n,
+                           "positions": f"3..{2 + n}", "load_s": round(t_load, 1),
+                           "per_call": "host call incl. logits download and one sync",
+                           "parity": "bit-identical to the CPU forward (tests/test_gpu_model.py)"}
+    log(f"  decode token: {out['decode_token']}")
+    dm.close()
     return out
 
 

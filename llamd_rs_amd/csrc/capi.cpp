@@ -36,6 +36,9 @@ int g_tune_moe_fused = 2;
 // batched decode: up to this many sequences through the decode kernels, more
 // through the expert-grouped (prefill) kernels
 int g_tune_batch_decode_max = 16;
+}  // namespace
+int llamd::g_tune_model_graph = 1;  // whole-token decode replays a captured graph
+namespace {
 
 int fail(const char *fmt, ...) {
     va_list ap;
@@ -152,6 +155,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "moe_fused")) {
         const int prev = g_tune_moe_fused;
         g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
+        return prev;
+    }
+    if (!strcmp(key, "model_graph")) {
+        const int prev = g_tune_model_graph;
+        g_tune_model_graph = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "batch_decode_max")) {

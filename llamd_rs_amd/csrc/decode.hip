@@ -129,7 +129,18 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     for (int d = tid; d < hd; d += blockDim.x) {
         const float *vr = vc + (size_t)kvh * hd + d;
         float acc = 0.0f;
-        for (int t = 0; t < n_kv; ++t) {
+        int t = 0;
+        for (; t + 8 <= n_kv; t += 8) {
+            float vv[8];  // eight loads in flight, then the eight ordered adds
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * kv_dim];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float w = lg[t + j] * inv;
+                acc = acc + w * vv[j];
+            }
+        }
+        for (; t < n_kv; ++t) {
             const float w = lg[t] * inv;
             acc = acc + w * vr[(size_t)t * kv_dim];
         }

@@ -11,7 +11,8 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
-extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
+extern int g_tune_mv_ks;
+extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from

@@ -50,6 +50,8 @@ struct Model {
     int8_t *aq = nullptr;
     float *ad = nullptr;
     int32_t *tokpos = nullptr, *next = nullptr;
+    hipGraphExec_t exec = nullptr;  // the captured step
+    bool use_graph = true;
     std::vector<void *> owned;     // device allocations to free
 };
 
@@ -77,9 +79,41 @@ float *upload_f32(Model &m, void *g, const std::string &name, uint64_t n) {
     return d;
 }
 
+// Every launch of one token's step (embedding .. argmax) on stream st; the
+// token and position come from m->tokpos.
+bool enqueue_step(Model *m, hipStream_t st) {
+    const int E = m->n_embd, eb = E / 256, qdim = m->n_head * m->hd, kv_dim = m->n_head_kv * m->hd;
+    int rc = llamd::launch_embed_q6k(m->tok_embd, m->tokpos, eb, m->x, st);
+    for (int il = 0; il < m->n_layer && !rc; ++il) {
+        Layer &l = m->layers[il];
+        // attn_norm = rms_norm(x) * w, quantized once for Q, K and V
+        llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
+        llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb, qdim,
+                            kv_dim, kv_dim);
+        // QK-norm per head, before RoPE (layer.rs:113-136)
+        if (l.q_norm) llamd_fwd_head_rms_norm_mul(m->q, l.q_norm, m->q, m->n_head, m->hd, m->eps);
+        if (l.k_norm) llamd_fwd_head_rms_norm_mul(m->k, l.k_norm, m->k, m->n_head_kv, m->hd, m->eps);
+        rc |= llamd::launch_rope_store(m->q, m->k, m->v, m->rope, m->tokpos + 1, m->n_head,
+                                       m->n_head_kv, m->hd, l.kc, l.vc, st);
+        rc |= llamd::launch_attend_decode(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head, m->n_head_kv,
+                                          m->hd, m->scale, m->attn, st);
+        // O projection, residual
+        llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
+        llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
+        rc |= llamd::launch_add_f32(m->x, m->o, m->ffn_inp, E, st);
+        // ffn_norm, then the MoE FFN with the second residual: x = ffn_inp + moe
+        llamd_fwd_rms_norm_mul(m->ffn_inp, l.ffn_norm, m->fn, E, m->eps);
+        rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
+    }
+    if (rc || llamd_fwd_last_error()) return set_error("model: a launch failed (%s)", llamd_hip_last_error()) == 0;
+    llamd_fwd_rms_norm_mul(m->x, m->output_norm, m->xn, E, m->eps);
+    return llamd_hip_lmhead_forward(m->lmhead, m->xn, 1, m->logits, m->next) == 0;
+}
+
 void destroy(Model *m) {
     if (!m) return;
     (void)llamd_fwd_sync();
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->lmhead) llamd_hip_lmhead_destroy(m->lmhead);
     for (Layer &l : m->layers) {
         if (l.moe) llamd_hip_moe_destroy(l.moe);
@@ -153,6 +187,7 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->hd = (int)hd;
     m->n_vocab = (int)edims[1];
     m->max_kv = max_kv;
+    m->use_graph = llamd::g_tune_model_graph != 0;
     m->eps = eps;
     m->rope_base = base;
     m->scale = 1.0f / sqrtf((float)hd);  // attention.rs:95
@@ -274,32 +309,28 @@ int llamd_hip_model_forward(void *h, int token, int pos, float *logits, int32_t 
     hipStream_t st = (hipStream_t)llamd_fwd_get_stream();
     const int32_t tp[2] = {token, pos};
     if (llamd_fwd_upload(m->tokpos, tp, sizeof tp)) return -1;
-    const int E = m->n_embd, eb = E / 256, qdim = m->n_head * m->hd, kv_dim = m->n_head_kv * m->hd;
-    int rc = llamd::launch_embed_q6k(m->tok_embd, m->tokpos, eb, m->x, st);
-    for (int il = 0; il < m->n_layer && !rc; ++il) {
-        Layer &l = m->layers[il];
-        // attn_norm = rms_norm(x) * w, quantized once for Q, K and V
-        llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
-        llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb, qdim,
-                            kv_dim, kv_dim);
-        // QK-norm per head, before RoPE (layer.rs:113-136)
-        if (l.q_norm) llamd_fwd_head_rms_norm_mul(m->q, l.q_norm, m->q, m->n_head, m->hd, m->eps);
-        if (l.k_norm) llamd_fwd_head_rms_norm_mul(m->k, l.k_norm, m->k, m->n_head_kv, m->hd, m->eps);
-        rc |= llamd::launch_rope_store(m->q, m->k, m->v, m->rope, m->tokpos + 1, m->n_head,
-                                       m->n_head_kv, m->hd, l.kc, l.vc, st);
-        rc |= llamd::launch_attend_decode(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head, m->n_head_kv,
-                                          m->hd, m->scale, m->attn, st);
-        // O projection, residual
-        llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
-        llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
-        rc |= llamd::launch_add_f32(m->x, m->o, m->ffn_inp, E, st);
-        // ffn_norm, then the MoE FFN with the second residual: x = ffn_inp + moe
-        llamd_fwd_rms_norm_mul(m->ffn_inp, l.ffn_norm, m->fn, E, m->eps);
-        rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
+    // The step reads token and position from device memory, so its launches
+    // are the same for every token: captured once into a HIP graph, replayed
+    // per token (no per-launch host work). If capture is refused, the step
+    // runs as plain launches.
+    if (!m->exec && m->use_graph) {
+        hipGraph_t graph = nullptr;
+        bool ok = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        const bool enq = ok && enqueue_step(m, st);
+        ok = hipStreamEndCapture(st, &graph) == hipSuccess && ok && enq;
+        ok = ok && hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0) == hipSuccess;
+        if (graph) (void)hipGraphDestroy(graph);
+        if (!ok) {
+            m->exec = nullptr;
+            m->use_graph = false;
+            (void)hipGetLastError();
+        }
     }
-    if (rc || llamd_fwd_last_error()) return set_error("model: a launch failed (%s)", llamd_hip_last_error());
-    llamd_fwd_rms_norm_mul(m->x, m->output_norm, m->xn, E, m->eps);
-    if (llamd_hip_lmhead_forward(m->lmhead, m->xn, 1, m->logits, m->next)) return -1;
+    if (m->exec) {
+        if (hipGraphLaunch(m->exec, st) != hipSuccess) return set_error("model: graph launch failed");
+    } else if (!enqueue_step(m, st)) {
+        return -1;
+    }
     if (logits && llamd_fwd_download(logits, m->logits, (size_t)m->n_vocab * 4)) return -1;
     if (next && llamd_fwd_download(next, m->next, 4)) return -1;
     return llamd_fwd_sync() ? -1 : 0;

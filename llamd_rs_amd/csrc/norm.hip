@@ -27,9 +27,38 @@ constexpr int NORM_MAX = 8192;  // elements of one row held in LDS
 // Returns scale on every lane of the wave.
 __device__ float row_scale_wave(const float *src, int n, float eps, float *sq) {
     const int lane = threadIdx.x & 63;
-    for (int i = lane; i < n; i += WAVE) {
-        const float v = src[i];
-        sq[i] = v * v;
+    // every load of the row in flight before the first square is stored (a
+    // loop of dependent load -> store would pay one memory latency per step)
+    if ((n & 3) == 0 && ((uintptr_t)src & 15) == 0) {
+        for (int base = 0; base < n; base += 8 * 4 * WAVE) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + 4 * (j * WAVE + lane);
+                if (i < n) v[j] = *(const float4 *)(src + i);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + 4 * (j * WAVE + lane);
+                if (i < n)
+                    *(float4 *)(sq + i) = make_float4(v[j].x * v[j].x, v[j].y * v[j].y,
+                                                       v[j].z * v[j].z, v[j].w * v[j].w);
+            }
+        }
+    } else {
+        for (int base = 0; base < n; base += 8 * WAVE) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + j * WAVE + lane;
+                if (i < n) v[j] = src[i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + j * WAVE + lane;
+                if (i < n) sq[i] = v[j] * v[j];
+            }
+        }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -70,9 +99,26 @@ __global__ __launch_bounds__(256) void rms_norm_mul(const float *x, const float 
     }
     __syncthreads();
     const float scale = sc;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = src[i] * scale;
-        out[(size_t)r * n + i] = w ? v * w[i % w_len] : v;
+    float *dst = out + (size_t)r * n;
+    // four loads of x (and w) in flight per thread before the stores
+    for (int base = 0; base < n; base += 4 * blockDim.x) {
+        float xv[4], wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            if (i < n) {
+                xv[j] = src[i];
+                wv[j] = w ? w[w_len == n ? i : i % w_len] : 1.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            if (i < n) {
+                const float v = xv[j] * scale;
+                dst[i] = w ? v * wv[j] : v;
+            }
+        }
     }
 }
 

@@ -1,8 +1,10 @@
-"""A small GGUF v3 writer for test fixtures (ggml/include/gguf.h layout).
+"""A small GGUF v3 writer (ggml/include/gguf.h layout).
 
-Test infrastructure only: it writes files whose every byte the tests know, so
-the reader can be checked field by field, and it can be told to write the
-malformed headers the reader must refuse.
+For synthetic models: the tests write files whose every byte they know (and
+the malformed headers the reader must refuse), and bench.py writes a
+Qwen3-30B-A3B-shaped model whose layers share one copy of their data (tensor
+infos may point at the same offset: a data object passed twice, the same
+Python object, is stored once).
 """
 from __future__ import annotations
 
@@ -36,13 +38,16 @@ def build(kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"
                                len(tensors) if n_tensors is None else n_tensors,
                                len(kvs) if n_kv is None else n_kv)
     body = b"".join(gstr(k) + struct.pack("<I", t) + value(t, v) for k, t, v in kvs)
-    infos, datas, off = [], [], 0
+    infos, datas, off, placed = [], [], 0, {}
     for name, dims, ty, data in tensors:
-        off = -(-off // alignment) * alignment
+        at = placed.get(id(data))
+        if at is None:
+            off = -(-off // alignment) * alignment
+            at = placed[id(data)] = off
+            datas.append((off, data))
+            off += len(data)
         infos.append(gstr(name) + struct.pack("<I", len(dims)) +
-                     b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", ty, off))
-        datas.append((off, data))
-        off += len(data)
+                     b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", ty, at))
     header = head + body + b"".join(infos)
     pad = -len(header) % alignment
     section = bytearray(off)
@@ -51,8 +56,6 @@ def build(kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"
     return header + b"\0" * pad + bytes(section) + tail
 
 
-def write(path, *args, **kw) -> bytes:
-    b = build(*args, **kw)
+def write(path, *args, **kw) -> None:
     with open(path, "wb") as f:
-        f.write(b)
-    return b
+        f.write(build(*args, **kw))

@@ -6,7 +6,7 @@ from __future__ import annotations
 
 import numpy as np
 
-import gguf_writer as W
+from llamd_rs_amd import gguf_writer as W
 from oracle import oracle as O
 
 HP = dict(n_layer=2, n_embd=512, n_head=4, n_head_kv=2, hd=128, n_expert=8, n_used=2, n_ff=256,

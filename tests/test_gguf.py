@@ -9,7 +9,7 @@ import struct
 import numpy as np
 import pytest
 
-import gguf_writer as W
+from llamd_rs_amd import gguf_writer as W
 from llamd_rs_amd._lib import HipError, lib
 
 try:
@@ -201,3 +201,16 @@ def test_moe_layer_from_a_gguf_file_refuses_bad_shapes(tmp_path):
             g.moe_layer(0)
         with pytest.raises(HipError, match="lacks"):
             g.moe_layer(1)
+
+
+def test_tensors_may_share_their_data(tmp_path):
+    """Tensor infos are offsets: two tensors may point at the same bytes (the
+    writer stores a repeated data object once)."""
+    data = rng_bytes(210 * 4, 9)
+    p = tmp_path / "shared.gguf"
+    W.write(p, [], [("a", [256, 4], 14, data), ("b", [256, 4], 14, data), ("c", [256], 14, data[:210])])
+    g = open_gguf(p)
+    ta, tb, tc = g.tensors
+    assert ta.offset == tb.offset != tc.offset
+    assert bytes(g.tensor_data(ta)) == bytes(g.tensor_data(tb)) == data
+    assert g.file_size() < g.data_offset + 3 * len(data)

@@ -4,7 +4,7 @@ built from blk.0's tensors give the CPU path's bits."""
 import numpy as np
 import pytest
 
-import gguf_writer as W
+from llamd_rs_amd import gguf_writer as W
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
