@@ -1,6 +1,6 @@
 // decode.hip -- the pieces of a whole-token decode step around the
-// quantized matvecs: embedding row, RoPE + KV-cache store, attention over the
-// cache, residual add. Each reproduces the reference CPU path's f32
+// quantized matvecs: embedding row and attention over the KV cache (QK-norm,
+// RoPE and the cache store are in norm.hip, beside the norms they fuse with). Each reproduces the reference CPU path's f32
 // operations in its order, so a step is bit-identical to
 // crates/llamd-runtime/src/layer.rs:forward (single token, single sequence).
 //
@@ -37,43 +37,6 @@ __global__ __launch_bounds__(64) void embed_q6k(const uint8_t *table, const int3
     y[l + 32] = d * (float)sc[is + 2] * (float)q2;
     y[l + 64] = d * (float)sc[is + 4] * (float)q3;
     y[l + 96] = d * (float)sc[is + 6] * (float)q4;
-}
-
-// CpuBackend::rope (crates/llamd-cpu/src/lib.rs:158-209) on Q (in place) and
-// K, then K and V into the cache row of this position (kv.rs:121-150).
-// cs[pos][i] = (cos, sin) of theta = pos / powf(base, 2i/hd), computed on the
-// host with the same libm calls as the reference; here only
-//   x[i] = a*cos - b*sin,  x[i + hd/2] = a*sin + b*cos   (no FMA).
-__global__ __launch_bounds__(256) void rope_store(float *q, const float *k, const float *v,
-                                                  const float2 *cs, const int32_t *pos_p,
-                                                  int n_head, int n_head_kv, int hd, float *kc,
-                                                  float *vc) {
-    const int half = hd / 2, pos = pos_p[0];
-    const int kv_dim = n_head_kv * hd;
-    const float2 *row = cs + (size_t)pos * half;
-    const int nq = n_head * half, nk = n_head_kv * half;
-    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < nq + nk + kv_dim;
-         j += gridDim.x * blockDim.x) {
-        if (j < nq + nk) {
-            const bool isq = j < nq;
-            const int jj = isq ? j : j - nq;
-            const int h = jj / half, i = jj - h * half;
-            const float *src = isq ? q : k;
-            const float a = src[h * hd + i], b = src[h * hd + i + half];
-            const float2 c = row[i];
-            const float lo = a * c.x - b * c.y, hi = a * c.y + b * c.x;
-            if (isq) {
-                q[h * hd + i] = lo;
-                q[h * hd + i + half] = hi;
-            } else {
-                kc[(size_t)pos * kv_dim + h * hd + i] = lo;
-                kc[(size_t)pos * kv_dim + h * hd + i + half] = hi;
-            }
-        } else {
-            const int e = j - nq - nk;
-            vc[(size_t)pos * kv_dim + e] = v[e];
-        }
-    }
 }
 
 constexpr int ATT_MAX_KV = 16384;  // positions whose logits fit in LDS
@@ -148,27 +111,12 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     }
 }
 
-__global__ void add_f32(const float *a, const float *b, float *out, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = a[i] + b[i];
-}
-
 }  // namespace
 
 int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st) {
     if (blocks <= 0) return -1;
     hipLaunchKernelGGL(embed_q6k, dim3(blocks), dim3(64), 0, st, (const uint8_t *)table, tok, blocks,
                        out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-int launch_rope_store(float *q, const float *k, const float *v, const float2 *cs,
-                      const int32_t *pos, int n_head, int n_head_kv, int hd, float *kc, float *vc,
-                      hipStream_t st) {
-    if (hd <= 0 || hd % 2 || n_head <= 0 || n_head_kv <= 0) return -1;
-    const int n = (n_head + n_head_kv) * hd / 2 + n_head_kv * hd;
-    hipLaunchKernelGGL(rope_store, dim3((n + 255) / 256), dim3(256), 0, st, q, k, v, cs, pos, n_head,
-                       n_head_kv, hd, kc, vc);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -180,11 +128,6 @@ int launch_attend_decode(const float *q, const float *kc, const float *vc, const
     if (hd <= 0 || hd % 4 || hd > 256 || n_head_kv <= 0 || n_head % n_head_kv) return -1;
     hipLaunchKernelGGL(attend_decode, dim3(n_head), dim3(256), 0, st, q, kc, vc, pos, n_head,
                        n_head_kv, hd, scale, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-int launch_add_f32(const float *a, const float *b, float *out, int n, hipStream_t st) {
-    hipLaunchKernelGGL(add_f32, dim3((n + 255) / 256), dim3(256), 0, st, a, b, out, n);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

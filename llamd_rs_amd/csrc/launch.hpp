@@ -114,14 +114,19 @@ int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs
 // decode.hip: the whole-token step around the matvecs (token / position read
 // from device memory)
 int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st);
-int launch_rope_store(float *q, const float *k, const float *v, const float2 *cs,
-                      const int32_t *pos, int n_head, int n_head_kv, int hd, float *kc, float *vc,
-                      hipStream_t st);
 int attend_max_kv();
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
                          int n_head, int n_head_kv, int hd, float scale, float *out,
                          hipStream_t st);
-int launch_add_f32(const float *a, const float *b, float *out, int n, hipStream_t st);
+
+// norm.hip, decode step: per-head QK-norm (w null: none) + RoPE, Q in place,
+// K and V into the cache row of *pos; and ffn_inp = x + o, out = rms_norm(ffn_inp) * w.
+int launch_qk_norm_rope_store(float *q, const float *k, const float *v, const float *qw,
+                              const float *kw, const float2 *cs, const int32_t *pos, int n_head,
+                              int n_head_kv, int hd, float eps, float *kc, float *vc,
+                              hipStream_t st);
+int launch_add_rms_norm_mul(const float *x, const float *o, const float *w, float *sum_out,
+                            float *out, int n, float eps, hipStream_t st);
 
 // moe.hip
 // The reference's router logits (sequential f32 fold per expert) and, in the

@@ -90,19 +90,18 @@ bool enqueue_step(Model *m, hipStream_t st) {
         llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
         llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb, qdim,
                             kv_dim, kv_dim);
-        // QK-norm per head, before RoPE (layer.rs:113-136)
-        if (l.q_norm) llamd_fwd_head_rms_norm_mul(m->q, l.q_norm, m->q, m->n_head, m->hd, m->eps);
-        if (l.k_norm) llamd_fwd_head_rms_norm_mul(m->k, l.k_norm, m->k, m->n_head_kv, m->hd, m->eps);
-        rc |= llamd::launch_rope_store(m->q, m->k, m->v, m->rope, m->tokpos + 1, m->n_head,
-                                       m->n_head_kv, m->hd, l.kc, l.vc, st);
+        // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append
+        rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
+                                               m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
+                                               m->eps, l.kc, l.vc, st);
         rc |= llamd::launch_attend_decode(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head, m->n_head_kv,
                                           m->hd, m->scale, m->attn, st);
         // O projection, residual
         llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
         llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
-        rc |= llamd::launch_add_f32(m->x, m->o, m->ffn_inp, E, st);
-        // ffn_norm, then the MoE FFN with the second residual: x = ffn_inp + moe
-        llamd_fwd_rms_norm_mul(m->ffn_inp, l.ffn_norm, m->fn, E, m->eps);
+        // ffn_inp = x + O, ffn_norm; then the MoE FFN with the second
+        // residual: x = ffn_inp + moe
+        rc |= llamd::launch_add_rms_norm_mul(m->x, m->o, l.ffn_norm, m->ffn_inp, m->fn, E, m->eps, st);
         rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
     }
     if (rc || llamd_fwd_last_error()) return set_error("model: a launch failed (%s)", llamd_hip_last_error()) == 0;

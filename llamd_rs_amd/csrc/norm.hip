@@ -151,7 +151,83 @@ __global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const flo
     }
 }
 
+// Per-head QK-norm, RoPE and the KV-cache store of one decode step, one
+// workgroup (one wave) per head: Q heads [0, n_head) in place, K heads after
+// them into the cache row of this position, with V copied beside them.
+//   norm: out = (x * scale) * w            (layer.rs:62-79; skipped if w is null)
+//   RoPE: x[i] = a*cos - b*sin, x[i + hd/2] = a*sin + b*cos   (lib.rs:196-205)
+// cs[pos][i] = (cos, sin), computed on the host with the reference's libm calls.
+__global__ __launch_bounds__(64) void qk_norm_rope_store(float *q, const float *k, const float *v,
+                                                         const float *qw, const float *kw,
+                                                         const float2 *cs, const int32_t *pos_p,
+                                                         int n_head, int n_head_kv, int hd,
+                                                         float eps, float *kc, float *vc) {
+    __shared__ __align__(16) float sq[256];
+    __shared__ float buf[256];
+    const int lane = threadIdx.x, h = blockIdx.x, half = hd / 2, pos = pos_p[0];
+    const bool isq = h < n_head;
+    const int hh = isq ? h : h - n_head;
+    const float *src = isq ? q + (size_t)hh * hd : k + (size_t)hh * hd;
+    const float *w = isq ? qw : kw;
+    const int kv_dim = n_head_kv * hd;
+    if (w) {
+        const float scale = row_scale_wave(src, hd, eps, sq);
+        for (int d = lane; d < hd; d += WAVE) buf[d] = (src[d] * scale) * w[d];
+    } else {
+        for (int d = lane; d < hd; d += WAVE) buf[d] = src[d];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const float2 *row = cs + (size_t)pos * half;
+    float *dst = isq ? q + (size_t)hh * hd : kc + (size_t)pos * kv_dim + (size_t)hh * hd;
+    for (int i = lane; i < half; i += WAVE) {
+        const float a = buf[i], b = buf[i + half];
+        const float2 c = row[i];
+        dst[i] = a * c.x - b * c.y;
+        dst[i + half] = a * c.y + b * c.x;
+    }
+    if (!isq)
+        for (int d = lane; d < hd; d += WAVE)
+            vc[(size_t)pos * kv_dim + (size_t)hh * hd + d] = v[(size_t)hh * hd + d];
+}
+
+// ffn_inp = x + o (the attention residual, layer.rs:170), then
+// out = rms_norm(ffn_inp) * w: one row, one workgroup.
+__global__ __launch_bounds__(256) void add_rms_norm_mul(const float *x, const float *o,
+                                                        const float *w, float *sum_out,
+                                                        float *out, int n, float eps) {
+    __shared__ __align__(16) float sq[NORM_MAX];
+    __shared__ float sc;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sum_out[i] = x[i] + o[i];
+    __syncthreads();
+    __threadfence_block();
+    if (threadIdx.x < WAVE) {
+        const float s = row_scale_wave(sum_out, n, eps, sq);
+        if (threadIdx.x == 0) sc = s;
+    }
+    __syncthreads();
+    const float scale = sc;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (sum_out[i] * scale) * w[i];
+}
+
 }  // namespace
+
+int launch_qk_norm_rope_store(float *q, const float *k, const float *v, const float *qw,
+                              const float *kw, const float2 *cs, const int32_t *pos, int n_head,
+                              int n_head_kv, int hd, float eps, float *kc, float *vc,
+                              hipStream_t st) {
+    if (hd <= 0 || hd % 2 || hd > 256 || n_head <= 0 || n_head_kv <= 0) return -1;
+    hipLaunchKernelGGL(qk_norm_rope_store, dim3(n_head + n_head_kv), dim3(64), 0, st, q, k, v, qw,
+                       kw, cs, pos, n_head, n_head_kv, hd, eps, kc, vc);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_add_rms_norm_mul(const float *x, const float *o, const float *w, float *sum_out,
+                            float *out, int n, float eps, hipStream_t st) {
+    if (n <= 0 || n > NORM_MAX || !w) return -1;
+    hipLaunchKernelGGL(add_rms_norm_mul, dim3(1), dim3(256), 0, st, x, o, w, sum_out, out, n, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
                         float eps, hipStream_t st) {
