@@ -497,9 +497,9 @@ __device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cas
 __device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 // Per-block constants of the fold: this lane's 4 scales as int16 pairs, and
-// -32 * scale likewise (so sc * (q - 32) is one packed multiply-add).
+// 128 - 32 * scale likewise (so sc * (q - 32) + 128 is one packed multiply-add).
 struct FoldScales {
-    s16x2 sc[4], m32[4];
+    s16x2 sc[4], off[4];
 };
 
 __device__ __forceinline__ FoldScales fold_scales(uint32_t scw) {
@@ -508,15 +508,18 @@ __device__ __forceinline__ FoldScales fold_scales(uint32_t scw) {
     for (int j = 0; j < 4; ++j) {
         const short v = (short)(int8_t)((scw >> (8 * j)) & 0xFF);
         f.sc[j] = s16x2{v, v};
-        f.m32[j] = s16x2{(short)(-32 * v), (short)(-32 * v)};
+        f.off[j] = s16x2{(short)(128 - 32 * v), (short)(128 - 32 * v)};
     }
     return f;
 }
 
 // w' = sc * (q - 32) for the lane's 8 class-c weights (codes: one byte each,
-// weight kk uses scale kk / 2), split into int8 digits w' = 64 * hi + lo with
-// lo in [0, 63] and hi in [-64, 64]: packed 16-bit arithmetic, two weights
-// per instruction, then byte permutes back to the 8-byte MFMA operands.
+// weight kk uses scale kk / 2), split into int8 digits w' = 256 * hi + lo with
+// lo in [-128, 127] and hi in [-16, 16]. One packed 16-bit multiply-add per
+// two weights gives v = w' + 128 in [-3936, 4224]; the high byte of v is hi
+// (arithmetic: floor(v / 256)) and its low byte, minus 128, is lo -- as a
+// byte, the low byte with its top bit flipped. Byte permutes gather the
+// 8-byte MFMA operands straight from the 16-bit lanes.
 __device__ __forceinline__ void fold_digits(uint64_t codes, const FoldScales &f, long &lo8,
                                             long &hi8) {
     const uint32_t c0 = (uint32_t)codes, c1 = (uint32_t)(codes >> 32);
@@ -524,17 +527,13 @@ __device__ __forceinline__ void fold_digits(uint64_t codes, const FoldScales &f,
                            __builtin_amdgcn_perm(0u, c0, 0x0C030C02u),
                            __builtin_amdgcn_perm(0u, c1, 0x0C010C00u),
                            __builtin_amdgcn_perm(0u, c1, 0x0C030C02u)};
-    uint32_t lo[4], hi[4];
+    uint32_t v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const s16x2 v = as_s16x2(w[j]) * f.sc[j] + f.m32[j];
-        lo[j] = as_u32(v) & 0x003F003Fu;
-        hi[j] = as_u32(v >> (s16x2){6, 6});
-    }
-    lo8 = (long)((uint64_t)__builtin_amdgcn_perm(lo[1], lo[0], 0x06040200u) |
-                 ((uint64_t)__builtin_amdgcn_perm(lo[3], lo[2], 0x06040200u) << 32));
-    hi8 = (long)((uint64_t)__builtin_amdgcn_perm(hi[1], hi[0], 0x06040200u) |
-                 ((uint64_t)__builtin_amdgcn_perm(hi[3], hi[2], 0x06040200u) << 32));
+    for (int j = 0; j < 4; ++j) v[j] = as_u32(as_s16x2(w[j]) * f.sc[j] + f.off[j]);
+    lo8 = (long)((uint64_t)(__builtin_amdgcn_perm(v[1], v[0], 0x06040200u) ^ 0x80808080u) |
+                 ((uint64_t)(__builtin_amdgcn_perm(v[3], v[2], 0x06040200u) ^ 0x80808080u) << 32));
+    hi8 = (long)((uint64_t)__builtin_amdgcn_perm(v[1], v[0], 0x07050301u) |
+                 ((uint64_t)__builtin_amdgcn_perm(v[3], v[2], 0x07050301u) << 32));
 }
 
 
@@ -619,7 +618,7 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
             }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int aux = dh[c & 1][v] * 64 + dl[c & 1][v];
+                const int aux = dh[c & 1][v] * 256 + dl[c & 1][v];
                 sums[c][v] = sums[c][v] + dd[v] * (float)aux;
             }
         }
