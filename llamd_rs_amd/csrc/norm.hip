@@ -5,22 +5,26 @@
 // of a row in f32, IN ORDER, from 0.0, then scale = 1 / sqrt(sum / n + eps)
 // and out = x * scale; the layer then multiplies by the norm weight as a
 // separate tensor op (be.mul, layer.rs:101-104 and per_head_rms_norm,
-// layer.rs:62-79). The in-order sum is a dependency chain: all lanes form
-// the rounded squares into LDS at once, and one lane adds them in order (the
-// same scheme as the router fold). sqrt and the divide are correctly rounded
-// (sqrt_rn, __fdiv_rn), as Rust's f32 sqrt and `/` are.
+// layer.rs:62-79). The in-order sum is a dependency chain. For whole rows the
+// workgroup reproduces it with exact_sum_nonneg (exact_sum.hpp: every step
+// whose rounding a bound certifies is applied as a known increment, one lane
+// replays the rest); for the 128-wide per-head norm, all lanes form the
+// rounded squares into LDS and one lane adds them in order. sqrt and the
+// divide are correctly rounded (sqrt_rn, __fdiv_rn), as Rust's f32 sqrt and
+// `/` are.
 //
 // The fused variant then forms (x * scale) * w for each 256-element block and
 // quantizes it to Q8_K with one wave per block, writing the reference's
 // BlockQ8K arrays for the Q / K / V matvecs.
 #include "common.hpp"
+#include "exact_sum.hpp"
 #include "launch.hpp"
 #include "q8k_wave.hpp"
 
 namespace llamd {
 namespace {
 
-constexpr int NORM_MAX = 8192;  // elements of one row held in LDS
+constexpr int NORM_MAX = 8192;  // longest row (the exact sum's bound holds to 8192 terms)
 
 // The sequential sum of squares of src[0..n) by lane 0 of the calling wave,
 // from squares parked in sq[] (all of the wave's lanes write them first).
@@ -85,39 +89,77 @@ __device__ float row_scale_wave(const float *src, int n, float eps, float *sq) {
     return __shfl(scale, 0, WAVE);
 }
 
+// 1 / sqrt(sum of src[j]^2 / n + eps) over src[0..n), the sum in the
+// reference's order, by the whole workgroup (every thread calls it; every
+// thread gets the scale). Each thread squares a contiguous run of the row.
+// This thread's run of a row (xsum_run(n) contiguous elements starting at
+// threadIdx.x * run) into registers; lanes past the row's end read its last
+// element (unconditional loads) and are ignored by the callers.
+__device__ __forceinline__ void load_run(const float *src, int n, float (&v)[XSUM_M]) {
+    const int m = xsum_run(n), j0 = min((int)threadIdx.x * m, n - 1);
+    if ((m & 3) == 0 && m <= XSUM_M && j0 + m <= n && ((uintptr_t)(src + j0) & 15) == 0) {
+#pragma unroll
+        for (int k = 0; k < XSUM_M; k += 4) {
+            const float4 q = k < m ? *(const float4 *)(src + j0 + k) : make_float4(0, 0, 0, 0);
+            v[k] = q.x;
+            v[k + 1] = q.y;
+            v[k + 2] = q.z;
+            v[k + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < XSUM_M; ++k) v[k] = src[min(j0 + k, n - 1)];
+    }
+}
+
+// 1 / sqrt(sum of v^2 / n + eps) for a row whose runs the threads hold in
+// vals (load_run), the sum in the reference's order, by the whole workgroup
+// (every thread calls it; every thread gets the scale). src is the row in
+// global memory, read only by the serial fallback.
+__device__ float row_scale_block(const float *src, const float (&vals)[XSUM_M], int n, float eps,
+                                 ExactSumLds &L) {
+    float sq[XSUM_M];
+#pragma unroll
+    for (int k = 0; k < XSUM_M; ++k) sq[k] = vals[k] * vals[k];
+    const float sum = exact_sum_nonneg(sq, n, L, [src](int i) {
+        const float v = src[i];
+        return v * v;
+    });
+    const float mean = __fdiv_rn(sum, (float)n);
+    return __fdiv_rn(1.0f, sqrt_rn(mean + eps));
+}
+
+// Threads for a one-row workgroup: enough that each run fits in registers.
+inline int row_threads(int n) {
+    const int need = ((n + XSUM_M - 1) / XSUM_M + WAVE - 1) / WAVE * WAVE;
+    return need < 256 ? 256 : (need > 1024 ? 1024 : need);
+}
+
 // out[r][i] = (x[r][i] * scale_r) * w[i % w_len], one workgroup per row
 // (rows = heads for the per-head QK norm). w may be null (no multiply).
-__global__ __launch_bounds__(256) void rms_norm_mul(const float *x, const float *w, float *out,
-                                                    int n, int w_len, float eps) {
-    __shared__ __align__(16) float sq[NORM_MAX];
-    __shared__ float sc;
+__global__ __launch_bounds__(1024) void rms_norm_mul(const float *x, const float *w, float *out,
+                                                     int n, int w_len, float eps) {
+    __shared__ ExactSumLds xs;
     const int r = blockIdx.x;
     const float *src = x + (size_t)r * n;
-    if (threadIdx.x < WAVE) {
-        const float s = row_scale_wave(src, n, eps, sq);
-        if (threadIdx.x == 0) sc = s;
-    }
-    __syncthreads();
-    const float scale = sc;
+    float v[XSUM_M];
+    load_run(src, n, v);
+    const float scale = row_scale_block(src, v, n, eps, xs);
     float *dst = out + (size_t)r * n;
-    // four loads of x (and w) in flight per thread before the stores
-    for (int base = 0; base < n; base += 4 * blockDim.x) {
-        float xv[4], wv[4];
+    const int m = xsum_run(n), j0 = (int)threadIdx.x * m;
+    if (m <= XSUM_M) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = base + j * blockDim.x + threadIdx.x;
-            if (i < n) {
-                xv[j] = src[i];
-                wv[j] = w ? w[w_len == n ? i : i % w_len] : 1.0f;
+        for (int k = 0; k < XSUM_M; ++k) {
+            const int i = j0 + k;
+            if (k < m && i < n) {
+                const float y = v[k] * scale;
+                dst[i] = w ? y * w[w_len == n ? i : i % w_len] : y;
             }
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = base + j * blockDim.x + threadIdx.x;
-            if (i < n) {
-                const float v = xv[j] * scale;
-                dst[i] = w ? v * wv[j] : v;
-            }
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float y = src[i] * scale;
+            dst[i] = w ? y * w[w_len == n ? i : i % w_len] : y;
         }
     }
 }
@@ -127,18 +169,12 @@ __global__ __launch_bounds__(256) void rms_norm_mul(const float *x, const float 
 __global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const float *w, float *out,
                                                        int8_t *qs, float *d, float *inv_out,
                                                        int n, float eps) {
-    __shared__ __align__(16) float sq[NORM_MAX];
-    __shared__ float sc;
+    __shared__ ExactSumLds xs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave == 0) {
-        const float s = row_scale_wave(x, n, eps, sq);
-        if (lane == 0) {
-            sc = s;
-            if (inv_out) *inv_out = s;
-        }
-    }
-    __syncthreads();
-    const float scale = sc;
+    float v0[XSUM_M];
+    load_run(x, n, v0);
+    const float scale = row_scale_block(x, v0, n, eps, xs);
+    if (inv_out && threadIdx.x == 0) *inv_out = scale;
     const int blocks = n / QK_K, waves = blockDim.x >> 6;
     for (int b = wave; b < blocks; b += waves) {
         const size_t o = (size_t)b * QK_K + 4 * lane;
@@ -193,21 +229,31 @@ __global__ __launch_bounds__(64) void qk_norm_rope_store(float *q, const float *
 
 // ffn_inp = x + o (the attention residual, layer.rs:170), then
 // out = rms_norm(ffn_inp) * w: one row, one workgroup.
-__global__ __launch_bounds__(256) void add_rms_norm_mul(const float *x, const float *o,
-                                                        const float *w, float *sum_out,
-                                                        float *out, int n, float eps) {
-    __shared__ __align__(16) float sq[NORM_MAX];
-    __shared__ float sc;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) sum_out[i] = x[i] + o[i];
-    __syncthreads();
-    __threadfence_block();
-    if (threadIdx.x < WAVE) {
-        const float s = row_scale_wave(sum_out, n, eps, sq);
-        if (threadIdx.x == 0) sc = s;
+__global__ __launch_bounds__(1024) void add_rms_norm_mul(const float *x, const float *o,
+                                                         const float *w, float *sum_out,
+                                                         float *out, int n, float eps) {
+    __shared__ ExactSumLds xs;
+    const int m = xsum_run(n), j0 = (int)threadIdx.x * m;
+    float v[XSUM_M], ov[XSUM_M];
+    load_run(x, n, v);
+    load_run(o, n, ov);
+#pragma unroll
+    for (int k = 0; k < XSUM_M; ++k) {
+        v[k] = v[k] + ov[k];
+        if (k < m && j0 + k < n) sum_out[j0 + k] = v[k];
     }
-    __syncthreads();
-    const float scale = sc;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (sum_out[i] * scale) * w[i];
+    if (m > XSUM_M)
+        for (int i = threadIdx.x; i < n; i += blockDim.x) sum_out[i] = x[i] + o[i];
+    // the serial fallback reads sum_out back; exact_sum_nonneg's barriers
+    // order these stores before it
+    const float scale = row_scale_block(sum_out, v, n, eps, xs);
+    if (m <= XSUM_M) {
+#pragma unroll
+        for (int k = 0; k < XSUM_M; ++k)
+            if (k < m && j0 + k < n) out[j0 + k] = (v[k] * scale) * w[j0 + k];
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (sum_out[i] * scale) * w[i];
+    }
 }
 
 }  // namespace
@@ -225,14 +271,14 @@ int launch_qk_norm_rope_store(float *q, const float *k, const float *v, const fl
 int launch_add_rms_norm_mul(const float *x, const float *o, const float *w, float *sum_out,
                             float *out, int n, float eps, hipStream_t st) {
     if (n <= 0 || n > NORM_MAX || !w) return -1;
-    hipLaunchKernelGGL(add_rms_norm_mul, dim3(1), dim3(256), 0, st, x, o, w, sum_out, out, n, eps);
+    hipLaunchKernelGGL(add_rms_norm_mul, dim3(1), dim3(row_threads(n)), 0, st, x, o, w, sum_out, out, n, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
                         float eps, hipStream_t st) {
     if (rows <= 0 || n <= 0 || n > NORM_MAX || (w && w_len <= 0)) return -1;
-    hipLaunchKernelGGL(rms_norm_mul, dim3(rows), dim3(256), 0, st, x, w, out, n, w_len, eps);
+    hipLaunchKernelGGL(rms_norm_mul, dim3(rows), dim3(row_threads(n)), 0, st, x, w, out, n, w_len, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

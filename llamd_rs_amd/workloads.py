@@ -12,6 +12,8 @@ rocprofv3 (--kernel-trace, --pmc) so a profile covers exactly one workload:
     lm_head_b16
     moe_decode   one MoE decode layer per call, 4 layers rotating
     prefill      the expert-grouped FFN of 512 tokens, top-8 of 128, Zipf 1.1
+    decode       whole-token decode of a Qwen3-30B-A3B-shaped model cut to 4
+                 layers (plain launches, no graph), positions 3..3+N
 """
 from __future__ import annotations
 
@@ -94,12 +96,35 @@ def prefill(L, iters):
     _sync(L)
 
 
+def decode(L, iters):
+    import os
+    import tempfile
+    from . import synth_model
+    from .gguf import Gguf
+    hp = dict(synth_model.QWEN3_30B_A3B, n_layer=4)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    if L.llamd_hip_tune(b"model_graph", 0) < 0:  # read when the model is created
+        raise RuntimeError("tune")
+    try:
+        synth_model.write_model(path, hp)
+        with Gguf(path) as g:
+            dm = rocm.DeviceModel(g, max_kv=1024)
+    finally:
+        os.unlink(path)
+    tok = 1
+    for pos in range(3 + iters):
+        _, tok = dm.forward(tok, pos)
+    dm.close()
+
+
 WORKLOADS = {
     "configs1": configs1,
     "lm_head_b1": lambda L, n: lm_head(L, n, 1),
     "lm_head_b16": lambda L, n: lm_head(L, n, 16),
     "moe_decode": moe_decode,
     "prefill": prefill,
+    "decode": decode,
 }
 
 

@@ -2,6 +2,8 @@
 (bit-identical), including the in-order f32 sum that a parallel reduction
 would not reproduce. The last test runs the attention block's front end:
 rms_norm_quant then one llamd_fwd_matvec_x3 launch for Q, K and V."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -129,3 +131,60 @@ def test_many_short_rows_exercise_sqrt_and_divide(gpu):
         want = O.mul(O.rms_norm(x, n_head, hd, eps), np.tile(w, n_head))
         bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
         assert bad.size == 0, (eps, bad[:5], got[bad[:5]], want[bad[:5]])
+
+
+def _rows(kind, rows, n, rng):
+    g = rng.standard_normal((rows, n))
+    if kind == "normal":
+        x = g
+    elif kind == "outliers":           # a few channels 100x, as in real hidden states
+        x = g * np.where(rng.random((rows, n)) < 0.01, 100.0, 1.0)
+    elif kind == "tiny_first":         # the first squares far below the rest
+        x = g.copy()
+        x[:, :2] = np.array([1e-7, 1e-5])[:n]
+    elif kind == "halves":             # squares k/4: increments that tie at coarse grids
+        x = rng.integers(-40, 40, (rows, n)) / 2.0
+    elif kind == "sparse":
+        x = np.where(rng.random((rows, n)) < 0.7, 0.0, g)
+    elif kind == "huge_range":         # too many uncertain steps: the serial fallback
+        x = g * 10.0 ** rng.integers(-15, 15, (rows, n))
+    elif kind == "subnormal_squares":
+        x = g * 1e-22
+    elif kind == "overflow":           # the sum overflows to inf part way
+        x = g * 1e18
+    elif kind == "constant":
+        x = np.full((rows, n), 0.3)
+    elif kind == "specials":           # inf and NaN in some rows
+        x = g.copy()
+        x[1, n // 2] = np.inf
+        x[2, 0] = np.nan
+        x[3, n - 1] = -np.inf
+    return x.astype(np.float32)
+
+
+KINDS = ["normal", "outliers", "tiny_first", "halves", "sparse", "huge_range",
+         "subnormal_squares", "overflow", "constant", "specials"]
+
+
+@pytest.mark.parametrize("n", [2048, 768, 8192, 129, 1])
+@pytest.mark.parametrize("kind", KINDS)
+def test_row_sum_of_squares_in_order(gpu, kind, n):              # llamd-cpu lib.rs:55-66
+    """The workgroup's certified-increment replay of the in-order sum
+    against the oracle's one-by-one f32 fold, row by row (bit-identical
+    output rows; a sum off by one ulp moves the scale in about half the
+    rows). Covers certain/uncertain mixes, ties, zeros, subnormal squares,
+    overflow, inf/NaN and the serial fallback."""
+    L = _lib()
+    rows = 16 if n == 8192 else 64
+    x = _rows(kind, rows, n, np.random.default_rng(zlib.crc32(f"{kind}/{n}".encode())))
+    w = np.ones(n, np.float32)
+    for eps in (0.0, 1e-6):
+        dx, dw, do = (gpu.DeviceBuffer.from_array(x.ravel()), gpu.DeviceBuffer.from_array(w),
+                      gpu.DeviceBuffer(x.nbytes))
+        L.llamd_fwd_head_rms_norm_mul(dx.ptr, dw.ptr, do.ptr, rows, n, eps)
+        _sync()
+        got = do.download(np.empty(x.size, np.float32))
+        want = O.mul(O.rms_norm(x.ravel(), rows, n, eps), np.tile(w, rows))
+        differ = (got.view(np.uint32) != want.view(np.uint32)) & ~(np.isnan(got) & np.isnan(want))
+        bad = np.flatnonzero(differ)
+        assert bad.size == 0, (kind, n, eps, bad[:5] // n)
