@@ -16,11 +16,13 @@
 //     the softmax from tying them) the exact top-k SET is certain and the
 //     experts are used in the estimate's order. Otherwise it waits for the
 //     exact logits and routes exactly. act = silu(g) * u.
+//   launch 1, last workgroup (per sequence): waits for the exact logits and
+//     routes them (route_finish) -- ids and weights in the reference's
+//     order -- while the gate/up tiles are still streaming.
 //   launch 2, one workgroup per 16-row tile of down: wave e computes the
-//     tile for act row e; one more wave routes the exact logits
-//     (route_finish) and the rows are combined in THAT order with those
-//     weights. No result depends on the estimate; it only decides how early
-//     gate/up may start.
+//     tile for act row e, and the rows are combined in the exact routing's
+//     order with its weights. No result depends on the estimate; it only
+//     decides how early gate/up may start.
 //
 // HAND-OFF WITHOUT CACHE-WIDE FENCES. Inside launch 1, values cross
 // workgroups in 64-bit words (value, ready mark) written with relaxed
@@ -300,28 +302,43 @@ __device__ void gateup_workgroup(const DecodeParams &p, DecodeLds &sm, int g, in
     }
 }
 
+// The exact routing of one sequence (moe.rs:82-113) from the exact logits,
+// by wave 0, into ids_out / w_out for launch 2's combine.
+__device__ void router_workgroup(const DecodeParams &p, DecodeLds &sm, int lane, int wave) {
+    if (wave != 0) return;
+    __builtin_amdgcn_s_setprio(3);
+    expf_ref_tab_fill(sm.g.rsh.tab);  // its load now, not after the wait
+    float l[RW];
+    bool late = false;
+    wait_logits(p, l, late);
+    route_finish(l, p.n_expert, p.n_used, true, sm.g.rsh, p.ids_out, p.w_out, nullptr);
+    if (lane == 0 && late && p.stats) p.stats[3] = 1;
+}
+
 __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
     asm volatile("" ::"s"(p.w_gate), "s"(p.w_up), "s"(p.rw), "s"(p.x), "s"(p.slots),
                  "s"(p.gu_stride), "s"(p.k), "s"(p.n_expert), "s"(p.n_used), "s"(p.n_chain));
     __shared__ DecodeLds sm;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // all sequences' chain workgroups first (the gate/up ones wait on them)
-    const int b = blockIdx.x, chains = p.n_chain * p.nseq;
+    // all sequences' chain workgroups first (the gate/up ones wait on them),
+    // then the gate/up tiles, then one router workgroup per sequence
+    const int b = blockIdx.x, chains = p.n_chain * p.nseq, gus = p.n_gu * p.nseq;
     if (b < chains) {
         chain_workgroup(for_seq(p, b / p.n_chain), sm, b % p.n_chain, lane, wave);
-    } else {
+    } else if (b < chains + gus) {
         const int g = b - chains;
         gateup_workgroup(for_seq(p, g / p.n_gu), sm, g % p.n_gu, lane, wave);
+    } else {
+        router_workgroup(for_seq(p, b - chains - gus), sm, lane, wave);
     }
 }
 
 // Launch 2: wave e < n_used computes the tile for expert spec_ids[e] on act
-// row e (Q8_K of act in LDS, quantize_q8_k bits); wave n_used (wave 0 after
-// its tile when n_used = 16) routes on the exact logits, and the tile's rows
-// are combined in the reference's order:
-// out = res + (((0 + w0*y[ids0]) + w1*y[ids1]) + ...). Workgroup 0 writes the
-// routing out, counts the call and empties the hand-off words.
+// row e (Q8_K of act in LDS, quantize_q8_k bits), and the tile's rows are
+// combined in the exact routing's order (ids_out / w_out, from launch 1):
+// out = res + (((0 + w0*y[ids0]) + w1*y[ids1]) + ...). Workgroup 0 counts
+// the call and empties the hand-off words.
 __global__ __launch_bounds__(1024) void moe_down_route(DecodeParams pb) {
     const DecodeParams p = for_seq(pb, blockIdx.y);
     asm volatile("" ::"s"(p.w_down), "s"(p.down_stride), "s"(p.spec_ids), "s"(p.act), "s"(p.n_ff),
@@ -329,14 +346,21 @@ __global__ __launch_bounds__(1024) void moe_down_route(DecodeParams pb) {
     __shared__ float ys[MAX_USED][TILE_ROWS];
     __shared__ __align__(16) int8_t lq[MAX_USED][DOWN_ACT_BLOCKS * QK_K];
     __shared__ float ld[MAX_USED][DOWN_ACT_BLOCKS];
-    __shared__ RouteLds rsh;
     __shared__ int rids[MAX_USED], sid[MAX_USED];
     __shared__ float rwt[MAX_USED];
     const int lane = threadIdx.x & 63;
     const int e = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t = blockIdx.x;
     const int n = lane & 15, s = lane >> 4;
-    const int route_wave = p.n_used < MAX_USED ? p.n_used : 0;
+    if (e == 0 && lane < p.n_used) {
+        // launch 1's routing and the act rows' experts; used after the matvec
+        rids[lane] = p.ids_out[lane];
+        rwt[lane] = p.w_out[lane];
+        sid[lane] = p.spec_ids[lane];
+    }
+    // the residual row, loaded now so its latency hides behind the matvec
+    const int orow = t * TILE_ROWS + lane;
+    const float resv = e == 0 && lane < TILE_ROWS && p.res && orow < p.k ? p.res[orow] : 0.0f;
     if (e < p.n_used) {
         const MaskSel msel = mask_selectors(n, (n >> 2) == s);
         // the activations do not depend on the expert id: their loads go first
@@ -400,43 +424,41 @@ __global__ __launch_bounds__(1024) void moe_down_route(DecodeParams pb) {
             ys[e][n] = tot;
         }
     }
-    if (e == route_wave) {
-        __builtin_amdgcn_s_setprio(3);  // serial routing beside the matvec waves
-        float l[RW];
+    __syncthreads();
+    if (e == 0) {
+        // act row of each routed expert (the routing's order -> spec order)
+        int pj = 0;
+        if (lane < p.n_used) {
+            const int id = rids[lane];
 #pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            const int i = lane + WAVE * j;
-            l[j] = i < p.n_expert ? p.logits[i] : 0.0f;
+            for (int j = MAX_USED - 1; j >= 0; --j)
+                if (j < p.n_used && sid[j] == id) pj = j;
         }
-        if (lane < p.n_used) sid[lane] = p.spec_ids[lane];
-        route_finish(l, p.n_expert, p.n_used, true, rsh, rids, rwt, nullptr);
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (t == 0) {
-            if (lane < p.n_used) {
-                p.ids_out[lane] = rids[lane];
-                p.w_out[lane] = rwt[lane];
-            }
-            if (lane == 0 && p.stats) {
-                atomicAdd(&p.stats[0], 1);
-                atomicAdd(&p.stats[1], 1);
-            }
-            for (int i = lane; i < 2 * p.n_expert; i += WAVE) p.slots[i] = SLOT_EMPTY;
+        float yv[MAX_USED], wv[MAX_USED];
+#pragma unroll
+        for (int q = 0; q < MAX_USED; ++q) {
+            const int jq = __shfl(pj, q, WAVE);
+            yv[q] = q < p.n_used && lane < TILE_ROWS ? ys[jq][lane] : 0.0f;
+            wv[q] = q < p.n_used ? rwt[q] : 0.0f;
+        }
+        const int row = t * TILE_ROWS + lane;
+        if (lane < TILE_ROWS && row < p.k) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < MAX_USED; ++q)
+                if (q < p.n_used) {
+                    const float prod = wv[q] * yv[q];
+                    acc = acc + prod;
+                }
+            p.out[row] = p.res ? resv + acc : acc;
         }
     }
-    __syncthreads();
-    if (e == 0 && lane < TILE_ROWS) {
-        const int row = t * TILE_ROWS + lane;
-        if (row < p.k) {
-            float acc = 0.0f;
-            for (int q = 0; q < p.n_used; ++q) {
-                int j = 0;
-                while (j < p.n_used - 1 && sid[j] != rids[q]) ++j;
-                const float prod = rwt[q] * ys[j][lane];
-                acc = acc + prod;
-            }
-            p.out[row] = p.res ? p.res[row] + acc : acc;
+    if (t == 0 && e == 0) {
+        if (lane == 0 && p.stats) {
+            atomicAdd(&p.stats[0], 1);
+            atomicAdd(&p.stats[1], 1);
         }
+        for (int i = lane; i < 2 * p.n_expert; i += WAVE) p.slots[i] = SLOT_EMPTY;
     }
 }
 
@@ -476,9 +498,8 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     p.n_chain = (l.n_expert + CHAIN_EXPERTS - 1) / CHAIN_EXPERTS;
     p.n_gu = l.n_used * p.gu_tiles;
     p.nseq = l.nseq;
-    hipLaunchKernelGGL(moe_router_gateup, dim3((p.n_chain + p.n_gu) * l.nseq), dim3(512), 0, st, p);
-    const int waves = l.n_used < MAX_USED ? l.n_used + 1 : MAX_USED;
-    hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles, l.nseq), dim3(64 * waves), 0, st, p);
+    hipLaunchKernelGGL(moe_router_gateup, dim3((p.n_chain + p.n_gu + 1) * l.nseq), dim3(512), 0, st, p);
+    hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles, l.nseq), dim3(64 * l.n_used), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

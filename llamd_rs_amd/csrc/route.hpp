@@ -93,13 +93,18 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float total = 0.0f;
     if (lane == 0) {
+        // 64 values per step: the LDS reads are issued together and retire
+        // in order, so the dependent adds start on the first
         float acc = -0.0f;
         int i = 0;
-        for (; i + 8 <= n_expert; i += 8) {
-            const float4 u = *(const float4 *)(sh.p + i);
-            const float4 v = *(const float4 *)(sh.p + i + 4);
-            acc = acc + u.x; acc = acc + u.y; acc = acc + u.z; acc = acc + u.w;
-            acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+        for (; i + 64 <= n_expert; i += 64) {
+            float4 u[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) u[j] = *(const float4 *)(sh.p + i + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                acc = acc + u[j].x; acc = acc + u[j].y; acc = acc + u[j].z; acc = acc + u[j].w;
+            }
         }
         for (; i < n_expert; ++i) acc = acc + sh.p[i];
         total = acc;
@@ -122,14 +127,17 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (lane == 0 && ids) {
-        // raw = p[chosen]; sum from -0.0, clamped; w = raw / sum (moe.rs:103-105)
+    if (ids) {
+        // raw = p[chosen]; sum from -0.0 in routing order, clamped; w = raw /
+        // sum (moe.rs:103-105). Lane q gathers raw q; lane 0 adds them in order.
+        const int id = lane < n_used ? sh.sorted[lane] : 0;
+        const float raw = lane < n_used ? sh.p[id] : 0.0f;
         float wsum = -0.0f;
-        for (int q = 0; q < n_used; ++q) wsum = wsum + sh.p[sh.sorted[q]];
+        for (int q = 0; q < n_used; ++q) wsum = wsum + __shfl(raw, q, WAVE);
         wsum = fmaxf(wsum, WEIGHT_SUM_FLOOR);
-        for (int q = 0; q < n_used; ++q) {
-            ids[q] = sh.sorted[q];
-            weights[q] = sh.p[sh.sorted[q]] / wsum;
+        if (lane < n_used) {
+            ids[lane] = id;
+            weights[lane] = raw / wsum;
         }
     }
 }
