@@ -38,6 +38,7 @@ int g_tune_moe_fused = 2;
 int g_tune_batch_decode_max = 16;
 }  // namespace
 int llamd::g_tune_model_graph = 1;  // whole-token decode replays a captured graph
+int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else three launches)
 namespace {
 
 int fail(const char *fmt, ...) {
@@ -155,6 +156,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "moe_fused")) {
         const int prev = g_tune_moe_fused;
         g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
+        return prev;
+    }
+    if (!strcmp(key, "model_fused_attn")) {
+        const int prev = g_tune_model_fused_attn;
+        g_tune_model_fused_attn = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "model_graph")) {

@@ -9,6 +9,8 @@
 #include "common.hpp"
 #include "expf_ref.h"
 #include "launch.hpp"
+#include "q8k_wave.hpp"
+#include "row_scale.hpp"
 
 namespace llamd {
 namespace {
@@ -111,6 +113,285 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     }
 }
 
+// Norm + RoPE of one head (hd values from src) into dst in LDS, as
+// qk_norm_rope_store does: (x * scale) * w, then a*cos - b*sin and
+// a*sin + b*cos on the halves. One wave; w null skips the norm.
+__device__ void head_norm_rope(const float *src, const float *w, const float2 *row, int hd,
+                               float eps, float *sq, float *buf, float *dst) {
+    const int lane = threadIdx.x & 63, half = hd / 2;
+    // every global value this wave needs, loaded before any is used (hd <= 256)
+    float xv[4], wv[4];
+    float2 cv[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + WAVE * j;
+        xv[j] = d < hd ? src[d] : 0.0f;
+        wv[j] = d < hd && w ? w[d] : 1.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = lane + WAVE * j;
+        cv[j] = i < half ? row[i] : make_float2(0.0f, 0.0f);
+    }
+    float scale = 1.0f;
+    if (w) {
+        // the sum of squares in order by lane 0 (row_scale_wave's fold)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + WAVE * j < hd) sq[lane + WAVE * j] = xv[j] * xv[j];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane == 0) {
+            float sum = 0.0f;
+            for (int d = 0; d < hd; d += 32) {
+                float4 v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = *(const float4 *)(sq + d + 4 * j);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    sum = sum + v[j].x;
+                    sum = sum + v[j].y;
+                    sum = sum + v[j].z;
+                    sum = sum + v[j].w;
+                }
+            }
+            const float mean = __fdiv_rn(sum, (float)hd);
+            scale = __fdiv_rn(1.0f, sqrt_rn(mean + eps));
+        }
+        scale = __shfl(scale, 0, WAVE);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + WAVE * j;
+        if (d < hd) buf[d] = w ? (xv[j] * scale) * wv[j] : xv[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = lane + WAVE * j;
+        if (i < half) {
+            const float a = buf[i], b = buf[i + half];
+            dst[i] = a * cv[j].x - b * cv[j].y;
+            dst[i + half] = a * cv[j].y + b * cv[j].x;
+        }
+    }
+}
+
+// One decode step's attention block after the Q/K/V matvecs, two query
+// heads (hd = 128) per workgroup -- one 256-value Q8_K block of the output:
+//   1. per head: QK-norm + RoPE of Q (wave 0 of the head's 256 threads) and
+//      of this position's K, plus its V (wave 1); the first query head of
+//      each kv group also appends K and V to the cache. The other workgroups
+//      of the group use their own copy of the same values for position pos,
+//      so no workgroup waits on another.
+//   2. attention exactly as attend_decode: the logits' dot products in
+//      order, the max, expf_ref, the in-order sum, 1 / sum, the in-order
+//      weighted V sum.
+//   3. Q8_K of the workgroup's 256 outputs (quantize_q8_k bits) for the O
+//      projection, and the f32 outputs if `out` is set.
+// Cached K and V rows reach LDS in chunks of ATT_CHUNK positions with
+// coalesced loads (all of a chunk's loads in flight at once; the first
+// chunk's while the norms run): one thread per position then folds its K
+// row, and one per dimension its V column, from LDS.
+// Bit-identical to qk_norm_rope_store + attend_decode + q8k_quantize.
+constexpr int ATT_HD = 128;
+constexpr int ATT_CHUNK = 64;
+constexpr int ATT_KS = ATT_HD + 4;  // padded K row in LDS (fewer bank conflicts)
+
+// Staging of cached K or V positions [c0, c0 + ATT_CHUNK) below pos into LDS
+// for the workgroup's nkv kv slots (512 threads): each thread loads its
+// float4s first (ATT_PER at most), then stores them.
+constexpr int ATT_PER = 2 * ATT_CHUNK * (ATT_HD / 4) / 512;
+// a native vector (HIP's float4 struct copies stayed in scratch memory here)
+typedef float att_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void att_stage_load(att_f4 (&r)[ATT_PER], const float *cache, int c0,
+                                               int pos, int nkv, int h0, int group, int kv_dim) {
+    constexpr int C = ATT_CHUNK, D4 = ATT_HD / 4;
+    const int np = min(C, pos - c0), last = np > 0 ? np - 1 : 0;
+#pragma unroll
+    for (int k = 0; k < ATT_PER; ++k) {
+        const int i = threadIdx.x + 512 * k;  // over [slot][t][d4]
+        const int sl = i / (C * D4), t = min((i / D4) % C, last), d4 = i % D4;
+        // a slot past nkv reads slot 0's row again (same lines; never stored)
+        const int kh = (h0 + (sl < nkv ? sl : 0)) / group;
+        r[k] = *(const att_f4 *)(cache + (size_t)(c0 + t) * kv_dim + (size_t)kh * ATT_HD + 4 * d4);
+    }
+}
+
+__device__ __forceinline__ void att_stage_store(const att_f4 (&r)[ATT_PER], float *dst, int stride,
+                                                int c0, int pos, int nkv) {
+    constexpr int C = ATT_CHUNK, D4 = ATT_HD / 4;
+    const int np = min(C, pos - c0);
+#pragma unroll
+    for (int k = 0; k < ATT_PER; ++k) {
+        const int i = threadIdx.x + 512 * k;
+        const int sl = i / (C * D4), t = (i / D4) % C, d4 = i % D4;
+        if (sl < nkv && t < np) *(att_f4 *)(dst + ((size_t)sl * C + t) * stride + 4 * d4) = r[k];
+    }
+}
+
+__global__ __launch_bounds__(512) void attend_fused(
+    const float *q_raw, const float *k_raw, const float *v_raw, const float *qw, const float *kw,
+    const float2 *cs, const int32_t *pos_p, int n_head, int n_head_kv, float eps, float scale,
+    int max_kv, float *kc, float *vc, int8_t *oq, float *od, float *out) {
+    constexpr int HD = ATT_HD, C = ATT_CHUNK, KS = ATT_KS;
+    extern __shared__ __align__(16) float dyn[];  // lg [2][max_kv] | K [nkv][C][KS] | V [nkv][C][HD]
+    __shared__ __align__(16) float qs[2][HD], kn[2][HD], vn[2][HD];
+    __shared__ __align__(16) float sq[2][2][HD], buf[2][2][HD];
+    __shared__ __align__(16) float ov[256];
+    __shared__ float red[2][4];
+    __shared__ uint64_t tab[2][32];
+    const int grp = threadIdx.x >> 8, tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    const int h0 = blockIdx.x * 2, h = h0 + grp, group = n_head / n_head_kv;
+    const int kvh = h / group, kv_dim = n_head_kv * HD, pos = pos_p[0], n_kv = pos + 1;
+    const int nkv = group >= 2 ? 1 : 2;   // distinct kv heads of the two query heads
+    const int slot = nkv == 1 ? 0 : grp;  // this head's K / V staging slot
+    const int lgs = (max_kv + 3) & ~3;    // logits row stride (float4-aligned)
+    float *lg = dyn + (size_t)grp * lgs;
+    float *kst = dyn + (size_t)2 * lgs;
+    float *vst = kst + (size_t)nkv * C * KS;
+    const float2 *row = cs + (size_t)pos * (HD / 2);
+
+    att_f4 sk[ATT_PER], sv[ATT_PER];
+    if (pos > 0) {
+        att_stage_load(sk, kc, 0, pos, nkv, h0, group, kv_dim);
+        att_stage_load(sv, vc, 0, pos, nkv, h0, group, kv_dim);
+    }
+    if (wave == 0) {
+        head_norm_rope(q_raw + (size_t)h * HD, qw, row, HD, eps, sq[grp][0], buf[grp][0], qs[grp]);
+    } else if (wave == 1) {
+        const float v0 = v_raw[(size_t)kvh * HD + lane], v1 = v_raw[(size_t)kvh * HD + WAVE + lane];
+        head_norm_rope(k_raw + (size_t)kvh * HD, kw, row, HD, eps, sq[grp][1], buf[grp][1], kn[grp]);
+        vn[grp][lane] = v0;
+        vn[grp][WAVE + lane] = v1;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (h % group == 0)
+            for (int d = lane; d < HD; d += WAVE) {
+                kc[(size_t)pos * kv_dim + (size_t)kvh * HD + d] = kn[grp][d];
+                vc[(size_t)pos * kv_dim + (size_t)kvh * HD + d] = vn[grp][d];
+            }
+    } else if (wave == 2) {
+        expf_ref_tab_fill(tab[grp]);
+    }
+    if (pos > 0) {
+        att_stage_store(sk, kst, KS, 0, pos, nkv);
+        att_stage_store(sv, vst, HD, 0, pos, nkv);
+    }
+    __syncthreads();
+
+    // logits: one thread per position, q . k in order from 0; 32 values of
+    // q and of the row read from LDS per step, then their 32 ordered adds
+    const auto qdot = [&](const float *kr) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int d0 = 0; d0 < HD; d0 += 32) {
+            float4 k4[8], q4[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                k4[j] = *(const float4 *)(kr + d0 + 4 * j);
+                q4[j] = *(const float4 *)(&qs[grp][d0 + 4 * j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                dot = dot + q4[j].x * k4[j].x;
+                dot = dot + q4[j].y * k4[j].y;
+                dot = dot + q4[j].z * k4[j].z;
+                dot = dot + q4[j].w * k4[j].w;
+            }
+        }
+        return dot;
+    };
+    float mx = -INFINITY;
+    for (int c0 = 0; c0 < n_kv; c0 += C) {
+        if (c0 > 0) {
+            // later chunks (long contexts): every thread stages, then folds
+            if (c0 < pos) att_stage_load(sk, kc, c0, pos, nkv, h0, group, kv_dim);
+            __syncthreads();
+            if (c0 < pos) att_stage_store(sk, kst, KS, c0, pos, nkv);
+            __syncthreads();
+        }
+        const int t = c0 + tid;
+        if (tid < C && t < n_kv) {
+            const float dot = t < pos ? qdot(kst + ((size_t)slot * C + tid) * KS) : qdot(kn[grp]);
+            const float l = dot * scale;
+            lg[t] = l;
+            mx = fmaxf(mx, l);  // f32::max fold: NaN-ignoring, order-free
+        }
+    }
+    mx = wave_reduce(mx, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    if (lane == 0) red[grp][wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[grp][0], red[grp][1]), fmaxf(red[grp][2], red[grp][3]));
+    for (int t = tid; t < n_kv; t += 256) lg[t] = expf_ref_tab(lg[t] - mx, tab[grp]);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        int t = 0;
+        for (; t + 32 <= n_kv; t += 32) {
+            float4 e[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = *(const float4 *)(lg + t + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                sum = sum + e[j].x;
+                sum = sum + e[j].y;
+                sum = sum + e[j].z;
+                sum = sum + e[j].w;
+            }
+        }
+        for (; t < n_kv; ++t) sum = sum + lg[t];
+        red[grp][0] = __fdiv_rn(1.0f, sum);
+    }
+    __syncthreads();
+    const float inv = red[grp][0];
+
+    // the weighted V sum, one thread per dimension, in position order; the
+    // first chunk was staged with K
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < pos; c0 += C) {
+        if (c0 > 0) {
+            att_stage_load(sv, vc, c0, pos, nkv, h0, group, kv_dim);
+            __syncthreads();
+            att_stage_store(sv, vst, HD, c0, pos, nkv);
+            __syncthreads();
+        }
+        if (tid < HD) {
+            const int np = min(C, pos - c0);
+            const float *vr = vst + (size_t)slot * C * HD + tid;
+            int t = 0;
+            for (; t + 8 <= np; t += 8) {
+                float vv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * HD];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float w = lg[c0 + t + j] * inv;
+                    acc = acc + w * vv[j];
+                }
+            }
+            for (; t < np; ++t) {
+                const float w = lg[c0 + t] * inv;
+                acc = acc + w * vr[(size_t)t * HD];
+            }
+        }
+    }
+    if (tid < HD) {
+        const float w = lg[pos] * inv;
+        acc = acc + w * vn[grp][tid];
+        ov[grp * HD + tid] = acc;
+        if (out) out[(size_t)h * HD + tid] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < WAVE) {
+        const float4 v4 = *(const float4 *)(ov + 4 * lane);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        quantize_wave(v, lane, oq + (size_t)blockIdx.x * QK_K, od + blockIdx.x, nullptr);
+    }
+}
+
 }  // namespace
 
 int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st) {
@@ -121,6 +402,45 @@ int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *o
 }
 
 int attend_max_kv() { return ATT_MAX_KV; }
+
+namespace {
+size_t g_fused_lds = 0;  // the dynamic LDS attend_fused may use (raised by prepare)
+}
+
+namespace {
+size_t fused_lds(int n_head, int n_head_kv, int max_kv) {
+    const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
+    return (size_t)2 * ((max_kv + 3) & ~3) * 4 + (size_t)nkv * ATT_CHUNK * (ATT_KS + ATT_HD) * 4;
+}
+}  // namespace
+
+bool attend_fused_fits(int n_head, int n_head_kv, int hd, int max_kv) {
+    if (hd != ATT_HD || n_head_kv <= 0 || n_head % n_head_kv || n_head % 2 || max_kv <= 0) return false;
+    return fused_lds(n_head, n_head_kv, max_kv) + 24 * 1024 <= 160 * 1024;
+}
+
+int attend_fused_prepare(int n_head, int n_head_kv, int hd, int max_kv) {
+    if (!attend_fused_fits(n_head, n_head_kv, hd, max_kv)) return -1;
+    const size_t lds = fused_lds(n_head, n_head_kv, max_kv);
+    if (lds <= g_fused_lds) return 0;
+    if (hipFuncSetAttribute((const void *)attend_fused, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+        return -1;
+    g_fused_lds = lds;
+    return 0;
+}
+
+int launch_attend_fused(const float *q, const float *k, const float *v, const float *qw,
+                        const float *kw, const float2 *cs, const int32_t *pos, int n_head,
+                        int n_head_kv, int hd, float eps, float scale, int max_kv, float *kc,
+                        float *vc, int8_t *oq, float *od, float *out, hipStream_t st) {
+    if (!attend_fused_fits(n_head, n_head_kv, hd, max_kv)) return -1;
+    const size_t lds = fused_lds(n_head, n_head_kv, max_kv);
+    if (lds > g_fused_lds) return -1;  // attend_fused_prepare first
+    hipLaunchKernelGGL(attend_fused, dim3(n_head / 2), dim3(512), lds, st, q, k, v, qw, kw, cs, pos,
+                       n_head, n_head_kv, eps, scale, max_kv, kc, vc, oq, od, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
                          int n_head, int n_head_kv, int hd, float scale, float *out,

@@ -11,8 +11,9 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
-extern int g_tune_mv_ks;
-extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
+extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
+extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
+extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -115,6 +116,13 @@ int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs
 // from device memory)
 int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st);
 int attend_max_kv();
+bool attend_fused_fits(int n_head, int n_head_kv, int hd, int max_kv);
+// raises attend_fused's dynamic LDS limit for max_kv positions (outside graph capture)
+int attend_fused_prepare(int n_head, int n_head_kv, int hd, int max_kv);
+int launch_attend_fused(const float *q, const float *k, const float *v, const float *qw,
+                        const float *kw, const float2 *cs, const int32_t *pos, int n_head,
+                        int n_head_kv, int hd, float eps, float scale, int max_kv, float *kc,
+                        float *vc, int8_t *oq, float *od, float *out, hipStream_t st);
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
                          int n_head, int n_head_kv, int hd, float scale, float *out,
                          hipStream_t st);

@@ -52,6 +52,7 @@ struct Model {
     int32_t *tokpos = nullptr, *next = nullptr;
     hipGraphExec_t exec = nullptr;  // the captured step
     bool use_graph = true;
+    bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
     std::vector<void *> owned;     // device allocations to free
 };
 
@@ -90,14 +91,22 @@ bool enqueue_step(Model *m, hipStream_t st) {
         llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
         llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb, qdim,
                             kv_dim, kv_dim);
-        // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append
-        rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
-                                               m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
-                                               m->eps, l.kc, l.vc, st);
-        rc |= llamd::launch_attend_decode(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head, m->n_head_kv,
-                                          m->hd, m->scale, m->attn, st);
+        // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append,
+        // attention, and Q8_K of its output for the O projection
+        if (m->fused_attn) {
+            rc |= llamd::launch_attend_fused(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
+                                             m->tokpos + 1, m->n_head, m->n_head_kv, m->hd, m->eps,
+                                             m->scale, m->max_kv, l.kc, l.vc, m->aq, m->ad,
+                                             nullptr, st);
+        } else {
+            rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
+                                                   m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
+                                                   m->eps, l.kc, l.vc, st);
+            rc |= llamd::launch_attend_decode(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head,
+                                              m->n_head_kv, m->hd, m->scale, m->attn, st);
+            llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
+        }
         // O projection, residual
-        llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
         llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
         // ffn_inp = x + O, ffn_norm; then the MoE FFN with the second
         // residual: x = ffn_inp + moe
@@ -187,6 +196,8 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->n_vocab = (int)edims[1];
     m->max_kv = max_kv;
     m->use_graph = llamd::g_tune_model_graph != 0;
+    m->fused_attn = llamd::g_tune_model_fused_attn != 0 &&
+                    llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;
     m->rope_base = base;
     m->scale = 1.0f / sqrtf((float)hd);  // attention.rs:95
