@@ -67,7 +67,7 @@ __device__ float row_scale_block(const float *src, const float (&vals)[XSUM_M], 
 // Threads for a one-row workgroup: enough that each run fits in registers.
 inline int row_threads(int n) {
     const int need = ((n + XSUM_M - 1) / XSUM_M + WAVE - 1) / WAVE * WAVE;
-    return need < 256 ? 256 : (need > 1024 ? 1024 : need);
+    return need < 512 ? 512 : (need > 1024 ? 1024 : need);
 }
 
 // out[r][i] = (x[r][i] * scale_r) * w[i % w_len], one workgroup per row
