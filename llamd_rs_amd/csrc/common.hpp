@@ -146,6 +146,17 @@ __device__ __forceinline__ double wave_inclusive_sum(double v) {
     return v;
 }
 
+// Inclusive prefix sum of ints over the wave (lane order).
+__device__ __forceinline__ int wave_incl_sum_i(int v) {
+    v += dpp<DPP_ROW_SHR1, 0xF, true>(0, v);
+    v += dpp<DPP_ROW_SHR2, 0xF, true>(0, v);
+    v += dpp<DPP_ROW_SHR4, 0xF, true>(0, v);
+    v += dpp<DPP_ROW_SHR8, 0xF, true>(0, v);
+    v += dpp<DPP_BCAST15, 0xA>(0, v);
+    v += dpp<DPP_BCAST31, 0xC>(0, v);
+    return v;
+}
+
 // Wave-wide sum in double (order-free enough for a bound; never used where a
 // bit-exact float result is claimed).
 __device__ __forceinline__ double wave_sum_d(double v) {

@@ -69,16 +69,6 @@ __device__ __forceinline__ void wave_seg_scan(float &v, int &f) {
     seg_step(v, f, dpp<DPP_BCAST31, 0xC>(0.0f, v), dpp<DPP_BCAST31, 0xC>(0, f));
 }
 
-__device__ __forceinline__ int wave_incl_sum_i(int v) {
-    v += dpp<DPP_ROW_SHR1, 0xF, true>(0, v);
-    v += dpp<DPP_ROW_SHR2, 0xF, true>(0, v);
-    v += dpp<DPP_ROW_SHR4, 0xF, true>(0, v);
-    v += dpp<DPP_ROW_SHR8, 0xF, true>(0, v);
-    v += dpp<DPP_BCAST15, 0xA>(0, v);
-    v += dpp<DPP_BCAST31, 0xC>(0, v);
-    return v;
-}
-
 __device__ __forceinline__ int read_lane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 __device__ __forceinline__ float read_lane(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));

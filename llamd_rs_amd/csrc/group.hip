@@ -44,21 +44,31 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
         if ((unsigned)e < (unsigned)n_expert) atomicAdd(&hist[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int start = 0, sub = 0;
-        for (int e = 0; e < n_expert; ++e) {
-            const int c = hist[e];
-            grp_expert[e] = e;
-            grp_start[e] = start;
-            grp_count[e] = c;
-            sub_start[e] = sub;
-            sub_lds[e] = sub;
-            start_lds[e] = start;
-            cursor[e] = start;
-            start += c;
-            sub += (c + 15) / 16;
-        }
-        sub_start[n_expert] = sub;
+    // exclusive prefix sums over experts (thread e owns expert e) of the
+    // pair counts and of the 16-token chunk counts
+    __shared__ int wsum_c[GROUP_MAX_EXPERTS / WAVE], wsum_s[GROUP_MAX_EXPERTS / WAVE];
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = tid < n_expert ? hist[tid] : 0, ch = (c + 15) / 16;
+    const int ic = wave_incl_sum_i(c), is = wave_incl_sum_i(ch);
+    if (lane == WAVE - 1) {
+        wsum_c[wave] = ic;
+        wsum_s[wave] = is;
+    }
+    __syncthreads();
+    int start = ic - c, sub = is - ch;
+    for (int w = 0; w < wave; ++w) {
+        start += wsum_c[w];
+        sub += wsum_s[w];
+    }
+    if (tid < n_expert) {
+        grp_expert[tid] = tid;
+        grp_start[tid] = start;
+        grp_count[tid] = c;
+        sub_start[tid] = sub;
+        sub_lds[tid] = sub;
+        start_lds[tid] = start;
+        cursor[tid] = start;
+        if (tid == n_expert - 1) sub_start[n_expert] = sub + ch;
     }
     __syncthreads();
     for (int p = tid; p < n_pairs; p += blockDim.x) {
