@@ -88,6 +88,7 @@ union DecodeLds {
         float terms[2][16][TILE_ROWS][8];
         float gu[2][TILE_ROWS];
         RouteLds rsh;
+        int given[MAX_USED];
         uint64_t tab[32];
         int8_t lq[GU_MAX_BLOCKS * QK_K];
         float ld[GU_MAX_BLOCKS];
@@ -307,11 +308,17 @@ __device__ void gateup_workgroup(const DecodeParams &p, DecodeLds &sm, int g, in
 __device__ void router_workgroup(const DecodeParams &p, DecodeLds &sm, int lane, int wave) {
     if (wave != 0) return;
     __builtin_amdgcn_s_setprio(3);
-    expf_ref_tab_fill(sm.g.rsh.tab);  // its load now, not after the wait
-    float l[RW];
+    // the gate/up tiles' selection, made here the same way: when certified,
+    // only the order of that set is left to the exact probabilities
     bool late = false;
+    const bool certain = select_experts(p, sm.g.rsh, late);
+    if (certain && lane < p.n_used) sm.g.given[lane] = sm.g.rsh.sorted[lane];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float l[RW];
     wait_logits(p, l, late);
-    route_finish(l, p.n_expert, p.n_used, true, sm.g.rsh, p.ids_out, p.w_out, nullptr);
+    route_finish(l, p.n_expert, p.n_used, true, sm.g.rsh, p.ids_out, p.w_out, nullptr,
+                 certain ? sm.g.given : nullptr);
     if (lane == 0 && late && p.stats) p.stats[3] = 1;
 }
 

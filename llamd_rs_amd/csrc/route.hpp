@@ -21,6 +21,7 @@ struct RouteLds {
     uint64_t tab[32];  // expf_ref's table
     float p[ROUTE_MAX_EXPERTS];
     int sorted[ROUTE_MAX_USED + 1];
+    int member[ROUTE_MAX_EXPERTS];  // route_finish with a given set: 1 for its experts
 };
 
 // Order-preserving 32-bit key of a float (larger float, larger key); 0 is
@@ -70,7 +71,8 @@ __device__ void wave_select(const float val[RW], const bool live[RW], int n_sel,
 // sequential total from -0.0, divide); if `resort`, select by probability;
 // then gather, clamp and renormalise (moe.rs:103-105).
 __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool resort,
-                             RouteLds &sh, int32_t *ids, float *weights, float *logits_used) {
+                             RouteLds &sh, int32_t *ids, float *weights, float *logits_used,
+                             const int *given = nullptr) {
     const int lane = threadIdx.x & 63;
     expf_ref_tab_fill(sh.tab);
     float m = -INFINITY;  // f32::max fold: NaN-ignoring, order-free
@@ -118,7 +120,48 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
             sh.p[i] = p[j];
         }
     }
-    if (resort) {
+    bool ranked = false;
+    if (resort && given) {
+        // The set is known (certified from the estimates): order its n_used
+        // experts by (probability desc, index asc) -- after checking that
+        // every member's probability key lies strictly above every other
+        // expert's, so the set is the top n_used by probability; else the
+        // full selection below runs.
+        const int id = lane < n_used ? given[lane] : 0;
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+            if (lane + WAVE * j < n_expert) sh.member[lane + WAVE * j] = 0;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane < n_used) sh.member[id] = 1;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        unsigned lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const int i = lane + WAVE * j;
+            if (i < n_expert) {
+                const unsigned k = sort_key(p[j]);
+                if (sh.member[i]) lo = min(lo, k);
+                else hi = max(hi, k);
+            }
+        }
+        lo = (unsigned)wave_reduce((int)lo, -1, [](int a, int b) { return (int)min((unsigned)a, (unsigned)b); });
+        hi = (unsigned)wave_reduce((int)hi, 0, [](int a, int b) { return (int)max((unsigned)a, (unsigned)b); });
+        if (lo > hi) {
+            const unsigned key = lane < n_used ? sort_key(sh.p[id]) : 0u;
+            int rank = 0;
+            for (int r = 0; r < n_used; ++r) {
+                const unsigned kr = (unsigned)__shfl((int)key, r, WAVE);
+                const int ir = __shfl(id, r, WAVE);
+                rank += (kr > key || (kr == key && ir < id)) ? 1 : 0;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane < n_used) sh.sorted[rank] = id;
+            ranked = true;
+        }
+    }
+    if (resort && !ranked) {
         bool live[RW];
 #pragma unroll
         for (int j = 0; j < RW; ++j) live[j] = lane + WAVE * j < n_expert;
