@@ -39,6 +39,7 @@ int g_tune_batch_decode_max = 16;
 }  // namespace
 int llamd::g_tune_model_graph = 1;  // whole-token decode replays a captured graph
 int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else three launches)
+int llamd::g_tune_model_fused_norm = 1;  // decode step: FFN norm inside the MoE decode launch
 namespace {
 
 int fail(const char *fmt, ...) {
@@ -156,6 +157,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "moe_fused")) {
         const int prev = g_tune_moe_fused;
         g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
+        return prev;
+    }
+    if (!strcmp(key, "model_fused_norm")) {
+        const int prev = g_tune_model_fused_norm;
+        g_tune_model_fused_norm = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "model_fused_attn")) {
@@ -723,6 +729,24 @@ MoeDecodeLaunch decode_launch(MoeLayer *m, const float *d_x, const float *d_res,
     dl.n_ff = m->n_ff;
     return dl;
 }
+
+}  // namespace
+
+int llamd::moe_forward_normed(void *h, const float *x, const float *o, const float *w, float eps,
+                              float *sum_out, float *out) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !x || !o || !w || !sum_out || !out) return -1;
+    if (g_tune_moe_fused != 2 || m->bf > 8 || m->be > 8) return -1;
+    MoeDecodeLaunch dl = decode_launch(m, sum_out, sum_out, out);
+    dl.norm_a = x;
+    dl.norm_b = o;
+    dl.norm_w = w;
+    dl.norm_eps = eps;
+    dl.norm_sum = sum_out;
+    return launch_moe_decode(dl, stream());
+}
+
+namespace {
 
 // Decode scratch for nseq sequences (the stream is drained first: no queued
 // kernel still reads the old buffers). The hand-off words start empty.

@@ -14,6 +14,7 @@ namespace llamd {
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
+extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode launch
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -73,8 +74,19 @@ struct MoeDecodeLaunch {
     int *stats;                     // [4]
     int k, n_expert, n_used, n_ff;
     int nseq = 1;  // a batch: every per-token array holds nseq rows (moe_decode.hip for_seq)
+    // Optional fused FFN norm: when norm_w is set, x = rms_norm(norm_a + norm_b) * norm_w is
+    // formed inside launch 1 (x is then unused), norm_a + norm_b is written to norm_sum for
+    // launch 2's residual (res must point at norm_sum). One sequence only.
+    const float *norm_a = nullptr, *norm_b = nullptr, *norm_w = nullptr;
+    float norm_eps = 0.0f;
+    float *norm_sum = nullptr;
 };
 int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st);
+// The decode step's FFN block with its norm (model.cpp): sum_out = x + o;
+// out = sum_out + moe(rms_norm(sum_out) * w). -1 when the layer's shapes need
+// the separate launches.
+int moe_forward_normed(void *moe, const float *x, const float *o, const float *w, float eps,
+                       float *sum_out, float *out);
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
                           const int32_t *grp_start, const int32_t *grp_count,
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,

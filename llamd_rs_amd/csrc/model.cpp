@@ -53,6 +53,7 @@ struct Model {
     hipGraphExec_t exec = nullptr;  // the captured step
     bool use_graph = true;
     bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
+    bool fused_norm = false;        // the FFN norm inside the MoE decode launch
     std::vector<void *> owned;     // device allocations to free
 };
 
@@ -110,8 +111,12 @@ bool enqueue_step(Model *m, hipStream_t st) {
         llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
         // ffn_inp = x + O, ffn_norm; then the MoE FFN with the second
         // residual: x = ffn_inp + moe
-        rc |= llamd::launch_add_rms_norm_mul(m->x, m->o, l.ffn_norm, m->ffn_inp, m->fn, E, m->eps, st);
-        rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
+        if (!m->fused_norm ||
+            llamd::moe_forward_normed(l.moe, m->x, m->o, l.ffn_norm, m->eps, m->ffn_inp, m->x)) {
+            rc |= llamd::launch_add_rms_norm_mul(m->x, m->o, l.ffn_norm, m->ffn_inp, m->fn, E,
+                                                 m->eps, st);
+            rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
+        }
     }
     if (rc || llamd_fwd_last_error()) return set_error("model: a launch failed (%s)", llamd_hip_last_error()) == 0;
     llamd_fwd_rms_norm_mul(m->x, m->output_norm, m->xn, E, m->eps);
@@ -196,6 +201,7 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->n_vocab = (int)edims[1];
     m->max_kv = max_kv;
     m->use_graph = llamd::g_tune_model_graph != 0;
+    m->fused_norm = llamd::g_tune_model_fused_norm != 0;
     m->fused_attn = llamd::g_tune_model_fused_attn != 0 &&
                     llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;

@@ -34,6 +34,7 @@
 // 30 us per token instead of 25: each cross-XCD hand-off costs microseconds,
 // more than the launch boundary it replaces.)
 #include "common.hpp"
+#include "exact_sum.hpp"
 #include "expf_ref.h"
 #include "launch.hpp"
 #include "q6k_tile.hpp"
@@ -61,6 +62,9 @@ struct DecodeParams {
     int *stats;                  // [4] calls, exact calls, certified calls, timed out
     size_t gu_stride, down_stride;
     int k, n_expert, n_used, n_ff, gu_tiles, bf, down_tiles, n_chain, n_gu, nseq;
+    const float *norm_a, *norm_b, *norm_w;  // fused FFN norm (norm_w null: x is given)
+    float norm_eps;
+    float *norm_sum;
 };
 
 // The parameters of sequence `seq` of a batch: every per-token array offset
@@ -168,13 +172,69 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     return certain;
 }
 
-__device__ void chain_workgroup(const DecodeParams &p, DecodeLds &sm, int blk, int lane, int wave) {
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// The fused FFN norm (layer.rs:170-172 and CpuBackend::rms_norm / mul,
+// llamd-cpu/src/lib.rs:55-75): v = a + b; x = (v * scale) * w with scale =
+// 1 / sqrt(sum(v^2) / k + eps), the sum in the reference's order
+// (exact_sum_nonneg). Every workgroup forms x itself, into xs (LDS); the
+// first chain workgroup also writes v for launch 2's residual. Called by
+// all threads of the workgroup.
+// wrow (or null): a router row this wave stages into wdst (LDS) meanwhile.
+__device__ void norm_prologue(const DecodeParams &p, float *xs, ExactSumLds &xl, bool write_sum,
+                              const float *wrow, float4 *wdst) {
+    const int m = xsum_run(p.k), j0 = min((int)threadIdx.x * m, p.k - 1), lane = threadIdx.x & 63;
+    float a[XSUM_M], b[XSUM_M], v[XSUM_M], sq[XSUM_M];
+#pragma unroll
+    for (int j = 0; j < XSUM_M; ++j) {
+        const int i = min(j0 + j, p.k - 1);
+        a[j] = p.norm_a[i];
+        b[j] = p.norm_b[i];
+    }
+    f4v wr[KMAX / 256];
+    if (wrow) {
+#pragma unroll
+        for (int j = 0; j < KMAX / 256; ++j)
+            if (64 * j < p.k / 4) wr[j] = ((const f4v *)wrow)[64 * j + lane];
+    }
+#pragma unroll
+    for (int j = 0; j < XSUM_M; ++j) {
+        v[j] = a[j] + b[j];
+        sq[j] = v[j] * v[j];
+    }
+    if (wrow) {
+#pragma unroll
+        for (int j = 0; j < KMAX / 256; ++j)
+            if (64 * j < p.k / 4) *(f4v *)&wdst[64 * j + lane] = wr[j];
+    }
+    const float *na = p.norm_a, *nb = p.norm_b;
+    const float sum = exact_sum_nonneg(sq, p.k, xl, [na, nb](int i) {
+        const float t = na[i] + nb[i];
+        return t * t;
+    });
+    const float scale = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, (float)p.k) + p.norm_eps));
+#pragma unroll
+    for (int j = 0; j < XSUM_M; ++j) {
+        const int i = j0 + j;
+        if (j < m && i < p.k) {
+            xs[i] = (v[j] * scale) * p.norm_w[i];
+            if (write_sum) p.norm_sum[i] = v[j];
+        }
+    }
+    __syncthreads();
+}
+
+// w_in_lds: the norm prologue has already put each wave's router row in
+// sm.prod (its loads ran under the norm); the products are then formed in
+// place.
+__device__ void chain_workgroup(const DecodeParams &p, DecodeLds &sm, int blk, int lane, int wave,
+                                bool w_in_lds) {
     const int e = wave & 3;
     const int row = blk * CHAIN_EXPERTS + e;
     const int n4 = p.k / 4;
     if (wave < CHAIN_EXPERTS && row < p.n_expert) {
-        const float4 *w4 = (const float4 *)(p.rw + (size_t)row * p.k);
-        const float4 *x4 = (const float4 *)p.x;
+        const float4 *w4 = w_in_lds ? sm.prod[e] : (const float4 *)(p.rw + (size_t)row * p.k);
+        const float4 *x4 = (const float4 *)p.x;  // LDS when the norm is fused
         float4 wr[KMAX / 256], xr[KMAX / 256];
 #pragma unroll
         for (int j = 0; j < KMAX / 256; ++j)
@@ -326,13 +386,24 @@ __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
     asm volatile("" ::"s"(p.w_gate), "s"(p.w_up), "s"(p.rw), "s"(p.x), "s"(p.slots),
                  "s"(p.gu_stride), "s"(p.k), "s"(p.n_expert), "s"(p.n_used), "s"(p.n_chain));
     __shared__ DecodeLds sm;
+    __shared__ __align__(16) float xs[KMAX];  // the fused norm's output
+    __shared__ ExactSumLds xl;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // all sequences' chain workgroups first (the gate/up ones wait on them),
     // then the gate/up tiles, then one router workgroup per sequence
     const int b = blockIdx.x, chains = p.n_chain * p.nseq, gus = p.n_gu * p.nseq;
+    if (p.norm_w && b < chains + gus) {
+        // one sequence: every chain and gate/up workgroup forms x itself;
+        // chain waves 0-3 stage their router rows under it
+        const int row = b * CHAIN_EXPERTS + (wave & 3);
+        const bool stage = b < chains && wave < CHAIN_EXPERTS && row < p.n_expert;
+        norm_prologue(p, xs, xl, b == 0, stage ? p.rw + (size_t)row * p.k : nullptr,
+                      sm.prod[wave & 3]);
+        p.x = xs;
+    }
     if (b < chains) {
-        chain_workgroup(for_seq(p, b / p.n_chain), sm, b % p.n_chain, lane, wave);
+        chain_workgroup(for_seq(p, b / p.n_chain), sm, b % p.n_chain, lane, wave, p.norm_w != nullptr);
     } else if (b < chains + gus) {
         const int g = b - chains;
         gateup_workgroup(for_seq(p, g / p.n_gu), sm, g % p.n_gu, lane, wave);
@@ -505,6 +576,14 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     p.n_chain = (l.n_expert + CHAIN_EXPERTS - 1) / CHAIN_EXPERTS;
     p.n_gu = l.n_used * p.gu_tiles;
     p.nseq = l.nseq;
+    p.norm_a = l.norm_a;
+    p.norm_b = l.norm_b;
+    p.norm_w = l.norm_w;
+    p.norm_eps = l.norm_eps;
+    p.norm_sum = l.norm_sum;
+    if (p.norm_w && (l.nseq != 1 || !l.norm_a || !l.norm_b || !l.norm_sum || l.res != l.norm_sum ||
+                     l.k > KMAX || l.k > XSUM_M * 512))
+        return -1;
     hipLaunchKernelGGL(moe_router_gateup, dim3((p.n_chain + p.n_gu + 1) * l.nseq), dim3(512), 0, st, p);
     hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles, l.nseq), dim3(64 * l.n_used), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
