@@ -375,10 +375,11 @@ __device__ void router_workgroup(const DecodeParams &p, DecodeLds &sm, int lane,
     if (certain && lane < p.n_used) sm.g.given[lane] = sm.g.rsh.sorted[lane];
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    expf_ref_tab_fill(sm.g.rsh.tab);
     float l[RW];
     wait_logits(p, l, late);
     route_finish(l, p.n_expert, p.n_used, true, sm.g.rsh, p.ids_out, p.w_out, nullptr,
-                 certain ? sm.g.given : nullptr);
+                 certain ? sm.g.given : nullptr, true);
     if (lane == 0 && late && p.stats) p.stats[3] = 1;
 }
 

@@ -21,7 +21,6 @@ struct RouteLds {
     uint64_t tab[32];  // expf_ref's table
     float p[ROUTE_MAX_EXPERTS];
     int sorted[ROUTE_MAX_USED + 1];
-    int member[ROUTE_MAX_EXPERTS];  // route_finish with a given set: 1 for its experts
 };
 
 // Order-preserving 32-bit key of a float (larger float, larger key); 0 is
@@ -72,9 +71,9 @@ __device__ void wave_select(const float val[RW], const bool live[RW], int n_sel,
 // then gather, clamp and renormalise (moe.rs:103-105).
 __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool resort,
                              RouteLds &sh, int32_t *ids, float *weights, float *logits_used,
-                             const int *given = nullptr) {
+                             const int *given = nullptr, bool tab_ready = false) {
     const int lane = threadIdx.x & 63;
-    expf_ref_tab_fill(sh.tab);
+    if (!tab_ready) expf_ref_tab_fill(sh.tab);
     float m = -INFINITY;  // f32::max fold: NaN-ignoring, order-free
 #pragma unroll
     for (int j = 0; j < RW; ++j)
@@ -128,21 +127,21 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         // expert's, so the set is the top n_used by probability; else the
         // full selection below runs.
         const int id = lane < n_used ? given[lane] : 0;
+        bool mem[RW];
 #pragma unroll
-        for (int j = 0; j < RW; ++j)
-            if (lane + WAVE * j < n_expert) sh.member[lane + WAVE * j] = 0;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (lane < n_used) sh.member[id] = 1;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (int j = 0; j < RW; ++j) mem[j] = false;
+        for (int q = 0; q < n_used; ++q) {
+            const int gq = __builtin_amdgcn_readlane(id, q);
+#pragma unroll
+            for (int j = 0; j < RW; ++j) mem[j] = mem[j] || lane + WAVE * j == gq;
+        }
         unsigned lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
         for (int j = 0; j < RW; ++j) {
             const int i = lane + WAVE * j;
             if (i < n_expert) {
                 const unsigned k = sort_key(p[j]);
-                if (sh.member[i]) lo = min(lo, k);
+                if (mem[j]) lo = min(lo, k);
                 else hi = max(hi, k);
             }
         }
@@ -152,8 +151,8 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
             const unsigned key = lane < n_used ? sort_key(sh.p[id]) : 0u;
             int rank = 0;
             for (int r = 0; r < n_used; ++r) {
-                const unsigned kr = (unsigned)__shfl((int)key, r, WAVE);
-                const int ir = __shfl(id, r, WAVE);
+                const unsigned kr = (unsigned)__builtin_amdgcn_readlane((int)key, r);
+                const int ir = __builtin_amdgcn_readlane(id, r);
                 rank += (kr > key || (kr == key && ir < id)) ? 1 : 0;
             }
             __builtin_amdgcn_wave_barrier();
@@ -176,7 +175,8 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         const int id = lane < n_used ? sh.sorted[lane] : 0;
         const float raw = lane < n_used ? sh.p[id] : 0.0f;
         float wsum = -0.0f;
-        for (int q = 0; q < n_used; ++q) wsum = wsum + __shfl(raw, q, WAVE);
+        for (int q = 0; q < n_used; ++q)
+            wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(raw), q));
         wsum = fmaxf(wsum, WEIGHT_SUM_FLOOR);
         if (lane < n_used) {
             ids[lane] = id;
