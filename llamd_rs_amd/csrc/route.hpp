@@ -21,6 +21,10 @@ struct RouteLds {
     uint64_t tab[32];  // expf_ref's table
     float p[ROUTE_MAX_EXPERTS];
     int sorted[ROUTE_MAX_USED + 1];
+    int member[ROUTE_MAX_EXPERTS];      // route_finish with a given set: 1 for its experts
+    unsigned ckey[ROUTE_MAX_USED];      // the given set's probability keys
+    int cid[ROUTE_MAX_USED];            // and ids
+    float raw[ROUTE_MAX_USED];          // the chosen probabilities, in routing order
 };
 
 // Order-preserving 32-bit key of a float (larger float, larger key); 0 is
@@ -127,35 +131,50 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         // expert's, so the set is the top n_used by probability; else the
         // full selection below runs.
         const int id = lane < n_used ? given[lane] : 0;
-        bool mem[RW];
+        // membership flags in LDS (one wave: a wave barrier orders them)
 #pragma unroll
-        for (int j = 0; j < RW; ++j) mem[j] = false;
-        for (int q = 0; q < n_used; ++q) {
-            const int gq = __builtin_amdgcn_readlane(id, q);
-#pragma unroll
-            for (int j = 0; j < RW; ++j) mem[j] = mem[j] || lane + WAVE * j == gq;
-        }
+        for (int j = 0; j < RW; ++j)
+            if (lane + WAVE * j < n_expert) sh.member[lane + WAVE * j] = 0;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane < n_used) sh.member[id] = 1;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         unsigned lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
         for (int j = 0; j < RW; ++j) {
             const int i = lane + WAVE * j;
             if (i < n_expert) {
                 const unsigned k = sort_key(p[j]);
-                if (mem[j]) lo = min(lo, k);
+                if (sh.member[i]) lo = min(lo, k);
                 else hi = max(hi, k);
             }
         }
         lo = (unsigned)wave_reduce((int)lo, -1, [](int a, int b) { return (int)min((unsigned)a, (unsigned)b); });
         hi = (unsigned)wave_reduce((int)hi, 0, [](int a, int b) { return (int)max((unsigned)a, (unsigned)b); });
         if (lo > hi) {
+            // each member's place: how many members beat it (the n_used
+            // (key, id) pairs read back from LDS together)
             const unsigned key = lane < n_used ? sort_key(sh.p[id]) : 0u;
-            int rank = 0;
-            for (int r = 0; r < n_used; ++r) {
-                const unsigned kr = (unsigned)__builtin_amdgcn_readlane((int)key, r);
-                const int ir = __builtin_amdgcn_readlane(id, r);
-                rank += (kr > key || (kr == key && ir < id)) ? 1 : 0;
+            if (lane < n_used) {
+                sh.ckey[lane] = key;
+                sh.cid[lane] = id;
             }
             __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            int rank = 0;
+            for (int r = 0; r < n_used; r += 8) {
+                unsigned kr[8];
+                int ir[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    kr[u] = sh.ckey[min(r + u, n_used - 1)];
+                    ir[u] = sh.cid[min(r + u, n_used - 1)];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    rank += (r + u < n_used && (kr[u] > key || (kr[u] == key && ir[u] < id))) ? 1 : 0;
+            }
             if (lane < n_used) sh.sorted[rank] = id;
             ranked = true;
         }
@@ -174,9 +193,17 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         // sum (moe.rs:103-105). Lane q gathers raw q; lane 0 adds them in order.
         const int id = lane < n_used ? sh.sorted[lane] : 0;
         const float raw = lane < n_used ? sh.p[id] : 0.0f;
+        if (lane < n_used) sh.raw[lane] = raw;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         float wsum = -0.0f;
-        for (int q = 0; q < n_used; ++q)
-            wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(raw), q));
+        for (int q = 0; q < n_used; q += 8) {
+            float rv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) rv[u] = sh.raw[min(q + u, n_used - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) wsum = wsum + (q + u < n_used ? rv[u] : -0.0f);
+        }
         wsum = fmaxf(wsum, WEIGHT_SUM_FLOOR);
         if (lane < n_used) {
             ids[lane] = id;
