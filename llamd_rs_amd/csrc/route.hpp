@@ -24,7 +24,6 @@ struct RouteLds {
     int member[ROUTE_MAX_EXPERTS];      // route_finish with a given set: 1 for its experts
     unsigned ckey[ROUTE_MAX_USED];      // the given set's probability keys
     int cid[ROUTE_MAX_USED];            // and ids
-    float raw[ROUTE_MAX_USED];          // the chosen probabilities, in routing order
 };
 
 // Order-preserving 32-bit key of a float (larger float, larger key); 0 is
@@ -193,17 +192,16 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         // sum (moe.rs:103-105). Lane q gathers raw q; lane 0 adds them in order.
         const int id = lane < n_used ? sh.sorted[lane] : 0;
         const float raw = lane < n_used ? sh.p[id] : 0.0f;
-        if (lane < n_used) sh.raw[lane] = raw;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // the first 8 by readlane with immediate lane numbers (no LDS round
+        // trip), any beyond one at a time; -0.0 past n_used changes nothing
         float wsum = -0.0f;
-        for (int q = 0; q < n_used; q += 8) {
-            float rv[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) rv[u] = sh.raw[min(q + u, n_used - 1)];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) wsum = wsum + (q + u < n_used ? rv[u] : -0.0f);
+        for (int u = 0; u < 8; ++u) {
+            const float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(raw), u));
+            wsum = wsum + (u < n_used ? r : -0.0f);
         }
+        for (int q = 8; q < n_used; ++q)
+            wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(raw), q));
         wsum = fmaxf(wsum, WEIGHT_SUM_FLOOR);
         if (lane < n_used) {
             ids[lane] = id;
