@@ -46,8 +46,9 @@ __global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int r
     int q[4];
     float dv;
     quantize_wave_q(v, lane, q, dv);
+    const uint32_t dw = chunk_dword(q, lane);
     for (int k = 0; k < fan; ++k)
-        store_chunk(q, dv, lane, cq, cd, slot_of ? slot_of[(size_t)r * fan + k] : r, b, blocks);
+        store_chunk(dw, dv, lane, cq, cd, slot_of ? slot_of[(size_t)r * fan + k] : r, b, blocks);
 }
 
 // act[i] = silu(gate[i]) * up[i], then Q8_K of act. Optionally stores act.
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k_chunks(const float *gate, cons
     int q[4];
     float dv;
     quantize_wave_q(v, lane, q, dv);
-    store_chunk(q, dv, lane, cq, cd, slot_of[r], b, blocks);
+    store_chunk(chunk_dword(q, lane), dv, lane, cq, cd, slot_of[r], b, blocks);
 }
 
 __global__ void silu_mul_f32(const float *gate, const float *up, float *out, int n) {

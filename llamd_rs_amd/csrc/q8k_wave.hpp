@@ -71,16 +71,30 @@ __device__ __forceinline__ void quantize_wave(const float v[4], int lane, int8_t
 constexpr int CHUNK_TOKENS = 16;
 constexpr int CHUNK_BLOCK_BYTES = 8 * 512;
 
-__device__ __forceinline__ void store_chunk(const int q[4], float dv, int lane, int8_t *cq, float *cd,
-                                            int slot, int b, int blocks) {
+// The wave's quants regrouped for the chunked layout: lane L ends up with
+// the 4 bytes of class plane L / 8 at bytes 4 (L % 8) .. +3 of the token's
+// 32 -- elements 8k + L / 8 for k = 4 (L % 8) .. +3 -- gathered from the
+// lanes that hold them (lane e / 4 holds element e), so each lane then
+// stores one dword per destination instead of four scattered bytes.
+__device__ __forceinline__ uint32_t chunk_dword(const int q[4], int lane) {
+    const uint32_t own = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                         ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    const int c = lane >> 3, k0 = 4 * (lane & 7);
+    uint32_t out = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t v = (uint32_t)__shfl((int)own, 2 * (k0 + t) + (c >> 2), WAVE);
+        out |= ((v >> (8 * (c & 3))) & 0xFFu) << (8 * t);
+    }
+    return out;
+}
+
+__device__ __forceinline__ void store_chunk(uint32_t dword, float dv, int lane, int8_t *cq,
+                                            float *cd, int slot, int b, int blocks) {
     if (slot < 0) return;  // a pair with no expert (out-of-range id)
     const size_t base = ((size_t)(slot / CHUNK_TOKENS) * blocks + b);
     int8_t *dst = cq + base * CHUNK_BLOCK_BYTES + (slot % CHUNK_TOKENS) * 32;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = 4 * lane + i;
-        dst[(e & 7) * 512 + (e >> 3)] = (int8_t)q[i];
-    }
+    *(uint32_t *)(dst + (lane >> 3) * 512 + 4 * (lane & 7)) = dword;
     if (lane == 0) cd[base * CHUNK_TOKENS + slot % CHUNK_TOKENS] = dv;
 }
 
