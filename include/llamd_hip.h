@@ -53,7 +53,9 @@ size_t llamd_rocm_free_mem(void);
 const char *llamd_hip_last_error(void);
 /* Not in the reference: tuning overrides for measurement. Returns the previous
  * value, -1 for an unknown key. "mv_ks": waves per 16-row tile of the Q6_K
- * matvec (1, 2 or 4; 0 = chosen from the shape). */
+ * matvec (1, 2 or 4; 0 = chosen from the shape); "batched_twin": the
+ * prefill GEMM's waves take two 16-token chunks of one expert (1, default)
+ * or one (0). */
 int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */

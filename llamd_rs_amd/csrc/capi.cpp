@@ -179,6 +179,11 @@ int llamd_hip_tune(const char *key, int value) {
         g_tune_batch_decode_max = value;
         return prev;
     }
+    if (!strcmp(key, "batched_twin")) {
+        const int prev = g_tune_batched_twin;
+        g_tune_batched_twin = value ? 1 : 0;
+        return prev;
+    }
     if (!strcmp(key, "mv_ks")) {
         const int prev = g_tune_mv_ks;
         g_tune_mv_ks = value;
@@ -945,7 +950,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
         bool ok = m->p_xq.alloc((size_t)chunks * m->be * CHUNK_BLOCK) &&
                   m->p_xd.alloc((size_t)chunks * m->be * CHUNK * 4) &&
                   m->p_grp_e.alloc(m->n_expert * 4) && m->p_grp_s.alloc(m->n_expert * 4) &&
-                  m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc((m->n_expert + 1) * 4) &&
+                  m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc(2 * (m->n_expert + 1) * 4) &&
                   m->p_slot.alloc(NP * 4) && m->p_idx.alloc(NP * 4) &&
                   m->p_g.alloc(NP * m->n_ff * 4) && m->p_u.alloc(NP * m->n_ff * 4) &&
                   m->p_aq.alloc((size_t)chunks * m->bf * CHUNK_BLOCK) &&

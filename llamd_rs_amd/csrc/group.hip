@@ -13,7 +13,9 @@
 // Outputs (all experts are groups, empty ones included):
 //   grp_expert[e] = e, grp_start[e], grp_count[e],
 //   sub_start[0..n_expert] = prefix sum of ceil(count/16) (16-token chunks
-//   of the batched kernel), slot_of_pair[p] = the chunk slot of pair p
+//   of the batched kernel), followed by twin_start = sub_start[n_expert + 1
+//   .. 2 n_expert + 1] = prefix sum of ceil(chunks/2) (twins: two chunks of
+//   one expert, the work items of the twin batched kernel), slot_of_pair[p] = the chunk slot of pair p
 //   (chunk sub_start[e] + j / 16, token j % 16 for the j-th pair of expert
 //   e), pair_idx[i] = the pair index t * n_used + k at sorted position i.
 #include "common.hpp"
@@ -46,29 +48,36 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     __syncthreads();
     // exclusive prefix sums over experts (thread e owns expert e) of the
     // pair counts and of the 16-token chunk counts
-    __shared__ int wsum_c[GROUP_MAX_EXPERTS / WAVE], wsum_s[GROUP_MAX_EXPERTS / WAVE];
+    __shared__ int wsum_c[GROUP_MAX_EXPERTS / WAVE], wsum_s[GROUP_MAX_EXPERTS / WAVE],
+        wsum_t[GROUP_MAX_EXPERTS / WAVE];
     const int lane = tid & 63, wave = tid >> 6;
-    const int c = tid < n_expert ? hist[tid] : 0, ch = (c + 15) / 16;
-    const int ic = wave_incl_sum_i(c), is = wave_incl_sum_i(ch);
+    const int c = tid < n_expert ? hist[tid] : 0, ch = (c + 15) / 16, tw = (ch + 1) / 2;
+    const int ic = wave_incl_sum_i(c), is = wave_incl_sum_i(ch), it = wave_incl_sum_i(tw);
     if (lane == WAVE - 1) {
         wsum_c[wave] = ic;
         wsum_s[wave] = is;
+        wsum_t[wave] = it;
     }
     __syncthreads();
-    int start = ic - c, sub = is - ch;
+    int start = ic - c, sub = is - ch, tst = it - tw;
     for (int w = 0; w < wave; ++w) {
         start += wsum_c[w];
         sub += wsum_s[w];
+        tst += wsum_t[w];
     }
     if (tid < n_expert) {
         grp_expert[tid] = tid;
         grp_start[tid] = start;
         grp_count[tid] = c;
         sub_start[tid] = sub;
+        sub_start[n_expert + 1 + tid] = tst;
         sub_lds[tid] = sub;
         start_lds[tid] = start;
         cursor[tid] = start;
-        if (tid == n_expert - 1) sub_start[n_expert] = sub + ch;
+        if (tid == n_expert - 1) {
+            sub_start[n_expert] = sub + ch;
+            sub_start[2 * n_expert + 1] = tst + tw;
+        }
     }
     __syncthreads();
     for (int p = tid; p < n_pairs; p += blockDim.x) {

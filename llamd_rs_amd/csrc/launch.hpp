@@ -11,6 +11,7 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
+extern int g_tune_batched_twin;  // grouped q6k_mv_batched: two chunks of one expert per wave
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
@@ -107,7 +108,8 @@ int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t
 int launch_swiglu_q8k_chunks(const float *gate, const float *up, int rows, int blocks,
                              const int32_t *slot_of, int8_t *cq, float *cd, hipStream_t st);
 // moe grouping (group.hip): counting sort of the (token, k) pairs by expert.
-// Outputs grp_* per expert, sub_start (prefix of ceil(count/16)), for each
+// Outputs grp_* per expert, sub_start (prefix of ceil(count/16), then the
+// twin prefix of ceil(chunks/2): 2 * (n_expert + 1) entries), for each
 // pair p = token * n_used + k its chunk slot slot_of_pair[p], and for each
 // sorted position its pair index pair_idx.
 int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,

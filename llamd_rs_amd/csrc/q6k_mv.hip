@@ -537,10 +537,128 @@ __device__ __forceinline__ void fold_digits(uint64_t codes, const FoldScales &f,
 }
 
 
+// The work of one wave on one 16-row tile t of expert `expert`'s weights
+// against NC consecutive 16-token chunks sub0.. of the token-chunked
+// activations (local chunk numbers st0.. inside the group of `cnt` pairs
+// starting at sorted position `start`). The weight codes are unpacked and
+// folded once per class and feed the MFMAs of all NC chunks, so a second
+// chunk costs only its MFMAs and its float epilogue. Each chunk's class plane
+// of a block is one contiguous 512-byte load for the wave.
+template <int NC>
+__device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int t, int sub0,
+                                             int st0, int cnt, int start, int expert) {
+    const int n = lane & 15, s = lane >> 4;
+    const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
+    const size_t chunk_q = (size_t)p.blocks * CHUNK_BLOCK_BYTES, chunk_d = (size_t)p.blocks * CHUNK_TOKENS;
+    const int8_t *aq = p.act_q + (size_t)sub0 * chunk_q + n * 32 + 8 * s;
+    const float *ad = p.act_d + (size_t)sub0 * chunk_d + n;
+
+    float sums[NC][8][4];
+#pragma unroll
+    for (int u = 0; u < NC; ++u)
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sums[u][c][v] = 0.0f;
+
+    for (int b = 0; b < p.blocks; ++b, seg += SEG_BYTES) {
+        const uint4 q0 = *(const uint4 *)(seg + 16 * lane);
+        const uint4 q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
+        const uint4 q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
+        const uint32_t scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
+        const uint2 dw = *(const uint2 *)(seg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
+        float adb[NC];
+        long act[NC][8];
+#pragma unroll
+        for (int u = 0; u < NC; ++u) {
+            adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                act[u][c] = *(const long *)(aq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
+        }
+        const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
+        const FoldScales fs = fold_scales(scw);
+        // f16(d) of the lane's 4 rows (D rows 4s..4s+3) times the token's scale
+        const float d4[4] = {f16_bits_to_f32((uint16_t)(dw.x & 0xFFFF)),
+                             f16_bits_to_f32((uint16_t)(dw.x >> 16)),
+                             f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)),
+                             f16_bits_to_f32((uint16_t)(dw.y >> 16))};
+        float dd[NC][4];
+#pragma unroll
+        for (int u = 0; u < NC; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dd[u][v] = d4[v] * adb[u];
+        // software-pipelined by one class: the MFMAs of class c+1 are issued
+        // before the epilogue of class c reads its results
+        const v4i zero = {0, 0, 0, 0};
+        v4i dh[2][NC], dl[2][NC];
+        {
+            long a_lo, a_hi;
+            fold_digits((uint64_t)unpack_codes(nib, hb, 0), fs, a_lo, a_hi);
+#pragma unroll
+            for (int u = 0; u < NC; ++u) {
+                dh[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[u][0], zero, 0, 0, 0);
+                dl[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[u][0], zero, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (c + 1 < 8) {
+                long a_lo, a_hi;
+                fold_digits((uint64_t)unpack_codes(nib, hb, c + 1), fs, a_lo, a_hi);
+#pragma unroll
+                for (int u = 0; u < NC; ++u) {
+                    dh[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[u][c + 1], zero, 0, 0, 0);
+                    dl[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[u][c + 1], zero, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NC; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int aux = dh[c & 1][u][v] * 256 + dl[c & 1][u][v];
+                    sums[u][c][v] = sums[u][c][v] + dd[u][v] * (float)aux;
+                }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NC; ++u) {
+        const int tok = 16 * (st0 + u) + n;  // this lane's token (B operand / output column)
+        const bool tok_ok = tok < cnt;       // slots past the last token hold no data;
+                                             // their columns are never stored
+        float bv = -INFINITY;  // arg-max candidate of this lane's rows (lowest row on ties)
+        int bi = 0x7FFFFFFF;
+        if (tok_ok) {
+            const int pos = start + tok;
+            const int orow = p.pair_out ? p.pair_out[pos] : pos;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = t * TILE_ROWS + 4 * s + v;
+                if (row < p.rows) {
+                    float tot = -0.0f;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) tot = tot + sums[u][c][v];
+                    p.y[(size_t)orow * p.ldy + row] = tot;
+                    if (!isnan(tot)) argmax_step(bv, bi, tot, row);
+                }
+            }
+        }
+        if (p.amax_v) {
+            // combine the 4 lanes (s = 0..3) of each token: lanes n, n+16, n+32, n+48
+            argmax_step(bv, bi, __shfl_xor(bv, 16, WAVE), __shfl_xor(bi, 16, WAVE));
+            argmax_step(bv, bi, __shfl_xor(bv, 32, WAVE), __shfl_xor(bi, 32, WAVE));
+            if (s == 0 && tok_ok) {
+                p.amax_v[(size_t)tok * p.tiles + t] = bv;
+                p.amax_i[(size_t)tok * p.tiles + t] = bi;
+            }
+        }
+    }
+}
+
 // One wave per (group, 16-token chunk, 16-row tile). The chunk index is the
 // global sub-tile number, which is also where the activations of its 16
-// tokens sit in the token-chunked layout: each class plane of a block is one
-// contiguous 512-byte load for the wave.
+// tokens sit in the token-chunked layout.
 __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
     const int lane = threadIdx.x & 63;
     const int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -564,96 +682,42 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
         cnt = p.single_count;
         if (sub >= (cnt + 15) / 16) return;
     }
-    const int n = lane & 15, s = lane >> 4;
-    const int tok = 16 * st + n;               // this lane's token (B operand / output column)
-    const bool tok_ok = tok < cnt;             // slots past the last token hold no data;
-                                               // their columns are never stored
-    const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
-    const int8_t *aq = p.act_q + (size_t)sub * p.blocks * CHUNK_BLOCK_BYTES + n * 32 + 8 * s;
-    const float *ad = p.act_d + (size_t)sub * p.blocks * CHUNK_TOKENS + n;
+    batched_tile<1>(p, lane, t, sub, st, cnt, start, expert);
+}
 
-    float sums[8][4];
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sums[c][v] = 0.0f;
-
-    for (int b = 0; b < p.blocks; ++b, seg += SEG_BYTES) {
-        const uint4 q0 = *(const uint4 *)(seg + 16 * lane);
-        const uint4 q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
-        const uint4 q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
-        const uint32_t scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
-        const uint2 dw = *(const uint2 *)(seg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
-        const float adb = ad[(size_t)b * CHUNK_TOKENS];
-        long act[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-            act[c] = *(const long *)(aq + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
-        const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
-        const FoldScales fs = fold_scales(scw);
-        // f16(d) of the lane's 4 rows (D rows 4s..4s+3) times the token's scale
-        float dd[4];
-        dd[0] = f16_bits_to_f32((uint16_t)(dw.x & 0xFFFF)) * adb;
-        dd[1] = f16_bits_to_f32((uint16_t)(dw.x >> 16)) * adb;
-        dd[2] = f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)) * adb;
-        dd[3] = f16_bits_to_f32((uint16_t)(dw.y >> 16)) * adb;
-        // software-pipelined by one class: the MFMAs of class c+1 are issued
-        // before the epilogue of class c reads its results
-        const v4i zero = {0, 0, 0, 0};
-        v4i dh[2], dl[2];
-        {
-            long a_lo, a_hi;
-            fold_digits((uint64_t)unpack_codes(nib, hb, 0), fs, a_lo, a_hi);
-            dh[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[0], zero, 0, 0, 0);
-            dl[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[0], zero, 0, 0, 0);
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (c + 1 < 8) {
-                long a_lo, a_hi;
-                fold_digits((uint64_t)unpack_codes(nib, hb, c + 1), fs, a_lo, a_hi);
-                dh[(c + 1) & 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c + 1], zero, 0, 0, 0);
-                dl[(c + 1) & 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c + 1], zero, 0, 0, 0);
-            }
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int aux = dh[c & 1][v] * 256 + dl[c & 1][v];
-                sums[c][v] = sums[c][v] + dd[v] * (float)aux;
-            }
-        }
+// One wave per (group, twin, 16-row tile): a twin is two consecutive chunks
+// of one group (the group's last twin holds one chunk when its chunk count is
+// odd). twin_start = sub_start + n_groups + 1 is the prefix sum of
+// ceil(chunks/2) over the groups. The shared fold takes the VALU work of a
+// twin from 2 x 325 to 460 instructions per block; the register budget is
+// capped at 3 waves per SIMD (168 VGPRs, a few spilled), which measured 20%
+// faster than the uncapped 178 VGPRs at 2 waves and 5% faster than one chunk
+// per wave.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void q6k_mv_batched_twin(BatchParams p) {
+    const int lane = threadIdx.x & 63;
+    const int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = item % p.tiles;
+    const int tw = item / p.tiles;
+    const int32_t *twin_start = p.sub_start + p.n_groups + 1;
+    if (tw >= twin_start[p.n_groups]) return;
+    int lo = 0, hi = p.n_groups;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (twin_start[mid] <= tw) lo = mid; else hi = mid;
     }
-    float bv = -INFINITY;  // arg-max candidate of this lane's rows (lowest row on ties)
-    int bi = 0x7FFFFFFF;
-    if (tok_ok) {
-        const int pos = start + tok;
-        const int orow = p.pair_out ? p.pair_out[pos] : pos;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int row = t * TILE_ROWS + 4 * s + v;
-            if (row < p.rows) {
-                float tot = -0.0f;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) tot = tot + sums[c][v];
-                p.y[(size_t)orow * p.ldy + row] = tot;
-                if (!isnan(tot)) argmax_step(bv, bi, tot, row);
-            }
-        }
-    }
-    if (p.amax_v) {
-        // combine the 4 lanes (s = 0..3) of each token: lanes n, n+16, n+32, n+48
-        argmax_step(bv, bi, __shfl_xor(bv, 16, WAVE), __shfl_xor(bi, 16, WAVE));
-        argmax_step(bv, bi, __shfl_xor(bv, 32, WAVE), __shfl_xor(bi, 32, WAVE));
-        if (s == 0 && tok_ok) {
-            p.amax_v[(size_t)tok * p.tiles + t] = bv;
-            p.amax_i[(size_t)tok * p.tiles + t] = bi;
-        }
-    }
+    const int st = 2 * (tw - twin_start[lo]);
+    const int sub = p.sub_start[lo] + st;
+    const int cnt = p.grp_count[lo], start = p.grp_start[lo], expert = p.grp_expert[lo];
+    if (sub + 1 < p.sub_start[lo + 1])
+        batched_tile<2>(p, lane, t, sub, st, cnt, start, expert);
+    else
+        batched_tile<1>(p, lane, t, sub, st, cnt, start, expert);
 }
 
 }  // namespace
 
 int g_tune_mv_ks = 0;
+int g_tune_batched_twin = 1;
 
 namespace {
 
@@ -833,6 +897,13 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
     p.blocks = blocks;
     p.n_groups = n_groups;
+    if (grp_expert && g_tune_batched_twin) {
+        // twins: sum of ceil(ch/2) <= (sum of ch + n_groups) / 2
+        const long items = (long)p.tiles * ((max_chunks + n_groups + 1) / 2);
+        if (items <= 0) return 0;
+        hipLaunchKernelGGL(q6k_mv_batched_twin, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     const long items = (long)p.tiles * max_chunks;
     if (items <= 0) return 0;
     hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);

@@ -1,6 +1,6 @@
 """Named device workloads of the path, for profilers:
 
-    python -m llamd_rs_amd.workloads NAME [--iters N]
+    python -m llamd_rs_amd.workloads NAME [--iters N] [--tune KEY=VALUE ...]
 
 runs NAME's launches N times on synthetic seeded inputs (the shapes of
 BASELINE.json's configs, weights rotating where one copy would sit in the
@@ -132,10 +132,16 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("name", choices=sorted(WORKLOADS))
     ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="llamd_hip_tune overrides applied before the workload")
     args = ap.parse_args(argv)
     L = lib()
     if not rocm.available():
         raise SystemExit("no ROCm device visible")
+    for kv in args.tune:
+        key, _, val = kv.partition("=")
+        if L.llamd_hip_tune(key.encode(), int(val)) < 0:
+            raise SystemExit(f"unknown tune key {key}")
     t0 = time.time()
     WORKLOADS[args.name](L, args.iters)
     print(f"{args.name}: {args.iters} iterations in {time.time() - t0:.2f}s", flush=True)

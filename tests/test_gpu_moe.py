@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 
 import helpers as H
+from llamd_rs_amd._lib import lib
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -135,19 +136,28 @@ def test_moe_layer_near_tied_router_stays_exact(gpu):
     layer.close()
 
 
-def test_prefill_grouped_equals_token_major(gpu):
+@pytest.mark.parametrize("twin", [1, 0])
+def test_prefill_grouped_equals_token_major(gpu, twin):
     """R14: expert-grouped prefill == per-token moe_ffn, EXACT, including a
-    1-token case and an expert with more than 16 tokens."""
+    1-token case and experts of 1 to 5 16-token chunks (twin = 1: two chunks of
+    one expert per wave, with a lone chunk where the count is odd)."""
     from llamd_rs_amd import synth
     n_embd, n_ff, n_expert, n_used = 512, 256, 16, 4
     router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 700)
     layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
-    for n_tok in (1, 5, 37):
-        x = synth.normal(10 + n_tok, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
-        ids, w = synth.zipf_routing(20 + n_tok, 1.1, n_tok, n_expert, n_used)
-        got = layer.prefill(x, ids.astype(np.int32), w)
-        want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
-        assert bits_equal(got, want), n_tok
+    prev = lib().llamd_hip_tune(b"batched_twin", twin)
+    try:
+        for n_tok in (1, 5, 37, 80):
+            x = synth.normal(10 + n_tok, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+            ids, w = synth.zipf_routing(20 + n_tok, 1.1, n_tok, n_expert, n_used)
+            got = layer.prefill(x, ids.astype(np.int32), w)
+            want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
+            assert bits_equal(got, want), n_tok
+        if n_tok == 80:
+            chunks = -(-np.bincount(ids.ravel(), minlength=n_expert) // 16)
+            assert chunks.max() >= 3 and (chunks % 2 == 1).any() and (chunks == 2).any()
+    finally:
+        lib().llamd_hip_tune(b"batched_twin", prev)
     layer.close()
 
 
@@ -247,6 +257,13 @@ def test_prefill_full_config_512_tokens(gpu, qwen_layer):
     sample = sorted(set(range(0, n_tok, 16)) | set(np.flatnonzero((ids == top).any(axis=1))[:8].tolist()))
     want = O.moe_ffn_tokens(x[sample], n_embd, n_ff, n_expert, gate, up, down, ids[sample], w[sample])
     assert bits_equal(got[sample], want)
+    # the one-chunk-per-wave kernel gives every token the same bits
+    prev = lib().llamd_hip_tune(b"batched_twin", 0)
+    try:
+        single = layer.prefill(x, ids.astype(np.int32), w)
+    finally:
+        lib().llamd_hip_tune(b"batched_twin", prev)
+    assert bits_equal(single, got)
 
 
 def _host_bound(router, x):
