@@ -161,6 +161,9 @@ __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, con
     constexpr int U = 8;
     const float *sv_in = pv + (size_t)seq * nparts;
     const int *si_in = pi + (size_t)seq * nparts;
+    // the reference's incumbent (index 0), loaded before the reduction so its
+    // round trip overlaps the candidates'
+    const float v0 = threadIdx.x == 0 ? x[(size_t)seq * ld] : 0.0f;
     for (int base = threadIdx.x; base < nparts; base += U * blockDim.x) {
         float v[U];
         int id[U];
@@ -182,7 +185,6 @@ __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, con
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(bv, bi, sv[w], si[w]);
         // the reference's incumbent is index 0: a NaN there is never beaten,
         // and when nothing beats -inf the answer stays 0
-        const float v0 = x[(size_t)seq * ld];
         out[seq] = (isnan(v0) || bi == 0x7FFFFFFF) ? 0 : bi;
     }
 }
