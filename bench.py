@@ -512,6 +512,9 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     from llamd_rs_amd.gguf import Gguf
     fd, path = tempfile.mkstemp(suffix=".gguf")
     os.close(fd)
+    # --eager: the step's launches stay plain (no HIP graph capture), like
+    # every other region of a profiler run; read when the model is created
+    prev_graph = L.llamd_hip_tune(b"model_graph", 0 if EAGER_ONLY else 1)
     try:
         t0 = time.time()
         synth_model.write_model(path)
@@ -533,9 +536,11 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                            "us_per_token": dt / n * 1e6, "tok_s": n / dt, "tokens": n,
                            "positions": f"3..{2 + n}", "load_s": round(t_load, 1),
                            "per_call": "host call incl. logits download and one sync",
+                           "graph": not EAGER_ONLY,
                            "parity": "bit-identical to the CPU forward (tests/test_gpu_model.py)"}
     log(f"  decode token: {out['decode_token']}")
     dm.close()
+    L.llamd_hip_tune(b"model_graph", prev_graph)
     return out
 
 
