@@ -55,7 +55,9 @@ const char *llamd_hip_last_error(void);
  * value, -1 for an unknown key. "mv_ks": waves per 16-row tile of the Q6_K
  * matvec (1, 2 or 4; 0 = chosen from the shape); "batched_twin": the
  * prefill GEMM's waves take two 16-token chunks of one expert (1, default)
- * or one (0). */
+ * or one (0); "moe_polls": loads a wait inside the MoE decode kernel makes
+ * before the waiting wave computes the awaited router logit itself (default
+ * 2^18; 0 = at once; the results are the same bits). */
 int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */
@@ -169,14 +171,13 @@ void llamd_fwd_matvec_grouped_x2_splitk(const void *wa, const void *wb, const in
 void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
                                         const float *d_ad, float *d_out, int blocks, int rows,
                                         int n_used, int nsub);
-/* llamd.hip:1607-1611 (d_bsums may be NULL) */
+/* llamd.hip:1607-1611: qs, d in the reference's layout (no bsums) */
 void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks);
 /* llamd_forward.hip:802-805 (exact SiLU: glibc-identical expf) */
 void llamd_fwd_silu_mul(const float *gate, const float *up, float *out, int n);
 /* llamd_forward.hip:807-811, from given logits. probs may be NULL. */
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs);
-/* llamd_forward.hip:856-861 */
 /* llamd_forward.hip:759-763: out = rms_norm(x) * w over one row of n.
  * Bit-identical to CpuBackend::rms_norm + mul (llamd-cpu/src/lib.rs:55-75,
  * 112-113): in-order f32 sum of squares, correctly rounded sqrt and divide.
@@ -245,14 +246,13 @@ int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, f
 int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, float *out,
                                      int32_t *ids, float *weights, float *logits, int nseq);
 /* Routing statistics since create: calls, and calls routed on the exact
- * sequential router fold (every call, so the two are equal). Returns -1 if a
- * bounded wait inside the decode kernel ever timed out (never observed; it
- * would mean workgroups were not placed in index order). */
+ * sequential router fold (every call, so the two are equal). */
 int llamd_hip_moe_stats(void *h, int *calls, int *exact_calls);
 /* Diagnostics, no counterpart in the reference: counters[4] = {calls,
  * exact calls, calls whose top-k set was certified from the logit estimates
  * (gate/up started before the exact fold ended), 1 if a wait inside the
- * decode kernel ever timed out}; estimates (optional) [2][n_expert] = the
+ * decode kernel ever gave up and computed the awaited logit itself (same
+ * bits; a timing event only)}; estimates (optional) [2][n_expert] = the
  * last call's estimates T and bounds E, |logit - T| <= E. Synchronous. */
 int llamd_hip_moe_counters(void *h, int *counters, double *estimates);
 

@@ -75,7 +75,7 @@ def build_hip(jobs: int = 8) -> Path:
     for src in HOST_HIP_SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
         steps.append([HIPCC, "-x", "hip", "--offload-arch=" + ARCH, "-O2", "-std=c++17", "-fPIC",
-                      "-Wall", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-c", str(CSRC / src), "-o",
+                      "-ffp-contract=off", "-fno-fast-math", "-Wall", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-c", str(CSRC / src), "-o",
                       str(obj)])
         objs.append(obj)
     for src in HOST_SOURCES:

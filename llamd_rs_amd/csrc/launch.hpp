@@ -55,8 +55,10 @@ int launch_q6k_gateup_silu(const void *w_gate, const void *w_up, size_t expert_s
                            int rows, int blocks, hipStream_t st);
 // Expert-grouped batched matvec (see q6k_mv.hip). Activations are in the
 // token-chunked layout (q8k_wave.hpp): chunk k holds the 16 tokens of
-// sub-tile k. sub_start has n_groups+1 entries (prefix of ceil(count/16));
-// max_chunks bounds sub_start[n_groups] and sizes the grid. The output of the
+// sub-tile k. sub_start has 2 * (n_groups + 1) entries: the prefix of
+// ceil(count/16) per group, then (read while g_tune_batched_twin is on) the
+// prefix of ceil(chunks/2), as launch_moe_group writes them; max_chunks bounds
+// sub_start[n_groups] and sizes the grid. The output of the
 // pair at sorted position i is row pair_out[i] of y (nullptr: row i). With
 // grp_expert == nullptr there is a single group (expert 0) of n_groups tokens.
 // moe_decode.hip: one MoE decode layer (router, top-k, gate, up, SwiGLU,
@@ -81,11 +83,16 @@ struct MoeDecodeLaunch {
     const float *norm_a = nullptr, *norm_b = nullptr, *norm_w = nullptr;
     float norm_eps = 0.0f;
     float *norm_sum = nullptr;
+    // Loads a wait on another workgroup of launch 1 makes before it computes
+    // the awaited router logit itself (bit-identical either way). 0 forces
+    // that path on every wait; tests use it.
+    int polls = 1 << 18;
 };
 int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st);
 // The decode step's FFN block with its norm (model.cpp): sum_out = x + o;
-// out = sum_out + moe(rms_norm(sum_out) * w). -1 when the layer's shapes need
-// the separate launches.
+// out = sum_out + moe(rms_norm(sum_out) * w). Only for layers where
+// moe_normed_applies() holds (decided once, at model create); -1 is an error.
+bool moe_normed_applies(void *moe);
 int moe_forward_normed(void *moe, const float *x, const float *o, const float *w, float eps,
                        float *sum_out, float *out);
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
@@ -182,5 +189,28 @@ int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, i
 int launch_q8_0_mv(const void *planar, const float *x, float *y, int rows, int k, hipStream_t st);
 int launch_q8_0_dequant(const void *planar, int rows, int k, float *out, hipStream_t st);
 int launch_f32_mv(const float *w, const float *x, float *y, int rows, int k, hipStream_t st);
+
+// ---- shared by the C ABI's host files ----
+// The library's stream (capi.cpp).
+hipStream_t lib_stream();
+// Shape of a tiled Q6_K handle from llamd_rocm_upload_q6k[_experts]; -1 if p
+// is not one.
+int q6k_handle_shape(const void *p, int *rows, int *blocks, int *n_expert);
+// Device scratch of one LM-head call (capi.cpp lmhead_enqueue): Q8_K of x
+// (nseq == 1: xq [blocks*256], xd [blocks]; nseq > 1: the token-chunked cq,
+// cd of lmhead_chunk_*_bytes) and the per-tile arg-max candidates pv, pi
+// [nseq][ceil(rows/16)].
+struct LmHeadScratch {
+    int8_t *xq;
+    float *xd;
+    int8_t *cq;
+    float *cd;
+    float *pv;
+    int *pi;
+};
+size_t lmhead_chunk_q_bytes(int nseq, int blocks);
+size_t lmhead_chunk_d_bytes(int nseq, int blocks);
+int lmhead_enqueue(const void *w, int rows, int blocks, const float *d_x, int nseq,
+                   float *d_logits, int32_t *d_ids, const LmHeadScratch &sc);
 
 }  // namespace llamd

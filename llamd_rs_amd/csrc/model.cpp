@@ -111,8 +111,9 @@ bool enqueue_step(Model *m, hipStream_t st) {
         llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
         // ffn_inp = x + O, ffn_norm; then the MoE FFN with the second
         // residual: x = ffn_inp + moe
-        if (!m->fused_norm ||
-            llamd::moe_forward_normed(l.moe, m->x, m->o, l.ffn_norm, m->eps, m->ffn_inp, m->x)) {
+        if (m->fused_norm) {
+            rc |= llamd::moe_forward_normed(l.moe, m->x, m->o, l.ffn_norm, m->eps, m->ffn_inp, m->x);
+        } else {
             rc |= llamd::launch_add_rms_norm_mul(m->x, m->o, l.ffn_norm, m->ffn_inp, m->fn, E,
                                                  m->eps, st);
             rc |= llamd_hip_moe_forward(l.moe, m->fn, m->ffn_inp, m->x, 0);
@@ -261,6 +262,9 @@ void *llamd_hip_model_create(void *g, int max_kv) {
         }
     }
     if (!ok) return fail_out();
+    // the FFN norm inside the MoE decode launch, when the layer's shapes allow it
+    // (decided once here: a launch error in the step is then always an error)
+    m->fused_norm = m->fused_norm && llamd::moe_normed_applies(m->layers[0].moe);
 
     // RoPE table: theta = pos / powf(base, 2i/hd), sin / cos (llamd-cpu lib.rs:196-200),
     // with the host libm the reference's f32 powf / sin / cos call

@@ -65,6 +65,7 @@ struct DecodeParams {
     const float *norm_a, *norm_b, *norm_w;  // fused FFN norm (norm_w null: x is given)
     float norm_eps;
     float *norm_sum;
+    int polls;  // bound of every wait on another workgroup (slot_wait)
 };
 
 // The parameters of sequence `seq` of a batch: every per-token array offset
@@ -99,7 +100,10 @@ union DecodeLds {
     } g;
 };
 
-// Exact logits of the lane's experts, waiting for each (whole wave).
+// Exact logits of the lane's experts, waiting for each (whole wave). A wait
+// that gives up (the producing chain workgroup was not placed in time)
+// computes that logit here: the same rounded products folded in the same
+// order from -0.0 (moe.rs:73-80), so the routing never depends on timing.
 __device__ void wait_logits(const DecodeParams &p, float l[RW], bool &late) {
     const int lane = threadIdx.x & 63;
     bool lt = false;
@@ -108,8 +112,17 @@ __device__ void wait_logits(const DecodeParams &p, float l[RW], bool &late) {
         const int i = lane + WAVE * j;
         unsigned long long v = 0;
         if (i < p.n_expert) {
-            v = slot_wait(&p.slots[p.n_expert + i]);
-            lt = lt || v == SLOT_EMPTY;
+            v = slot_wait(&p.slots[p.n_expert + i], p.polls);
+            if (v == SLOT_EMPTY) {
+                lt = true;
+                const float *w = p.rw + (size_t)i * p.k;
+                float acc = -0.0f;
+                for (int t = 0; t < p.k; ++t) {
+                    const float prod = w[t] * p.x[t];
+                    acc = acc + prod;
+                }
+                v = __float_as_uint(acc);
+            }
         }
         l[j] = __uint_as_float((unsigned)v);
     }
@@ -130,7 +143,7 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
         live[j] = i < p.n_expert;
         unsigned long long v = 0;
         if (live[j]) {
-            v = slot_wait(&p.slots[i]);
+            v = slot_wait(&p.slots[i], p.polls);
             lt = lt || v == SLOT_EMPTY;
         }
         key[j] = __uint_as_float((unsigned)v);
@@ -394,9 +407,10 @@ __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
     // all sequences' chain workgroups first (the gate/up ones wait on them),
     // then the gate/up tiles, then one router workgroup per sequence
     const int b = blockIdx.x, chains = p.n_chain * p.nseq, gus = p.n_gu * p.nseq;
-    if (p.norm_w && b < chains + gus) {
-        // one sequence: every chain and gate/up workgroup forms x itself;
-        // chain waves 0-3 stage their router rows under it
+    if (p.norm_w) {
+        // one sequence: every workgroup forms x itself (the router
+        // workgroup for the fallback folds of wait_logits); chain waves 0-3
+        // stage their router rows under it
         const int row = b * CHAIN_EXPERTS + (wave & 3);
         const bool stage = b < chains && wave < CHAIN_EXPERTS && row < p.n_expert;
         norm_prologue(p, xs, xl, b == 0, stage ? p.rw + (size_t)row * p.k : nullptr,
@@ -582,6 +596,8 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     p.norm_w = l.norm_w;
     p.norm_eps = l.norm_eps;
     p.norm_sum = l.norm_sum;
+    p.polls = l.polls;
+    if (p.polls < 0) return -1;
     if (p.norm_w && (l.nseq != 1 || !l.norm_a || !l.norm_b || !l.norm_sum || l.res != l.norm_sum ||
                      l.k > KMAX || l.k > XSUM_M * 512))
         return -1;

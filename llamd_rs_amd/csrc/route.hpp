@@ -286,12 +286,13 @@ __device__ __forceinline__ void slot_store(unsigned long long *slot, unsigned lo
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Bounded wait for a slot to be filled. Only ever waits on workgroups with
-// lower indices, which the dispatcher has already placed; the bound (about a
-// quarter of a second) guarantees every wave exits even if that ever fails.
-// Returns SLOT_EMPTY on timeout.
-__device__ __forceinline__ unsigned long long slot_wait(const unsigned long long *slot) {
-    for (int it = 0; it < (1 << 18); ++it) {
+// Bounded wait for a slot to be filled: at most `polls` loads (about a
+// quarter of a second at the default 2^18). A producer normally has a lower
+// workgroup index and is already placed, but HIP does not promise dispatch
+// order, so every caller must survive SLOT_EMPTY: the MoE decode kernel then
+// computes the value it waited for itself (wait_logits), the same bits.
+__device__ __forceinline__ unsigned long long slot_wait(const unsigned long long *slot, int polls) {
+    for (int it = 0; it < polls; ++it) {
         const unsigned long long v =
             __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (v != SLOT_EMPTY) return v;

@@ -29,11 +29,15 @@ def value(t: int, v) -> bytes:
     return struct.pack(_FMT[t], v)
 
 
-def build(kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"GGUF",
-          n_kv=None, n_tensors=None, tail: bytes = b"") -> bytes:
-    """kvs: [(key, type, value)] (arrays: value = (inner_type, [items]));
-    tensors: [(name, dims, ggml_type, data_bytes)], laid out in order, each
-    at the next multiple of `alignment` from the data section's start."""
+def _bytes(data):
+    """bytes-like view of a tensor's data (numpy arrays as their raw bytes)."""
+    if hasattr(data, "dtype"):
+        import numpy as np
+        return memoryview(np.ascontiguousarray(data)).cast("B")
+    return memoryview(data).cast("B")
+
+
+def _layout(kvs, tensors, alignment, version, magic, n_kv, n_tensors):
     head = magic + struct.pack("<IQQ", version,
                                len(tensors) if n_tensors is None else n_tensors,
                                len(kvs) if n_kv is None else n_kv)
@@ -42,20 +46,40 @@ def build(kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"
     for name, dims, ty, data in tensors:
         at = placed.get(id(data))
         if at is None:
+            mv = _bytes(data)
             off = -(-off // alignment) * alignment
             at = placed[id(data)] = off
-            datas.append((off, data))
-            off += len(data)
+            datas.append((off, mv))
+            off += len(mv)
         infos.append(gstr(name) + struct.pack("<I", len(dims)) +
                      b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", ty, at))
     header = head + body + b"".join(infos)
-    pad = -len(header) % alignment
-    section = bytearray(off)
+    return header + b"\0" * (-len(header) % alignment), datas, off
+
+
+def build(kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"GGUF",
+          n_kv=None, n_tensors=None, tail: bytes = b"") -> bytes:
+    """kvs: [(key, type, value)] (arrays: value = (inner_type, [items]));
+    tensors: [(name, dims, ggml_type, data)] with data bytes or a numpy array,
+    laid out in order, each at the next multiple of `alignment` from the data
+    section's start."""
+    header, datas, size = _layout(kvs, tensors, alignment, version, magic, n_kv, n_tensors)
+    section = bytearray(size)
     for o, d in datas:
         section[o:o + len(d)] = d
-    return header + b"\0" * pad + bytes(section) + tail
+    return header + bytes(section) + tail
 
 
-def write(path, *args, **kw) -> None:
+def write(path, kvs, tensors, alignment: int = 32, version: int = 3, magic: bytes = b"GGUF",
+          n_kv=None, n_tensors=None, tail: bytes = b"") -> None:
+    """build(), streamed to the file (no copy of the data section in memory)."""
+    header, datas, size = _layout(kvs, tensors, alignment, version, magic, n_kv, n_tensors)
     with open(path, "wb") as f:
-        f.write(build(*args, **kw))
+        f.write(header)
+        pos = 0
+        for o, d in datas:
+            f.write(b"\0" * (o - pos))
+            f.write(d)
+            pos = o + len(d)
+        f.write(b"\0" * (size - pos))
+        f.write(tail)

@@ -14,30 +14,44 @@ QWEN3_30B_A3B = dict(n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, hd=128, n_
                      n_used=8, n_ff=768, n_vocab=151936, eps=1e-6, base=1_000_000.0)
 
 
-def write_model(path, hp=QWEN3_30B_A3B, seed=0) -> None:
+def write_model(path, hp=QWEN3_30B_A3B, seed=0, expert_sets: int = 1,
+                distinct_layers: bool = False) -> dict:
+    """Write the model and return its tensors {name: array} (arrays may be
+    shared between layers). With distinct_layers, every layer gets its own
+    norms, router and attention matrices; the expert tensors cycle through
+    `expert_sets` distinct copies (layer L uses set L % expert_sets)."""
     E, hd, nh, nkv = hp["n_embd"], hp["hd"], hp["n_head"], hp["n_head_kv"]
     ne, nff, V = hp["n_expert"], hp["n_ff"], hp["n_vocab"]
     s = seed * 100
-    norm = lambda k, n: (1 + 0.1 * synth.normal(k, 1.0, n)).astype(np.float32).tobytes()
-    layer = {  # one copy, shared by every layer
-        "attn_norm.weight": ([E], 0, norm(s + 1, E)),
-        "ffn_norm.weight": ([E], 0, norm(s + 2, E)),
-        "attn_q_norm.weight": ([hd], 0, norm(s + 3, hd)),
-        "attn_k_norm.weight": ([hd], 0, norm(s + 4, hd)),
-        "attn_q.weight": ([E, nh * hd], 14, synth.q6k_matrix(s + 5, 0.05, nh * hd, E).tobytes()),
-        "attn_k.weight": ([E, nkv * hd], 14, synth.q6k_matrix(s + 6, 0.05, nkv * hd, E).tobytes()),
-        "attn_v.weight": ([E, nkv * hd], 14, synth.q6k_matrix(s + 7, 0.05, nkv * hd, E).tobytes()),
-        "attn_output.weight": ([nh * hd, E], 14, synth.q6k_matrix(s + 8, 0.05, E, nh * hd).tobytes()),
-        "ffn_gate_inp.weight": ([E, ne], 0, synth.normal(s + 9, 0.05, ne * E).tobytes()),
-        "ffn_gate_exps.weight": ([E, nff, ne], 14, synth.q6k_matrix(s + 10, 0.05, ne * nff, E).tobytes()),
-        "ffn_up_exps.weight": ([E, nff, ne], 14, synth.q6k_matrix(s + 11, 0.05, ne * nff, E).tobytes()),
-        "ffn_down_exps.weight": ([nff, E, ne], 14, synth.q6k_matrix(s + 12, 0.05, ne * E, nff).tobytes()),
-    }
-    tensors = [("token_embd.weight", [E, V], 14, synth.q6k_matrix(s + 13, 0.5, V, E).tobytes()),
-               ("output.weight", [E, V], 14, synth.q6k_matrix(s + 14, 0.05, V, E).tobytes()),
-               ("output_norm.weight", [E], 0, norm(s + 15, E))]
+    norm = lambda k, n: (1 + 0.1 * synth.normal(k, 1.0, n)).astype(np.float32)
+    experts = [{
+        "ffn_gate_exps.weight": ([E, nff, ne], synth.q6k_matrix(s + 10 + 1000 * i, 0.05, ne * nff, E)),
+        "ffn_up_exps.weight": ([E, nff, ne], synth.q6k_matrix(s + 11 + 1000 * i, 0.05, ne * nff, E)),
+        "ffn_down_exps.weight": ([nff, E, ne], synth.q6k_matrix(s + 12 + 1000 * i, 0.05, ne * E, nff)),
+    } for i in range(expert_sets)]
+
+    def small(k):  # the per-layer tensors other than the experts
+        return {
+            "attn_norm.weight": ([E], norm(k + 1, E)),
+            "ffn_norm.weight": ([E], norm(k + 2, E)),
+            "attn_q_norm.weight": ([hd], norm(k + 3, hd)),
+            "attn_k_norm.weight": ([hd], norm(k + 4, hd)),
+            "attn_q.weight": ([E, nh * hd], synth.q6k_matrix(k + 5, 0.05, nh * hd, E)),
+            "attn_k.weight": ([E, nkv * hd], synth.q6k_matrix(k + 6, 0.05, nkv * hd, E)),
+            "attn_v.weight": ([E, nkv * hd], synth.q6k_matrix(k + 7, 0.05, nkv * hd, E)),
+            "attn_output.weight": ([nh * hd, E], synth.q6k_matrix(k + 8, 0.05, E, nh * hd)),
+            "ffn_gate_inp.weight": ([E, ne], synth.normal(k + 9, 0.05, ne * E).reshape(ne, E)),
+        }
+
+    shared = small(s)
+    w = {"token_embd.weight": ([E, V], synth.q6k_matrix(s + 13, 0.5, V, E)),
+         "output.weight": ([E, V], synth.q6k_matrix(s + 14, 0.05, V, E)),
+         "output_norm.weight": ([E], norm(s + 15, E))}
     for il in range(hp["n_layer"]):
-        tensors += [(f"blk.{il}.{n}", d, t, b) for n, (d, t, b) in layer.items()]
+        lay = small(s + 50 + 20 * il) if distinct_layers else shared
+        lay = dict(lay, **experts[il % expert_sets])
+        w.update({f"blk.{il}.{n}": v for n, v in lay.items()})
+    tensors = [(n, d, 0 if a.dtype == np.float32 else 14, a) for n, (d, a) in w.items()]
     p = "qwen3moe"
     kvs = [("general.architecture", W.STRING, p), (p + ".block_count", W.U32, hp["n_layer"]),
            (p + ".embedding_length", W.U32, E), (p + ".attention.head_count", W.U32, nh),
@@ -48,3 +62,4 @@ def write_model(path, hp=QWEN3_30B_A3B, seed=0) -> None:
            (p + ".expert_feed_forward_length", W.U32, nff),
            (p + ".feed_forward_length", W.U32, 6144), (p + ".context_length", W.U32, 40960)]
     W.write(path, kvs, tensors)
+    return {n: a for n, (d, a) in w.items()}

@@ -106,3 +106,15 @@ def q6k_block(codes: np.ndarray, scale: int, d: float) -> np.ndarray:
     blk[D_OFF] = dh & 0xFF
     blk[D_OFF + 1] = dh >> 8
     return blk
+
+
+def par_map(fn, items, workers: int | None = None) -> list:
+    """fn over items on a thread pool. The oracle's ctypes calls release the
+    GIL, so full-size oracle checks spread over the host's cores (at most 16:
+    a GPU box's CPU share)."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    items = list(items)
+    workers = workers or max(1, min(16, os.cpu_count() or 1, len(items)))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        return list(ex.map(fn, items))

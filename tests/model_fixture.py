@@ -66,14 +66,30 @@ class OracleModel:
         kv_dim = hp["n_head_kv"] * hp["hd"]
         self.K = np.zeros((hp["n_layer"], max_kv, kv_dim), np.float32)
         self.V = np.zeros_like(self.K)
-        E, V = hp["n_embd"], hp["n_vocab"]
-        self.embd = O.dequantize(14, w["token_embd.weight"], V * E).reshape(V, E)
+        self.row_bytes = hp["n_embd"] // 256 * 210   # one Q6_K embedding row
+
+    def embed(self, token):
+        rb = self.row_bytes
+        row = np.asarray(self.w["token_embd.weight"]).reshape(-1)[token * rb:(token + 1) * rb]
+        return O.dequantize(14, row, self.hp["n_embd"])
+
+    def lm_head(self, xn):
+        """matvec_quant over the vocabulary, rows split over a thread pool
+        (rows are independent: the same bits as one call)."""
+        import helpers as H
+        V, E = self.hp["n_vocab"], self.hp["n_embd"]
+        wo = np.asarray(self.w["output.weight"]).reshape(V, -1)
+        cuts = np.linspace(0, V, 17).astype(int) if V >= 4096 else np.array([0, V])
+        parts = H.par_map(lambda i: O.matvec_q6k(wo[cuts[i]:cuts[i + 1]].reshape(-1),
+                                                 int(cuts[i + 1] - cuts[i]), E, xn),
+                          range(len(cuts) - 1))
+        return np.concatenate(parts)
 
     def forward(self, token, pos):
         hp, w = self.hp, self.w
         E, hd, nh, nkv, eps = hp["n_embd"], hp["hd"], hp["n_head"], hp["n_head_kv"], hp["eps"]
         f32 = np.float32
-        x = self.embd[token].copy()
+        x = self.embed(token)
         for il in range(hp["n_layer"]):
             b = f"blk.{il}."
             attn_norm = O.rms_norm(x, 1, E, eps) * w[b + "attn_norm.weight"]
@@ -93,5 +109,5 @@ class OracleModel:
                                      w[b + "ffn_gate_inp.weight"], w[b + "ffn_gate_exps.weight"],
                                      w[b + "ffn_up_exps.weight"], w[b + "ffn_down_exps.weight"])
         xn = O.rms_norm(x, 1, E, eps) * w["output_norm.weight"]
-        logits = O.matvec_q6k(w["output.weight"], hp["n_vocab"], E, xn)
+        logits = self.lm_head(xn)
         return logits, O.argmax(logits)

@@ -70,3 +70,56 @@ def test_decode_loop_refuses_bad_tokens_and_positions(gpu, tmp_path):
         assert np.all(np.isfinite(logits)) and 0 <= nxt < 768
     finally:
         dm.close()
+
+
+def test_decode_full_qwen3_30b_a3b_widths(gpu, tmp_path):
+    """The whole-token step at Qwen3-30B-A3B's real widths: hidden 2048, 32
+    query / 4 kv heads of 128, 128 experts top-8 of n_ff 768, vocabulary
+    151936; 4 layers (each with its own norms, router and attention; two
+    distinct expert sets alternate), 3 tokens. Every logit's bits and the
+    argmax against the CPU forward composed from the oracle."""
+    from llamd_rs_amd import synth_model
+    from llamd_rs_amd.gguf import Gguf
+    hp = dict(synth_model.QWEN3_30B_A3B, n_layer=4)
+    p = tmp_path / "qwen3-30b-a3b-4l.gguf"
+    w = synth_model.write_model(p, hp, seed=7, expert_sets=2, distinct_layers=True)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=16)
+    p.unlink()
+    ref = MF.OracleModel(w, hp=hp, max_kv=16)
+    try:
+        assert (dm.n_layer, dm.n_embd, dm.n_vocab) == (4, 2048, 151936)
+        tok = 1234
+        for pos in range(3):
+            logits, nxt = dm.forward(tok, pos)
+            want, want_next = ref.forward(tok, pos)
+            assert bits_equal(logits, want), pos
+            assert nxt == want_next, pos
+            tok = nxt
+    finally:
+        dm.close()
+
+
+def test_decode_loop_exact_when_router_waits_give_up(gpu, tmp_path):
+    """The decode step with the FFN norm fused into the MoE launch, with every
+    cross-workgroup wait giving up at once (moe_polls = 0): the waiting waves
+    fold the router logits themselves from the normed x, same bits."""
+    from llamd_rs_amd._lib import lib
+    from llamd_rs_amd.gguf import Gguf
+    p = tmp_path / "tiny.gguf"
+    w = MF.make(p, seed=5)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=16)
+    ref = MF.OracleModel(w)
+    prev = lib().llamd_hip_tune(b"moe_polls", 0)
+    try:
+        tok = 9
+        for pos in range(4):
+            logits, nxt = dm.forward(tok, pos)
+            want, want_next = ref.forward(tok, pos)
+            assert bits_equal(logits, want), pos
+            assert nxt == want_next, pos
+            tok = nxt
+    finally:
+        lib().llamd_hip_tune(b"moe_polls", prev)
+        dm.close()
