@@ -264,6 +264,17 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
 void llamd_hip_lmhead_destroy(void *h);
 int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logits,
                              int32_t *d_ids);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): llamd_hip_lmhead_forward without a handle, allocating nothing.
+ * Its scratch is one file-scope device array per GPU (about 2.3 MB, held
+ * until the process ends), so rows <= 262144, blocks <= 32 (k <= 8192) and
+ * nseq <= 16; larger requests return -1. d_w is a tiled Q6_K handle of
+ * exactly rows x blocks. Calls that overlap on one GPU race on the array. */
+int llamd_hip_lmhead_forward_noalloc(const void *d_w, int rows, int blocks, const float *d_x,
+                                     int nseq, float *d_logits, int32_t *d_ids);
+/* Bytes of that array (for the caller's memory budget). */
+size_t llamd_hip_lmhead_noalloc_scratch_bytes(void);
 
 /* ---- timing on the library stream ---------------------------------------- */
 /* Not in the reference (its llamd_rocm_matvec_bench, llamd.hip:1101-1148,

@@ -120,6 +120,8 @@ SIGNATURES = {
     "llamd_hip_lmhead_create": (vp, [vp, i32, i32, i32]),
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),
+    "llamd_hip_lmhead_forward_noalloc": (i32, [vp, i32, i32, vp, i32, vp, vp]),
+    "llamd_hip_lmhead_noalloc_scratch_bytes": (sz, []),
     "llamd_hip_event_create": (vp, []),
     "llamd_hip_event_destroy": (None, [vp]),
     "llamd_hip_event_record": (i32, [vp]),
