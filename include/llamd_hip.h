@@ -9,12 +9,19 @@
  * signature; each cites the definition it replaces. Functions the reference
  * does not have are prefixed llamd_hip_ and say so.
  *
- * Weights: Q6_K matrices are uploaded with llamd_rocm_upload_q6k, which
- * re-lays the ggml bytes into this backend's tiled device layout (a pure
- * byte/bit permutation, see llamd_hip_q6k_tile). Every Q6_K entry point below
- * takes such a handle. Rows of one matrix are k = blocks*256 weights; an
- * expert tensor is n_expert matrices uploaded as one (rows*n_expert rows,
- * rows % 16 == 0) or with llamd_rocm_upload_q6k_experts.
+ * Weights: the kernels read Q6_K in this backend's tiled device layout (a
+ * pure byte/bit permutation of ggml's, see llamd_hip_q6k_tile), uploaded with
+ * llamd_rocm_upload_q6k. Every Q6_K entry point also accepts the reference's
+ * own device forms, unchanged: ggml bytes (llamd_rocm_upload, or
+ * llamd_fwd_alloc + llamd_fwd_upload) and the planar repack (the
+ * llamd_fwd_planar_* / llamd_u_* entry points, with its plane offsets). Such
+ * a tensor gets a tiled copy on first use, re-made when the library writes
+ * its bytes (llamd_fwd_upload / llamd_fwd_memset) and freed with it
+ * (llamd_fwd_free / llamd_rocm_release); it must lie in memory from
+ * llamd_fwd_alloc or llamd_rocm_upload. Rows of one matrix are
+ * k = blocks*256 weights; an expert tensor is n_expert matrices uploaded as
+ * one (rows*n_expert rows, rows % 16 == 0) or with
+ * llamd_rocm_upload_q6k_experts.
  *
  * Activations follow the reference's BlockQ8K split into arrays: qs (int8,
  * 256 per block), d (f32 per block), bsums (int16, 16 per block).
@@ -80,7 +87,14 @@ void llamd_fwd_free(void *p);
 int llamd_fwd_upload(void *dst, const void *src, size_t bytes);
 int llamd_fwd_download(void *dst, const void *src, size_t bytes);
 int llamd_fwd_sync(void);
+/* -1 if queued work failed, or if a void device-pointer entry point refused
+ * its arguments since the last call (the reason is in llamd_hip_last_error). */
 int llamd_fwd_last_error(void);
+/* llamd_forward.hip:735-737, as a fill kernel on the library stream (no
+ * memset node when captured). */
+int llamd_fwd_memset(void *p, int value, size_t bytes);
+/* llamd_forward.hip:747-751 */
+size_t llamd_fwd_free_mem(void);
 
 /* ---- weight layouts (host-side, no device needed) ------------------------- */
 /* Not in the reference (its closest relative is the planar repack,
@@ -175,7 +189,8 @@ void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, c
 void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks);
 /* llamd_forward.hip:802-805 (exact SiLU: glibc-identical expf) */
 void llamd_fwd_silu_mul(const float *gate, const float *up, float *out, int n);
-/* llamd_forward.hip:807-811, from given logits. probs may be NULL. */
+/* llamd_forward.hip:807-811, from given logits (n_expert <= 256). probs
+ * (optional) receives route()'s softmax over every expert. */
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs);
 /* llamd_forward.hip:759-763: out = rms_norm(x) * w over one row of n.
@@ -206,6 +221,191 @@ void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int
 /* Not in the reference (its Q8_0 path is CPU-only, model.rs:253-262): Q8_0
  * weight from llamd_hip_upload_q8_0 times an f32 activation. */
 void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, int rows, int k);
+/* llamd.hip:1389-1398; nsub ignored as for the other split-K spellings. */
+void llamd_fwd_matvec_splitk(const void *d_w, const int8_t *d_aq, const float *d_ad, float *d_out,
+                             int blocks, int rows, int nsub);
+/* llamd.hip:1348-1387: timing of llamd_fwd_matvec (host activations), ms. */
+int llamd_rocm_splitk_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,
+                            int rows, int nsub, int iters, float *ms_out);
+
+/* ---- the planar repack (PlanarWeights, crates/llamd-rocm/src/lib.rs:619-843) */
+/* off = {ql, qh, sc, d} plane offsets from PlanarQ6K::layout
+ * (crates/llamd-quant/src/dot.rs:349-398), a host array; base a device
+ * buffer holding the repack. Same results as the ggml-layout calls. */
+/* llamd.hip:1470-1478 */
+void llamd_fwd_planar_matvec(const void *base, const size_t *off, const int8_t *d_aq,
+                             const float *d_ad, float *d_out, int blocks, int rows);
+/* llamd.hip:1480-1491 */
+void llamd_fwd_planar_grouped(const void *base, const size_t *off, const int32_t *d_ids,
+                              const int8_t *d_aq, const float *d_ad, float *d_out, int blocks,
+                              int rows, int n_used);
+/* llamd.hip:1493-1504 */
+void llamd_fwd_planar_grouped_pa(const void *base, const size_t *off, const int32_t *d_ids,
+                                 const int8_t *d_aq, const float *d_ad, float *d_out, int blocks,
+                                 int rows, int n_used);
+/* llamd.hip:1506-1522 */
+void llamd_fwd_planar_x3(const void *b0, const size_t *f0, const void *b1, const size_t *f1,
+                         const void *b2, const size_t *f2, const int8_t *d_aq, const float *d_ad,
+                         float *o0, float *o1, float *o2, int blocks, int rows0, int rows1,
+                         int rows2);
+/* llamd.hip:1524-1538 */
+void llamd_fwd_planar_grouped_x2(const void *ba, const size_t *fa, const void *bb, const size_t *fb,
+                                 const int32_t *d_ids, const int8_t *d_aq, const float *d_ad,
+                                 float *oa, float *ob, int blocks, int rows, int n_used);
+/* llamd.hip:1542-1564: host activations in, host results out. */
+int llamd_rocm_planar_matvec(const void *base, const size_t *off, const int8_t *aq,
+                             const float *ad, float *out, int blocks, int rows);
+/* llamd.hip:1567-1605: ms for iters launches. */
+int llamd_rocm_planar_bench(const void *base, const size_t *off, const int8_t *aq, const float *ad,
+                            int blocks, int rows, int iters, float *ms_out);
+
+/* ---- the rest of the decode step (llamd_forward.hip), bit-exact ----------- */
+/* Each matches the reference CPU path's f32 operations (crates/llamd-cpu,
+ * crates/llamd-runtime/src/layer.rs, attention.rs) bit for bit. RoPE angles
+ * come from a table filled on the host with the reference's libm calls,
+ * covering 32768 positions (more when a max_kv says so); a position beyond
+ * it gives NaN. Attention covers at most 16384 positions; the scores buffer
+ * is not used. meta = {token, pos} on the device. */
+/* llamd_forward.hip:753-757: row `token` of a ggml Q6_K table, dequantized */
+void llamd_fwd_embed(const void *table, int token, float *out, int blocks);
+/* llamd_forward.hip:863-868: the token read from meta[0] */
+void llamd_fwd_embed_meta(const void *table, const int32_t *meta, float *out, int blocks);
+/* llamd_forward.hip:772-776: NeoX RoPE in place at pos */
+void llamd_fwd_rope(float *x, int pos, int n_head, int hd, float freq_base);
+/* llamd_forward.hip:827-833: per-head QK-norm (w may be NULL) + RoPE at meta[1] */
+void llamd_fwd_norm_rope(float *x, const float *w, int n_head, int hd, const int32_t *meta,
+                         float freq_base, float eps);
+/* llamd_forward.hip:835-843: the same for K (in place), then K and V stored
+ * at cache row meta[1]; kv_dim must be n_head_kv * hd */
+void llamd_fwd_k_norm_rope_store(float *k, const float *w, const float *v, float *kc, float *vc,
+                                 int n_head_kv, int hd, int kv_dim, const int32_t *meta,
+                                 float freq_base, float eps);
+/* llamd_forward.hip:778-782 */
+void llamd_fwd_kv_store(float *kc, float *vc, const float *k, const float *v, int pos, int kv_dim);
+/* llamd_forward.hip:784-790: attend over n_kv cached positions */
+void llamd_fwd_attention(const float *q, const float *kc, const float *vc, float *out,
+                         float *scores, int n_head, int n_head_kv, int hd, int n_kv);
+/* llamd_forward.hip:870-877: n_kv = meta[1] + 1 */
+void llamd_fwd_attention_meta(const float *q, const float *kc, const float *vc, float *out,
+                              float *scores, int n_head, int n_head_kv, int hd, const int32_t *meta,
+                              int max_kv);
+/* llamd_forward.hip:798-800 */
+void llamd_fwd_add(const float *a, const float *b, float *out, int n);
+
+/* ---- batched decode (crates/llamd-rocm/kernels/llamd_batch.hip) ----------- */
+/* nseq independent sequences; activations [nseq][...], results [nseq][...],
+ * meta [nseq][2] = {token, pos}; each sequence owns a max_kv * kv_dim slice
+ * of a layer's cache. Weights in ggml layout are read once per 16
+ * sequences. Results equal nseq single-sequence calls, bit for bit. */
+/* llamd_batch.hip:837: sequences per call (16) */
+int llamd_batch_max_seq(void);
+/* llamd_batch.hip:839-844 */
+void llamd_b_embed(const void *table, const int32_t *meta, float *out, int blocks, int nseq);
+/* llamd_batch.hip:846-853 */
+void llamd_b_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
+                            float *inv, int n, int nseq, float eps);
+/* llamd_batch.hip:855-859 */
+void llamd_b_rms_norm_mul(const float *x, const float *w, float *out, int n, int nseq, float eps);
+/* llamd_batch.hip:861-864 */
+void llamd_b_quantize(const float *x, int8_t *qs, float *d, int nblocks);
+/* llamd_batch.hip:875-887 */
+void llamd_b_matvec(const void *w, const int8_t *aq, const float *ad, float *out, int blocks,
+                    int rows, int nseq);
+/* llamd_batch.hip:889-906 */
+void llamd_b_matvec_x3(const void *w0, const void *w1, const void *w2, const int8_t *aq,
+                       const float *ad, float *o0, float *o1, float *o2, int blocks, int r0, int r1,
+                       int r2, int nseq);
+/* llamd_batch.hip:908-916: ids [nseq][n_used]; oa, ob [nseq][n_used][rows] */
+void llamd_b_grouped_x2(const void *wa, const void *wb, const int32_t *ids, const int8_t *aq,
+                        const float *ad, float *oa, float *ob, int blocks, int rows, int n_used,
+                        int nseq);
+/* llamd_batch.hip:918-925: activation (s, k) for slot (s, k) */
+void llamd_b_grouped_pa(const void *w, const int32_t *ids, const int8_t *aq, const float *ad,
+                        float *out, int blocks, int rows, int n_used, int nseq);
+/* llamd_batch.hip:927-933 */
+void llamd_b_norm_rope(float *x, const float *w, int n_head, int hd, const int32_t *meta, int nseq,
+                       float freq_base, float eps);
+/* llamd_batch.hip:935-944 */
+void llamd_b_k_norm_rope_store(float *k, const float *w, const float *v, float *kc, float *vc,
+                               int n_head_kv, int hd, int kv_dim, int max_kv, const int32_t *meta,
+                               int nseq, float freq_base, float eps);
+/* llamd_batch.hip:946-952 */
+void llamd_b_attention(const float *q, const float *kc, const float *vc, float *out, float *scores,
+                       int n_head, int n_head_kv, int hd, int max_kv, const int32_t *meta,
+                       int nseq);
+/* llamd_batch.hip:954-960 */
+void llamd_b_add(const float *a, const float *b, float *o, int n);
+void llamd_b_silu_mul(const float *g, const float *u, float *o, int n);
+/* llamd_batch.hip:962-966 (FMA accumulation, as llamd_fwd_matvec_f32) */
+void llamd_b_matvec_f32(const float *w, const float *x, float *out, int k, int rows, int nseq);
+/* llamd_batch.hip:968-972 (n_expert <= 256) */
+void llamd_b_router(const float *logits, int n_expert, int n_used, int32_t *ids, float *weights,
+                    float *probs, int nseq);
+/* llamd_batch.hip:974-980 */
+void llamd_b_moe_combine_add(const float *down, const float *weights, const float *residual,
+                             float *out, int n_used, int n_embd, int nseq);
+/* llamd_batch.hip:982-988: sv, si hold nchunk partials per sequence */
+void llamd_b_argmax(const float *x, int n, float *sv, int32_t *si, int32_t *out, int nchunk,
+                    int nseq);
+
+/* ---- unsigned-activation form (crates/llamd-rocm/kernels/llamd_udot.hip) -- */
+/* qb = Q8_K quants biased to unsigned (q ^ 0x80), sb = per-16 sums of qb,
+ * d as usual; weights in the planar repack. The matvecs recover the signed
+ * quants exactly, so results are dot_q6k_q8k's bits (the reference's udot
+ * kernels are only within REDUCTION of them); sb is produced, not read. */
+/* llamd_udot.hip:599-600: accepted and reported; the kernels choose their tiling */
+void llamd_u_set_tile(int t);
+int llamd_u_get_tile(void);
+/* llamd_udot.hip:584-587 (kernel uk_bias_sums, :55-75) */
+void llamd_u_bias_sums(const int8_t *qs, uint8_t *qb, int32_t *sb, int nblocks);
+/* llamd_udot.hip:569-576: rms_norm(x) * w -> out, qb, sb, d */
+void llamd_u_norm_quant(const float *x, const float *w, float *out, uint8_t *qb, int32_t *sb,
+                        float *d, float *inv, int n, int nseq, float eps);
+/* llamd_udot.hip:578-582 */
+void llamd_u_quantize(const float *x, uint8_t *qb, int32_t *sb, float *d, int nblocks);
+/* llamd_udot.hip:602-663: out [nseq][rows] */
+void llamd_u_matvec(const void *base, const size_t *off, const uint8_t *qb, const int32_t *sb,
+                    const float *ad, float *out, int blocks, int rows, int nseq);
+void llamd_u_x3(const void *b0, const size_t *f0, const void *b1, const size_t *f1, const void *b2,
+                const size_t *f2, const uint8_t *qb, const int32_t *sb, const float *ad, float *o0,
+                float *o1, float *o2, int blocks, int r0, int r1, int r2, int nseq);
+void llamd_u_grouped_x2(const void *ba, const size_t *fa, const void *bb, const size_t *fb,
+                        const int32_t *ids, const uint8_t *qb, const int32_t *sb, const float *ad,
+                        float *oa, float *ob, int blocks, int rows, int n_used, int nseq);
+void llamd_u_grouped_pa(const void *base, const size_t *off, const int32_t *ids, const uint8_t *qb,
+                        const int32_t *sb, const float *ad, float *out, int blocks, int rows,
+                        int n_used, int nseq);
+/* llamd_udot.hip:714-751, 756-785: host in, host out */
+int llamd_u_norm_quant_host(const float *x, const float *w, int n, int nseq, float eps, float *out,
+                            uint8_t *qb, int32_t *sb, float *d);
+int llamd_u_quantize_host(const float *x, int nblocks, uint8_t *qb, int32_t *sb, float *d);
+/* llamd_udot.hip:789-826: signed quants qs [nseq][blocks*256] from the host */
+int llamd_u_matvec_host(const void *base, const size_t *off, const int8_t *qs, const float *ad,
+                        float *out, int blocks, int rows, int nseq);
+/* llamd_udot.hip:668-711: ms for iters launches */
+int llamd_u_matvec_bench(const void *base, const size_t *off, const int8_t *qs, const float *ad,
+                         int blocks, int rows, int nseq, int iters, float *ms_out);
+
+/* ---- llamd-tensor Backend ops on device tensors --------------------------- */
+/* Not in the reference's C ABI: the f32 half of the Backend trait
+ * (crates/llamd-tensor/src/lib.rs:148-174), row-major [rows][n] device
+ * tensors, bit-identical to CpuBackend (crates/llamd-cpu/src/lib.rs:55-224).
+ * Asynchronous on the library stream except be_rope (host positions). */
+int llamd_hip_be_rms_norm(const float *x, float *out, int rows, int n, float eps);
+int llamd_hip_be_softmax(const float *x, float *out, int rows, int n);
+int llamd_hip_be_silu(const float *x, float *out, size_t n);
+int llamd_hip_be_add(const float *a, const float *b, float *out, size_t n);
+int llamd_hip_be_mul(const float *a, const float *b, float *out, size_t n);
+int llamd_hip_be_scale(const float *x, float by, float *out, size_t n);
+/* out [n][m] = w [m][k] . x [n][k] (ggml order: w [k, m], x [k, n]) */
+int llamd_hip_be_matmul(const float *w, const float *x, float *out, int m, int n, int k);
+/* NeoX RoPE of rows [rows][row_len] (heads of head_dim), row r at
+ * positions[r] * freq_scale; positions is a host array */
+int llamd_hip_be_rope(float *x, int rows, int row_len, const uint32_t *positions, int head_dim,
+                      float freq_base, float freq_scale);
+/* rows ids[j] (host array) of table [table_rows][row_len] -> out [n_ids][row_len] */
+int llamd_hip_be_get_rows(const float *table, int table_rows, int row_len, const uint32_t *ids,
+                          int n_ids, float *out);
 
 /* ---- one MoE decode layer (R8 router -> R9 route -> R11 moe_ffn -> R12) ---- */
 /* Not in the reference as one call: DeviceModel::queue_token's MoE phases

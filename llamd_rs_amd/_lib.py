@@ -129,6 +129,66 @@ SIGNATURES = {
     "llamd_hip_copy_calibration": (i32, [vp, vp, sz]),
     "llamd_rocm_matvec_bench": (i32, [vp, vp, vp, i32, i32, i32, f32p]),
     "llamd_rocm_matvec_grouped_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32p]),
+    "llamd_fwd_memset": (i32, [vp, i32, sz]),
+    "llamd_fwd_free_mem": (sz, []),
+    "llamd_fwd_matvec_splitk": (None, [vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_rocm_splitk_bench": (i32, [vp, vp, vp, i32, i32, i32, i32, f32p]),
+    "llamd_fwd_planar_matvec": (None, [vp, vp, vp, vp, vp, i32, i32]),
+    "llamd_fwd_planar_grouped": (None, [vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_fwd_planar_grouped_pa": (None, [vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_fwd_planar_x3": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_fwd_planar_grouped_x2": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_rocm_planar_matvec": (i32, [vp, vp, vp, vp, vp, i32, i32]),
+    "llamd_rocm_planar_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, f32p]),
+    "llamd_fwd_embed": (None, [vp, i32, vp, i32]),
+    "llamd_fwd_embed_meta": (None, [vp, vp, vp, i32]),
+    "llamd_fwd_rope": (None, [vp, i32, i32, i32, f]),
+    "llamd_fwd_norm_rope": (None, [vp, vp, i32, i32, vp, f, f]),
+    "llamd_fwd_k_norm_rope_store": (None, [vp, vp, vp, vp, vp, i32, i32, i32, vp, f, f]),
+    "llamd_fwd_kv_store": (None, [vp, vp, vp, vp, i32, i32]),
+    "llamd_fwd_attention": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_fwd_attention_meta": (None, [vp, vp, vp, vp, vp, i32, i32, i32, vp, i32]),
+    "llamd_fwd_add": (None, [vp, vp, vp, i32]),
+    "llamd_batch_max_seq": (i32, []),
+    "llamd_b_embed": (None, [vp, vp, vp, i32, i32]),
+    "llamd_b_rms_norm_quant": (None, [vp, vp, vp, vp, vp, vp, i32, i32, f]),
+    "llamd_b_rms_norm_mul": (None, [vp, vp, vp, i32, i32, f]),
+    "llamd_b_quantize": (None, [vp, vp, vp, i32]),
+    "llamd_b_matvec": (None, [vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_b_matvec_x3": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "llamd_b_grouped_x2": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_b_grouped_pa": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_b_norm_rope": (None, [vp, vp, i32, i32, vp, i32, f, f]),
+    "llamd_b_k_norm_rope_store": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, f, f]),
+    "llamd_b_attention": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32]),
+    "llamd_b_add": (None, [vp, vp, vp, i32]),
+    "llamd_b_silu_mul": (None, [vp, vp, vp, i32]),
+    "llamd_b_matvec_f32": (None, [vp, vp, vp, i32, i32, i32]),
+    "llamd_b_router": (None, [vp, i32, i32, vp, vp, vp, i32]),
+    "llamd_b_moe_combine_add": (None, [vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_b_argmax": (None, [vp, i32, vp, vp, vp, i32, i32]),
+    "llamd_u_set_tile": (None, [i32]),
+    "llamd_u_get_tile": (i32, []),
+    "llamd_u_bias_sums": (None, [vp, vp, vp, i32]),
+    "llamd_u_norm_quant": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, f]),
+    "llamd_u_quantize": (None, [vp, vp, vp, vp, i32]),
+    "llamd_u_matvec": (None, [vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_u_x3": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "llamd_u_grouped_x2": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_u_grouped_pa": (None, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "llamd_u_norm_quant_host": (i32, [vp, vp, i32, i32, f, vp, vp, vp, vp]),
+    "llamd_u_quantize_host": (i32, [vp, i32, vp, vp, vp]),
+    "llamd_u_matvec_host": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+    "llamd_u_matvec_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32p]),
+    "llamd_hip_be_rms_norm": (i32, [vp, vp, i32, i32, f]),
+    "llamd_hip_be_softmax": (i32, [vp, vp, i32, i32]),
+    "llamd_hip_be_silu": (i32, [vp, vp, sz]),
+    "llamd_hip_be_add": (i32, [vp, vp, vp, sz]),
+    "llamd_hip_be_mul": (i32, [vp, vp, vp, sz]),
+    "llamd_hip_be_scale": (i32, [vp, f, vp, sz]),
+    "llamd_hip_be_matmul": (i32, [vp, vp, vp, i32, i32, i32]),
+    "llamd_hip_be_rope": (i32, [vp, i32, i32, vp, i32, f, f]),
+    "llamd_hip_be_get_rows": (i32, [vp, i32, i32, vp, i32, vp]),
     # host-side synthetic data (llamd_rs_amd/csrc/host/synth.cpp)
     "llamd_synth_normal": (None, [u64, f, vp, sz]),
     "llamd_synth_f32_to_f16": (u16, [f]),

@@ -47,8 +47,8 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", f"-I{R
               f"-I{CSRC}"]
 
 HIP_SOURCES = ["q6k_mv.hip", "q8k.hip", "moe.hip", "moe_decode.hip", "group.hip", "norm.hip",
-               "decode.hip", "noalloc.hip"]
-HOST_HIP_SOURCES = ["capi.cpp", "model.cpp"]  # host code that calls the HIP runtime
+               "decode.hip", "noalloc.hip", "compat.hip"]
+HOST_HIP_SOURCES = ["capi.cpp", "model.cpp", "compat_abi.cpp"]  # host code that calls the HIP runtime
 HOST_SOURCES = ["host/layout.cpp", "host/synth.cpp", "host/gguf.cpp"]
 
 

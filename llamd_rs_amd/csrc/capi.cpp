@@ -28,6 +28,9 @@ constexpr int QK = 256;
 constexpr int SEGB = 16 * 210;
 
 thread_local char g_err[512] = "";
+// Set by a device-pointer launcher (void in the reference's ABI) that refused
+// its arguments; llamd_fwd_last_error reports it once, then clears it.
+bool g_fwd_refused = false;
 std::mutex g_mu;             // serialises host-in/host-out calls and the registry
 hipStream_t g_stream = nullptr;
 // MoE decode schedule: 2 router fold beside gate/up, then down (moe_decode.hip);
@@ -54,6 +57,8 @@ int fail(const char *fmt, ...) {
 }
 
 }  // namespace
+
+void llamd::fwd_refused() { g_fwd_refused = true; }
 
 // The error text of the calling thread, for the other host files of the
 // library (errors.hpp).
@@ -151,6 +156,58 @@ int batched_dev(const void *w, const int8_t *cq, const float *cd, float *y, int 
 
 }  // namespace
 
+// Resolve a Q6_K weight pointer to the tiled layout the kernels read
+// (launch.hpp Q6kView). Tiled uploads (llamd_rocm_upload_q6k[_experts]) are
+// used as they are. Anything else is the reference's own device layout --
+// ggml blocks (planar_off null) or the planar repack -- in memory from
+// llamd_fwd_alloc / llamd_rocm_upload, and resolves to its tiled copy
+// (compat_abi.cpp). grouped: `rows` per expert of an expert tensor, either one
+// upload of rows*n rows (rows % 16 == 0) or llamd_rocm_upload_q6k_experts;
+// otherwise a matrix of at least `rows` rows.
+int llamd::resolve_q6k(const void *d_w, const size_t *planar_off, int rows, int blocks,
+                       bool grouped, Q6kView *v) {
+    if (!d_w) return fail("Q6_K weight: null pointer");
+    if (rows <= 0 || blocks <= 0) return fail("Q6_K weight: rows %d, blocks %d", rows, blocks);
+    WInfo wi;
+    int total = 0;
+    if (!planar_off && lookup(d_w, KIND_Q6K, &wi)) {
+        if (blocks != wi.blocks) return fail("blocks %d != uploaded %d", blocks, wi.blocks);
+        v->tiled = d_w;
+        if (wi.n_expert > 1) {
+            if (grouped ? rows != wi.rows : rows > wi.rows)
+                return fail("rows %d do not match the uploaded expert rows %d", rows, wi.rows);
+            v->expert_stride = wi.stride;
+            v->n_expert = wi.n_expert;
+            return 0;
+        }
+        total = wi.rows;
+    } else {
+        if (shadow_q6k(d_w, planar_off, rows, blocks, &v->tiled, &total)) return -1;
+    }
+    if (!grouped) {
+        if (rows > total) return fail("rows %d exceed the weight's %d", rows, total);
+        v->expert_stride = 0;
+        v->n_expert = 1;
+        return 0;
+    }
+    if (total % rows) return fail("rows %d does not divide the weight's %d", rows, total);
+    if (total != rows && rows % 16) return fail("rows %d not a multiple of 16", rows);
+    v->expert_stride = (size_t)(rows / 16) * blocks * SEGB;
+    v->n_expert = total / rows;
+    return 0;
+}
+
+static int expert_view(const void *d_w, int rows, int blocks, size_t *stride, int *n_expert,
+                       const void **tiled) {
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, true, &v)) return -1;
+    *stride = v.expert_stride;
+    *n_expert = v.n_expert;
+    *tiled = v.tiled;
+    return 0;
+}
+
+
 extern "C" {
 
 const char *llamd_hip_last_error(void) { return g_err; }
@@ -234,6 +291,7 @@ void *llamd_rocm_upload(const void *host, size_t bytes) {
         (void)hipFree(d);
         return nullptr;
     }
+    note_alloc(d, bytes);
     return d;
 }
 
@@ -243,6 +301,7 @@ void llamd_rocm_release(void *dev) {
         std::lock_guard<std::mutex> lk(g_mu);
         g_weights.erase(dev);
     }
+    note_free(dev);
     (void)hipFree(dev);
 }
 
@@ -262,7 +321,9 @@ static void drop_graph() {
 int llamd_fwd_begin_capture(void) {
     if (!stream()) return fail("stream create failed");
     drop_graph();
-    return hip_ok(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal), "begin capture")
+    // relaxed: a raw or planar Q6_K weight first used inside the capture gets
+    // its tiled copy allocated and filled on a side stream (compat.hip)
+    return hip_ok(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed), "begin capture")
                ? 0 : -1;
 }
 
@@ -291,19 +352,32 @@ int llamd_fwd_stream_init(void) { return stream() ? 0 : fail("stream create fail
 void *llamd_fwd_alloc(size_t bytes) {
     void *p = nullptr;
     if (!hip_ok(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc")) return nullptr;
+    note_alloc(p, bytes ? bytes : 16);
     return p;
 }
 void llamd_fwd_free(void *p) {
-    if (p) (void)hipFree(p);
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_weights.erase(p);
+    }
+    note_free(p);
+    (void)hipFree(p);
 }
 int llamd_fwd_upload(void *dst, const void *src, size_t bytes) {
-    return up(dst, src, bytes) && sync() ? 0 : -1;
+    if (!(up(dst, src, bytes) && sync())) return -1;
+    // a tiled copy made of these bytes is re-made from them
+    return note_write(dst, bytes, stream()) || !sync() ? -1 : 0;
 }
 int llamd_fwd_download(void *dst, const void *src, size_t bytes) {
     return down(dst, src, bytes) && sync() ? 0 : -1;
 }
 int llamd_fwd_sync(void) { return sync() ? 0 : -1; }
 int llamd_fwd_last_error(void) {
+    if (g_fwd_refused) {
+        g_fwd_refused = false;
+        return -1;  // g_err holds the refusal
+    }
     return hip_ok(hipGetLastError(), "queued work") ? 0 : -1;
 }
 
@@ -354,35 +428,13 @@ void *llamd_hip_upload_q8_0(const void *ggml, int rows, int k) {
     return d;
 }
 
-// Resolve (weight, rows-per-expert) to an expert stride and expert count,
-// accepting both upload forms: one tiled matrix of rows*n rows (rows % 16 == 0)
-// or llamd_rocm_upload_q6k_experts.
-static int expert_view(const void *d_w, int rows, int blocks, size_t *stride, int *n_expert) {
-    WInfo wi;
-    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
-    if (blocks != wi.blocks) return fail("blocks %d != uploaded %d", blocks, wi.blocks);
-    if (rows <= 0) return fail("rows must be positive");
-    if (wi.n_expert > 1) {
-        if (rows != wi.rows) return fail("rows %d != uploaded expert rows %d", rows, wi.rows);
-        *stride = wi.stride;
-        *n_expert = wi.n_expert;
-        return 0;
-    }
-    if (wi.rows % rows) return fail("rows %d does not divide the upload's %d", rows, wi.rows);
-    if (wi.rows != rows && rows % 16) return fail("rows %d not a multiple of 16", rows);
-    *stride = (size_t)(rows / 16) * blocks * SEGB;
-    *n_expert = wi.rows / rows;
-    return 0;
-}
-
 // ---- host-in/host-out ----------------------------------------------------------
 int llamd_rocm_matvec_q6k_resident(const void *d_w, const int8_t *aq, const float *ad, float *out,
                                    int blocks, int rows) {
-    WInfo wi;
-    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
-    if (blocks != wi.blocks || rows <= 0 || rows > wi.rows * wi.n_expert || !aq || !ad || !out)
-        return fail("matvec: shape mismatch");
-    if (wi.n_expert > 1 && rows > wi.rows) return fail("matvec: rows span experts");
+    if (!aq || !ad || !out) return fail("matvec: null pointer");
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return -1;
+    d_w = v.tiled;
     std::lock_guard<std::mutex> lk(g_mu);
     DevBuf q((size_t)blocks * QK), d((size_t)blocks * 4), y((size_t)rows * 4);
     if (!q.p || !d.p || !y.p) return fail("hipMalloc");
@@ -400,7 +452,7 @@ static int grouped_host(const void *d_w, const int32_t *eid, const int8_t *aq, c
     if (!eid || !aq || !ad || !out) return fail("grouped: null pointer");
     size_t stride = 0;
     int n_expert = 0;
-    if (expert_view(d_w, rows, blocks, &stride, &n_expert)) return -1;
+    if (expert_view(d_w, rows, blocks, &stride, &n_expert, &d_w)) return -1;
     for (int i = 0; i < n_used; ++i)
         if (eid[i] < 0 || eid[i] >= n_expert)
             return fail("grouped: expert id %d out of range [0,%d)", eid[i], n_expert);
@@ -433,12 +485,10 @@ int llamd_hip_matvec_grouped_pa(const void *d_w, const int32_t *eid, const int8_
 // re-ordered class-major on the host for the kernel's operand loads.
 int llamd_hip_matvec_q6k_batched(const void *d_w, const int8_t *aq, const float *ad, float *out,
                                  int blocks, int rows, int nseq) {
-    WInfo wi;
-    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
-    if (blocks != wi.blocks || rows <= 0 || rows > wi.rows * wi.n_expert || nseq <= 0 || !aq ||
-        !ad || !out)
-        return fail("batched: shape mismatch");
-    if (wi.n_expert > 1 && rows > wi.rows) return fail("batched: rows span experts");
+    if (nseq <= 0 || !aq || !ad || !out) return fail("batched: bad arguments");
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return -1;
+    d_w = v.tiled;
     // the reference's BlockQ8K arrays -> the token-chunked operand layout
     const size_t nq = chunk_q_bytes(nseq, blocks), nd = chunk_d_bytes(nseq, blocks);
     std::vector<int8_t> cq(nq, 0);
@@ -494,10 +544,14 @@ int llamd_hip_swiglu_q8k(const float *gate, const float *upv, int nblocks, float
 }
 
 int llamd_hip_dequant_q6k(const void *d_w, int rows, int blocks, float *out) {
+    if (!out) return fail("dequant: null output");
     WInfo wi;
-    if (!lookup(d_w, KIND_Q6K, &wi)) return fail("not a Q6_K weight handle");
-    if (wi.n_expert != 1 || rows != wi.rows || blocks != wi.blocks || !out)
+    if (lookup(d_w, KIND_Q6K, &wi) && (wi.n_expert != 1 || rows != wi.rows || blocks != wi.blocks))
         return fail("dequant: shape mismatch");
+    // a raw ggml tensor dequantizes through its tiled copy (its first rows rows)
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return -1;
+    d_w = v.tiled;
     std::lock_guard<std::mutex> lk(g_mu);
     const size_t n = (size_t)rows * blocks * QK;
     DevBuf y(n * 4);
@@ -567,14 +621,17 @@ int llamd_hip_argmax(const float *x, int n, int nseq, int32_t *ids) {
 // ---- device-pointer launchers ------------------------------------------------
 void llamd_fwd_matvec(const void *d_w, const int8_t *d_aq, const float *d_ad, float *d_out,
                       int blocks, int rows) {
-    launch_q6k_mv_b1(d_w, 0, nullptr, d_aq, d_ad, d_out, rows, blocks, 1, 0, stream());
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return fwd_refused();
+    if (launch_q6k_mv_b1(v.tiled, 0, nullptr, d_aq, d_ad, d_out, rows, blocks, 1, 0, stream()))
+        return (void)fail("matvec: launch"), fwd_refused();
 }
 
 void llamd_fwd_matvec_grouped(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
                               const float *d_ad, float *d_out, int blocks, int rows, int n_used) {
     size_t stride = 0;
     int ne = 0;
-    if (expert_view(d_w, rows, blocks, &stride, &ne)) return;
+    if (n_used <= 0 || expert_view(d_w, rows, blocks, &stride, &ne, &d_w)) return fwd_refused();
     launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 0, stream());
 }
 
@@ -583,7 +640,7 @@ void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const in
                                  int n_used) {
     size_t stride = 0;
     int ne = 0;
-    if (expert_view(d_w, rows, blocks, &stride, &ne)) return;
+    if (n_used <= 0 || expert_view(d_w, rows, blocks, &stride, &ne, &d_w)) return fwd_refused();
     launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 1, stream());
 }
 
@@ -597,8 +654,11 @@ void llamd_fwd_silu_mul(const float *gate, const float *upv, float *out, int n) 
 
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
                       float *weights, float *probs) {
-    (void)probs;
-    launch_route_logits(logits, n_expert, n_used, ids, weights, stream());
+    if (n_expert <= 0 || n_expert > 256 || n_used <= 0 || n_used > n_expert) {  // route_logits: 4 logits per lane
+        fail("router: n_expert %d, n_used %d", n_expert, n_used);
+        return fwd_refused();
+    }
+    launch_route_logits(logits, n_expert, n_used, ids, weights, stream(), 1, probs);
 }
 
 void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
@@ -608,12 +668,9 @@ void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const i
     float *y[3] = {o0, o1, o2};
     const int rows[3] = {rows0, rows1, rows2};
     for (int i = 0; i < 3; ++i) {
-        WInfo wi;
-        if (!lookup(w[i], KIND_Q6K, &wi) || wi.blocks != blocks || rows[i] <= 0 ||
-            rows[i] > wi.rows * wi.n_expert) {
-            fail("matvec_x3: weight %d is not a Q6_K handle of that shape", i);
-            return;
-        }
+        Q6kView v;
+        if (resolve_q6k(w[i], nullptr, rows[i], blocks, false, &v)) return fwd_refused();
+        w[i] = v.tiled;
     }
     launch_q6k_mv_x3(w, y, rows, 3, d_aq, d_ad, blocks, stream());
 }
@@ -630,10 +687,12 @@ void llamd_fwd_matvec_grouped_x2(const void *wa, const void *wb, const int32_t *
                                  int blocks, int rows, int n_used) {
     size_t sa = 0, sb = 0;
     int na = 0, nb = 0;
-    if (expert_view(wa, rows, blocks, &sa, &na) || expert_view(wb, rows, blocks, &sb, &nb)) return;
+    if (n_used <= 0 || expert_view(wa, rows, blocks, &sa, &na, &wa) ||
+        expert_view(wb, rows, blocks, &sb, &nb, &wb))
+        return fwd_refused();
     if (sa != sb) {
         fail("matvec_grouped_x2: the two expert tensors differ in shape");
-        return;
+        return fwd_refused();
     }
     launch_q6k_mv_grouped_x2(wa, wb, sa, d_ids, d_aq, d_ad, oa, ob, rows, blocks, n_used, stream());
 }
@@ -1207,13 +1266,13 @@ static int bench_common(const void *d_w, const int32_t *eid, const int8_t *aq, c
     size_t stride = 0;
     int ne = 1;
     if (eid) {
-        if (expert_view(d_w, rows, blocks, &stride, &ne)) return -1;
+        if (expert_view(d_w, rows, blocks, &stride, &ne, &d_w)) return -1;
         for (int i = 0; i < n_used; ++i)
             if (eid[i] < 0 || eid[i] >= ne) return fail("bench: bad expert id");
     } else {
-        WInfo wi;
-        if (!lookup(d_w, KIND_Q6K, &wi) || wi.blocks != blocks || rows > wi.rows * wi.n_expert)
-            return fail("bench: weight handle mismatch");
+        Q6kView v;
+        if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return -1;
+        d_w = v.tiled;
     }
     std::lock_guard<std::mutex> lk(g_mu);
     DevBuf q((size_t)blocks * QK), d((size_t)blocks * 4), y((size_t)rows * n_used * 4),

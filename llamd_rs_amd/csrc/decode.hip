@@ -20,10 +20,15 @@ namespace {
 // products exact in f32. get_rows of the dequantized table
 // (crates/llamd-cpu/src/lib.rs:211-224). One wave per 256-value block; lane
 // (half h, l) writes elements l, l+32, l+64, l+96 of half h.
+// Sequence s = blockIdx.y reads its token at tok[s * tok_stride] (tok null:
+// tok_fixed) and writes row s of out.
 __global__ __launch_bounds__(64) void embed_q6k(const uint8_t *table, const int32_t *tok,
-                                                int blocks, float *out) {
-    const int b = blockIdx.x, lane = threadIdx.x;
-    const uint8_t *blk = table + ((size_t)tok[0] * blocks + b) * 210;
+                                                int tok_stride, int tok_fixed, int blocks,
+                                                float *out) {
+    const int b = blockIdx.x, lane = threadIdx.x, sq = blockIdx.y;
+    const int token = tok ? tok[(size_t)sq * tok_stride] : tok_fixed;
+    out += (size_t)sq * blocks * 256;
+    const uint8_t *blk = table + ((size_t)token * blocks + b) * 210;
     const int half = lane >> 5, l = lane & 31;
     const uint8_t *ql = blk + half * 64, *qh = blk + 128 + half * 32;
     const int8_t *sc = (const int8_t *)(blk + 192 + half * 8);
@@ -49,16 +54,29 @@ constexpr int ATT_MAX_KV = 16384;  // positions whose logits fit in LDS
 //   max; e_t = expf(logit_t - max)                                all lanes
 //   sum_t e_t in order from 0; inv = 1 / sum                      one lane
 //   out[d] = sum_t (e_t * inv) v_t[d] in order from 0             one lane per d
+// Sequence s = blockIdx.y: n_kv = pos_p[s * pos_stride] + 1 (pos_p null:
+// n_kv_fixed), q / out row s, its cache slice at s * cache_seq_stride. An
+// n_kv outside 1..ATT_MAX_KV writes NaN.
 __global__ __launch_bounds__(256) void attend_decode(const float *q, const float *kc,
                                                      const float *vc, const int32_t *pos_p,
                                                      int n_head, int n_head_kv, int hd, float scale,
-                                                     float *out) {
+                                                     float *out, int n_kv_fixed, int pos_stride,
+                                                     size_t cache_seq_stride) {
     __shared__ float lg[ATT_MAX_KV];
     __shared__ float qs[256];
     __shared__ float red[4];
     __shared__ uint64_t tab[32];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n_kv = pos_p[0] + 1;
+    const int sq = blockIdx.y;
+    const int n_kv = pos_p ? pos_p[(size_t)sq * pos_stride] + 1 : n_kv_fixed;
+    q += (size_t)sq * n_head * hd;
+    out += (size_t)sq * n_head * hd;
+    kc += (size_t)sq * cache_seq_stride;
+    vc += (size_t)sq * cache_seq_stride;
+    if (n_kv < 1 || n_kv > ATT_MAX_KV) {
+        for (int d = tid; d < hd; d += blockDim.x) out[h * hd + d] = __builtin_nanf("");
+        return;
+    }
     const int kv_dim = n_head_kv * hd, kvh = h / (n_head / n_head_kv);
     if (wave == 0) expf_ref_tab_fill(tab);
     for (int d = tid; d < hd; d += blockDim.x) qs[d] = q[h * hd + d];
@@ -394,10 +412,11 @@ __global__ __launch_bounds__(512) void attend_fused(
 
 }  // namespace
 
-int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st) {
-    if (blocks <= 0) return -1;
-    hipLaunchKernelGGL(embed_q6k, dim3(blocks), dim3(64), 0, st, (const uint8_t *)table, tok, blocks,
-                       out);
+int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st,
+                     int nseq, int tok_stride, int tok_fixed) {
+    if (blocks <= 0 || nseq <= 0) return -1;
+    hipLaunchKernelGGL(embed_q6k, dim3(blocks, nseq), dim3(64), 0, st, (const uint8_t *)table, tok,
+                       tok_stride, tok_fixed, blocks, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -444,10 +463,12 @@ int launch_attend_fused(const float *q, const float *k, const float *v, const fl
 
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
                          int n_head, int n_head_kv, int hd, float scale, float *out,
-                         hipStream_t st) {
-    if (hd <= 0 || hd % 4 || hd > 256 || n_head_kv <= 0 || n_head % n_head_kv) return -1;
-    hipLaunchKernelGGL(attend_decode, dim3(n_head), dim3(256), 0, st, q, kc, vc, pos, n_head,
-                       n_head_kv, hd, scale, out);
+                         hipStream_t st, int nseq, int n_kv_fixed, int pos_stride,
+                         size_t cache_seq_stride) {
+    if (hd <= 0 || hd % 4 || hd > 256 || n_head_kv <= 0 || n_head % n_head_kv || nseq <= 0)
+        return -1;
+    hipLaunchKernelGGL(attend_decode, dim3(n_head, nseq), dim3(256), 0, st, q, kc, vc, pos, n_head,
+                       n_head_kv, hd, scale, out, n_kv_fixed, pos_stride, cache_seq_stride);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

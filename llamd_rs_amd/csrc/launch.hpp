@@ -19,7 +19,8 @@ extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode la
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
-// w_b (gate and up in one launch).
+// w_b (gate and up in one launch). act_per_slot 0: every slot reads
+// activation 0; d > 0: slot i reads activation i / d.
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
                      hipStream_t st, const void *w_b = nullptr, float *amax_v = nullptr,
@@ -34,7 +35,8 @@ int launch_q6k_mv_x3(const void *const w[3], float *const y[3], const int rows[3
 // oa = Wa[ids] x, ob = Wb[ids] x, each [n_used][rows].
 int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_stride,
                              const int32_t *ids, const int8_t *aq, const float *ad, float *oa,
-                             float *ob, int rows, int blocks, int n_used, hipStream_t st);
+                             float *ob, int rows, int blocks, int n_used, hipStream_t st,
+                             int act_per_slot = 0);
 // Gate and up of the routed experts in one launch, routing (softmax, top-k,
 // renormalise) in the prologue on exact logits; y = [gate | up][n_used][rows].
 int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
@@ -130,12 +132,15 @@ int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipSt
 int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
                         float eps, hipStream_t st);
 // rms_norm(x) * w, then Q8_K (qs, d natural layout); out and inv_out optional.
+// rows > 1: rows of n each ([rows][n] x / out / qs, [rows][n/256] d, [rows] inv_out).
 int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
-                          float *inv_out, int n, float eps, hipStream_t st);
+                          float *inv_out, int n, float eps, hipStream_t st, int rows = 1);
 
 // decode.hip: the whole-token step around the matvecs (token / position read
 // from device memory)
-int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st);
+// nseq rows: sequence s embeds token tok[s * tok_stride] (tok null: tok_fixed)
+int launch_embed_q6k(const void *table, const int32_t *tok, int blocks, float *out, hipStream_t st,
+                     int nseq = 1, int tok_stride = 0, int tok_fixed = 0);
 int attend_max_kv();
 bool attend_fused_fits(int n_head, int n_head_kv, int hd, int max_kv);
 // raises attend_fused's dynamic LDS limit for max_kv positions (outside graph capture)
@@ -144,9 +149,12 @@ int launch_attend_fused(const float *q, const float *k, const float *v, const fl
                         const float *kw, const float2 *cs, const int32_t *pos, int n_head,
                         int n_head_kv, int hd, float eps, float scale, int max_kv, float *kc,
                         float *vc, int8_t *oq, float *od, float *out, hipStream_t st);
+// nseq sequences: n_kv = pos[s * pos_stride] + 1 (pos null: n_kv_fixed); q, out
+// [nseq][n_head * hd]; sequence s's cache starts cache_seq_stride floats after s-1's.
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,
                          int n_head, int n_head_kv, int hd, float scale, float *out,
-                         hipStream_t st);
+                         hipStream_t st, int nseq = 1, int n_kv_fixed = 0, int pos_stride = 0,
+                         size_t cache_seq_stride = 0);
 
 // norm.hip, decode step: per-head QK-norm (w null: none) + RoPE, Q in place,
 // K and V into the cache row of *pos; and ffn_inp = x + o, out = rms_norm(ffn_inp) * w.
@@ -171,9 +179,10 @@ struct RouterLaunch {
     int nseq = 1;  // x [nseq][k] -> logits [nseq][n_expert]; xblocks only with nseq = 1
 };
 int launch_router(const RouterLaunch &l, hipStream_t st);
-// nseq sequences: logits [nseq][n_expert] -> ids, weights [nseq][n_used]
+// nseq sequences: logits [nseq][n_expert] -> ids, weights [nseq][n_used];
+// probs (optional): the softmax over every expert, [nseq][n_expert]
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
-                        float *weights, hipStream_t st, int nseq = 1);
+                        float *weights, hipStream_t st, int nseq = 1, float *probs = nullptr);
 // out[t] = res[t] + sum_e weights[t][e] * down[t][e] in e order; with skip,
 // pairs whose skip entry is negative add nothing.
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
@@ -184,15 +193,90 @@ int argmax_parts(int n);
 // reference's arg-max of row x[seq * ld ..] (index 0 wins if x[0] is NaN).
 int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
                         int nparts, int32_t *out, hipStream_t st);
+// pv, pi hold [nseq][parts] candidates, parts = argmax_parts(n) capped at
+// max_parts (> 0)
 int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, int32_t *out,
-                  hipStream_t st);
+                  hipStream_t st, int max_parts = 0);
 int launch_q8_0_mv(const void *planar, const float *x, float *y, int rows, int k, hipStream_t st);
 int launch_q8_0_dequant(const void *planar, int rows, int k, float *out, hipStream_t st);
 int launch_f32_mv(const float *w, const float *x, float *y, int rows, int k, hipStream_t st);
 
+// compat.hip: the reference's own weight layouts and operand forms.
+// A Q6_K tensor in device memory as the reference lays it out: byte j of
+// field f (ql 128 B, qh 64 B, sc 16 B, d 2 B) of block i = row * blocks + b
+// at base + off[f] + i * stride[f] + j. ggml blocks: off = {0, 128, 192, 208},
+// stride 210; the planar repack: off = the plane offsets, stride = field size.
+struct Q6kSource {
+    const uint8_t *base;
+    size_t off[4];
+    size_t stride[4];
+};
+// Gather rows x blocks of a Q6kSource into the tiled layout
+// (llamd_hip_q6k_tiled_bytes(rows, blocks) bytes at tiled).
+int launch_q6k_retile(const Q6kSource &s, int rows, int blocks, void *tiled, hipStream_t st);
+// memset as a kernel (capturable, no memset graph node)
+int launch_fill(void *p, int value, size_t bytes, hipStream_t st);
+// Q8_K quants [n_act][blocks*256], signed or biased (q ^ 0x80) -> signed copy
+int launch_act_unbias(const void *q, bool biased, int n_act, int blocks, int8_t *out,
+                      hipStream_t st);
+// natural [n_act] quants + scales -> token-chunked operand layout (zero past n_act)
+int launch_act_to_chunks(const void *q, const float *d, bool biased, int n_act, int blocks,
+                         int8_t *cq, float *cd, hipStream_t st);
+// signed quants -> biased quants (may be the same memory) + per-16 sums of them
+int launch_bias_sums(const int8_t *qs, uint8_t *qb, int32_t *sb, int nblocks, hipStream_t st);
+// Per-head QK-norm (w optional) + NeoX RoPE in place, with a position per
+// sequence; optionally stores the rotated head (and v) into a KV cache.
+struct HeadRopeArgs {
+    float *x;                 // [nseq][n_heads][hd]
+    const float *w;           // [hd] or null
+    float eps;
+    const float2 *cs;         // [cs_rows][hd / 2] (cos, sin)
+    int cs_rows;
+    const int32_t *pos_p;     // pos of sequence s at pos_p[s * pos_stride]
+    int pos_stride;
+    int pos_fixed;            // without pos_p: this position (< 0: pos = s)
+    int n_heads, hd;
+    float *kc, *vc;           // null: no store
+    const float *v;           // [nseq][n_heads][hd] with kc
+    int kv_dim;               // n_heads * hd
+    size_t cache_seq_stride;  // floats between sequences' cache slices
+};
+int launch_head_norm_rope(const HeadRopeArgs &a, int nseq, hipStream_t st);
+int launch_kv_store(float *kc, float *vc, const float *k, const float *v, int pos, int kv_dim,
+                    hipStream_t st);
+enum { EW_ADD = 0, EW_MUL = 1, EW_SCALE = 2, EW_SILU = 3 };
+int launch_ew(int op, const float *a, const float *b, float by, float *o, size_t n,
+              hipStream_t st);
+int launch_softmax_rows(const float *x, float *o, int rows, int n, hipStream_t st);
+// out [n][m] = w [m][k] . x [n][k], each sum in order (CpuBackend::matmul)
+int launch_matmul_f32_seq(const float *w, const float *x, float *out, int m, int n, int k,
+                          hipStream_t st);
+
 // ---- shared by the C ABI's host files ----
 // The library's stream (capi.cpp).
 hipStream_t lib_stream();
+// A void device-pointer entry point refused its arguments (the text is in
+// llamd_hip_last_error); llamd_fwd_last_error reports it once (capi.cpp).
+void fwd_refused();
+// A Q6_K weight as the kernels read it: the tiled layout, experts
+// expert_stride bytes apart (capi.cpp resolve_q6k).
+struct Q6kView {
+    const void *tiled;
+    size_t expert_stride;
+    int n_expert;
+};
+int resolve_q6k(const void *w, const size_t *planar_off, int rows, int blocks, bool grouped,
+                Q6kView *v);
+// compat_abi.cpp: device memory the library handed out, and the tiled copies of
+// Q6_K tensors that live in it in the reference's layouts (ggml blocks when
+// planar_off is null, else the planar repack with plane offsets planar_off).
+// shadow_q6k gives the copy (made on first use) and the row count it holds.
+void note_alloc(void *p, size_t bytes);
+void note_free(void *p);
+// after a write of [p, p + bytes) queued on st: re-make the copies of what it touched
+int note_write(const void *p, size_t bytes, hipStream_t st);
+int shadow_q6k(const void *w, const size_t *planar_off, int rows, int blocks, const void **tiled,
+               int *rows_total);
 // Shape of a tiled Q6_K handle from llamd_rocm_upload_q6k[_experts]; -1 if p
 // is not one.
 int q6k_handle_shape(const void *p, int *rows, int *blocks, int *n_expert);

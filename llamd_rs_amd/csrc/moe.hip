@@ -82,21 +82,22 @@ __global__ __launch_bounds__(64 * RPW) void router_logits(RouterArgs a) {
 }
 // Routing from given logits (llamd_hip_route / llamd_fwd_router).
 // One workgroup per sequence (blockIdx.x): logits [nseq][n_expert] -> ids,
-// weights [nseq][n_used].
+// weights [nseq][n_used], and (probs not null) the softmax [nseq][n_expert].
 __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_expert, int n_used,
-                                                   int32_t *ids, float *weights) {
+                                                   int32_t *ids, float *weights, float *probs) {
     __shared__ RouteLds sh;
     const int lane = threadIdx.x;
     logits += (size_t)blockIdx.x * n_expert;
     ids += (size_t)blockIdx.x * n_used;
     weights += (size_t)blockIdx.x * n_used;
+    if (probs) probs += (size_t)blockIdx.x * n_expert;
     float l[RW];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         const int i = lane + WAVE * j;
         l[j] = i < n_expert ? logits[i] : 0.0f;
     }
-    route_finish(l, n_expert, n_used, true, sh, ids, weights, nullptr);
+    route_finish(l, n_expert, n_used, true, sh, ids, weights, nullptr, nullptr, false, probs);
 }
 
 // ---- 3. weighted combine + residual (layer.rs:245-258, 281-287) -------------
@@ -273,10 +274,10 @@ int launch_router(const RouterLaunch &l, hipStream_t st) {
 }
 
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,
-                        float *weights, hipStream_t st, int nseq) {
+                        float *weights, hipStream_t st, int nseq, float *probs) {
     if (nseq <= 0) return -1;
     hipLaunchKernelGGL(route_logits, dim3(nseq), dim3(64), 0, st, logits, n_expert, n_used, ids,
-                       weights);
+                       weights, probs);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -295,8 +296,9 @@ int argmax_parts(int n) {
 }
 
 int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, int32_t *out,
-                  hipStream_t st) {
-    const int parts = argmax_parts(n);
+                  hipStream_t st, int max_parts) {
+    int parts = argmax_parts(n);
+    if (max_parts > 0 && parts > max_parts) parts = max_parts;
     hipLaunchKernelGGL(argmax_partial, dim3(parts, nseq), dim3(256), 0, st, x, n, ld, pv, pi);
     hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(64), 0, st, x, ld, pv, pi, parts, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -99,13 +99,20 @@ __global__ __launch_bounds__(1024) void rms_norm_mul(const float *x, const float
     }
 }
 
-// One row of n = 256 * blocks: wave 0 finds the scale, then wave k forms
-// block k (and k + waves, ...) of (x * scale) * w and quantizes it.
+// One row of n = 256 * blocks per workgroup (row blockIdx.x of x, out, qs,
+// d, inv_out): the workgroup finds the scale, then wave k forms block k (and
+// k + waves, ...) of (x * scale) * w and quantizes it.
 __global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const float *w, float *out,
                                                        int8_t *qs, float *d, float *inv_out,
                                                        int n, float eps) {
     __shared__ ExactSumLds xs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t r = blockIdx.x;
+    x += r * n;
+    if (out) out += r * n;
+    qs += r * n;
+    d += r * (n / QK_K);
+    if (inv_out) inv_out += r;
     float v0[XSUM_M];
     load_run(x, n, v0);
     const float scale = row_scale_block(x, v0, n, eps, xs);
@@ -218,10 +225,10 @@ int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, in
 }
 
 int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
-                          float *inv_out, int n, float eps, hipStream_t st) {
-    if (n <= 0 || n % QK_K || n > NORM_MAX || !w) return -1;
+                          float *inv_out, int n, float eps, hipStream_t st, int rows) {
+    if (n <= 0 || n % QK_K || n > NORM_MAX || !w || rows <= 0) return -1;
     const int waves = n / QK_K < 16 ? n / QK_K : 16;
-    hipLaunchKernelGGL(rms_norm_quant, dim3(1), dim3(64 * waves), 0, st, x, w, out, qs, d, inv_out,
+    hipLaunchKernelGGL(rms_norm_quant, dim3(rows), dim3(64 * waves), 0, st, x, w, out, qs, d, inv_out,
                        n, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

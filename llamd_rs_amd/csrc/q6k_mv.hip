@@ -57,7 +57,7 @@ struct MvParams {
     const int32_t *ids;       // slot -> expert (nullptr: slot -> expert 0)
     size_t expert_stride;     // bytes between experts' tiled matrices
     int items, blocks;        // items over all segments; 256-blocks per row
-    int n_slots, act_per_slot;  // act_per_slot 1: slot i uses activation i
+    int n_slots, act_per_slot;  // > 0: slot i uses activation i / act_per_slot; 0: activation 0
     MvSeg seg1, seg2;
     int n_seg;
     // routing prologue (ROUTE): wave 0 of every workgroup routes on the exact
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
     } else {
         expert = (live && p.ids) ? p.ids[slot] : 0;
     }
-    const int act = p.act_per_slot ? slot : 0;
+    const int act = p.act_per_slot ? slot / p.act_per_slot : 0;
     const int8_t *aq = p.aq + (size_t)act * p.blocks * QK_K;
     const float *ad = p.ad + (size_t)act * p.blocks;
     const uint8_t *seg0 = sgm.w + (size_t)expert * p.expert_stride +
@@ -808,7 +808,8 @@ int launch_q6k_mv_x3(const void *const w[3], float *const y[3], const int rows[3
 
 int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_stride,
                              const int32_t *ids, const int8_t *aq, const float *ad, float *oa,
-                             float *ob, int rows, int blocks, int n_used, hipStream_t st) {
+                             float *ob, int rows, int blocks, int n_used, hipStream_t st,
+                             int act_per_slot) {
     MvParams p = {};
     const void *ws[2] = {wa, wb};
     float *ys[2] = {oa, ob};
@@ -819,6 +820,7 @@ int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_strid
     p.aq = aq;
     p.ad = ad;
     p.blocks = blocks;
+    p.act_per_slot = act_per_slot;
     return launch_b1(p, st);
 }
 

@@ -74,7 +74,8 @@ __device__ void wave_select(const float val[RW], const bool live[RW], int n_sel,
 // then gather, clamp and renormalise (moe.rs:103-105).
 __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool resort,
                              RouteLds &sh, int32_t *ids, float *weights, float *logits_used,
-                             const int *given = nullptr, bool tab_ready = false) {
+                             const int *given = nullptr, bool tab_ready = false,
+                             float *probs_out = nullptr) {
     const int lane = threadIdx.x & 63;
     if (!tab_ready) expf_ref_tab_fill(sh.tab);
     float m = -INFINITY;  // f32::max fold: NaN-ignoring, order-free
@@ -120,6 +121,7 @@ __device__ void route_finish(const float l[RW], int n_expert, int n_used, bool r
         if (i < n_expert) {
             p[j] = p[j] / total;
             sh.p[i] = p[j];
+            if (probs_out) probs_out[i] = p[j];
         }
     }
     bool ranked = false;

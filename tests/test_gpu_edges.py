@@ -40,11 +40,15 @@ def test_refused_arguments_return_errors(gpu):
         assert L.llamd_rocm_matvec_q6k_resident(w.ptr, p(q), p(d), p(y), 2, 32) == -1
         assert L.llamd_rocm_matvec_q6k_resident(w.ptr, p(q), p(d), p(y), 1, 0) == -1
         assert L.llamd_rocm_matvec_q6k_resident(w.ptr, p(q), p(d), p(y), 1, 33) == -1
-        # a device pointer that is not a weight handle
+        # device memory too small to hold the rows as ggml Q6_K (19 rows of
+        # one block fit in 4096 bytes), and memory the library never handed out
         junk = gpu.DeviceBuffer(4096)
         assert L.llamd_rocm_matvec_q6k_resident(junk.ptr, p(q), p(d), p(y), 1, 32) == -1
-        assert "handle" in last_error()
+        assert "19 rows" in last_error()
         junk.close()
+        host = np.zeros(32 * 210, np.uint8)
+        assert L.llamd_rocm_matvec_q6k_resident(p(host), p(q), p(d), p(y), 1, 32) == -1
+        assert "neither a tiled upload" in last_error()
         # null buffers, empty input
         assert L.llamd_rocm_matvec_q6k_resident(w.ptr, None, p(d), p(y), 1, 32) == -1
         assert L.llamd_rocm_quantize_q8k(None, 1, p(q), p(d), None) == -1

@@ -62,12 +62,14 @@ def test_matvec_x3_refuses_a_foreign_pointer(gpu):
     L = _lib()
     blocks = 1
     w = gpu.DeviceWeights.upload(H.weights(16, blocks, 5), 16, blocks)
-    junk = gpu.DeviceBuffer(4096)
+    junk = gpu.DeviceBuffer(1024)  # 4 rows of ggml Q6_K: too few for 16
     o = gpu.DeviceBuffer(64)
     q, d = gpu.DeviceBuffer(256), gpu.DeviceBuffer(4)
     L.llamd_fwd_matvec_x3(w.ptr, junk.ptr, w.ptr, q.ptr, d.ptr, o.ptr, o.ptr, o.ptr, blocks, 16, 16, 16)
     from llamd_rs_amd._lib import last_error
-    assert "matvec_x3" in last_error()
+    assert "4 rows" in last_error()
+    # the refusal is reported once by llamd_fwd_last_error, then cleared
+    assert L.llamd_fwd_last_error() == -1
     _sync()
 
 
