@@ -487,6 +487,12 @@ float llamd_hip_event_elapsed_ms(void *start, void *stop);
  * multiple of 16) on the library stream, asynchronous. Its known traffic
  * (bytes read, bytes written) calibrates the profiler's HBM counters. */
 int llamd_hip_copy_calibration(void *d_dst, const void *d_src, size_t bytes);
+/* Not in the reference: n launches of llamd_fwd_matvec (w[i], aq[i], ad[i],
+ * out[i], blocks[i], rows[i]) enqueued by one call, for timing short launches
+ * back to back without the caller's per-call overhead. 0, or -1 at the first
+ * refused or failed launch (the earlier ones stay queued). */
+int llamd_hip_matvec_many(const void *const *w, const int8_t *const *aq, const float *const *ad,
+                          float *const *out, const int *blocks, const int *rows, int n);
 /* llamd.hip:1101-1148: one warm launch, then iters launches, total ms. */
 int llamd_rocm_matvec_bench(const void *d_w, const int8_t *aq, const float *ad, int blocks,
                             int rows, int iters, float *ms_out);

@@ -180,6 +180,7 @@ SIGNATURES = {
     "llamd_u_quantize_host": (i32, [vp, i32, vp, vp, vp]),
     "llamd_u_matvec_host": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
     "llamd_u_matvec_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32p]),
+    "llamd_hip_matvec_many": (i32, [vp, vp, vp, vp, vp, vp, i32]),
     "llamd_hip_be_rms_norm": (i32, [vp, vp, i32, i32, f]),
     "llamd_hip_be_softmax": (i32, [vp, vp, i32, i32]),
     "llamd_hip_be_silu": (i32, [vp, vp, sz]),

@@ -907,6 +907,23 @@ int llamd_u_matvec_bench(const void *base, const size_t *off, const int8_t *qs, 
     return bench_matvec(base, off, qs, ad, blocks, rows, nseq, iters, ms_out);
 }
 
+// ---- benchmarking -------------------------------------------------------------------
+// n Q6_K matvecs (the same checks and launch as llamd_fwd_matvec) enqueued
+// from one call, so a timed region of short launches measures the device and
+// not the calling language's per-call overhead.
+int llamd_hip_matvec_many(const void *const *w, const int8_t *const *aq, const float *const *ad,
+                          float *const *out, const int *blocks, const int *rows, int n) {
+    if (n < 0 || (n && (!w || !aq || !ad || !out || !blocks || !rows)))
+        return set_error("matvec_many: bad arguments");
+    for (int i = 0; i < n; ++i) {
+        Q6kView v;
+        if (resolve_q6k(w[i], nullptr, rows[i], blocks[i], false, &v)) return -1;
+        if (launch_q6k_mv_b1(v.tiled, 0, nullptr, aq[i], ad[i], out[i], rows[i], blocks[i], 1, 0, S()))
+            return set_error("matvec_many: launch %d failed", i);
+    }
+    return 0;
+}
+
 // ---- llamd-tensor Backend, row-wise (not in the reference's C ABI) ----------------
 // CpuBackend (crates/llamd-cpu/src/lib.rs:55-224) on device tensors, with the
 // same float operations in the same order: bit-identical results.

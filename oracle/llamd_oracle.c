@@ -32,6 +32,7 @@
  * Nothing here is "parity unpinned"; the Q6_K/Q8_0 weight QUANTIZERS (input
  * generators, not part of the reference) live with the synthetic-data code.
  */
+#include <omp.h>
 #include "llamd_oracle.h"
 
 #include <fenv.h>
@@ -223,6 +224,25 @@ void orc_matvec_q6k_act(const uint8_t *w, size_t rows, size_t k, const float *ad
                         const int8_t *aq, float *y) {
     size_t rb = k / QK_K * Q6K_BB;
     for (size_t r = 0; r < rows; ++r) y[r] = orc_dot_q6k_q8k(w + r * rb, ad, aq, k);
+}
+
+/* orc_matvec_q6k_act with the rows split over nthreads host threads (one
+ * OpenMP team, kept by the runtime between calls). Rows are independent, so
+ * the result is the same bits; only the CPU baseline's all-core figure uses
+ * it. Returns the team size. */
+int orc_matvec_q6k_act_mt(const uint8_t *w, size_t rows, size_t k, const float *ad,
+                          const int8_t *aq, float *y, int nthreads) {
+    size_t rb = k / QK_K * Q6K_BB;
+    int used = 1;
+#pragma omp parallel num_threads(nthreads)
+    {
+#pragma omp single
+        used = omp_get_num_threads();
+#pragma omp for schedule(static)
+        for (long r = 0; r < (long)rows; ++r)
+            y[r] = orc_dot_q6k_q8k(w + (size_t)r * rb, ad, aq, k);
+    }
+    return used;
 }
 
 /* Model::matvec_quant, Q6_K branch: crates/llamd-models/src/model.rs:241-276 */

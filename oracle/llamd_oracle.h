@@ -69,6 +69,9 @@ void orc_matvec_q6k_act(const uint8_t *w, size_t rows, size_t k, const float *ad
 /* R7: Model::matvec_quant, Q6_K branch: quantize x then dot every row
  * (crates/llamd-models/src/model.rs:241-276). */
 int orc_matvec_q6k(const uint8_t *w, size_t rows, size_t k, const float *x, float *y);
+/* orc_matvec_q6k_act over nthreads host threads (same bits); returns the threads used */
+int orc_matvec_q6k_act_mt(const uint8_t *w, size_t rows, size_t k, const float *ad,
+                          const int8_t *aq, float *y, int nthreads);
 
 /* R8: Model::matvec_quant fallback for F32 weights: sequential f32 sum
  * (crates/llamd-models/src/model.rs:253-262). */

@@ -41,6 +41,7 @@ def _lib():
             "orc_quantize_q8_k": (C.c_int, [vp, sz, vp, vp, vp]),
             "orc_dot_q6k_q8k": (f, [vp, vp, vp, sz]),
             "orc_matvec_q6k_act": (None, [vp, sz, sz, vp, vp, vp]),
+            "orc_matvec_q6k_act_mt": (C.c_int, [vp, sz, sz, vp, vp, vp, C.c_int]),
             "orc_matvec_q6k": (C.c_int, [vp, sz, sz, vp, vp]),
             "orc_matvec_f32": (None, [vp, sz, sz, vp, vp]),
             "orc_matvec_q8_0": (C.c_int, [vp, sz, sz, vp, vp]),
@@ -124,6 +125,15 @@ def matvec_q6k_act(w, rows: int, k: int, a: Q8K) -> np.ndarray:
     _lib().orc_matvec_q6k_act(_p(w), rows, k, _p(_f32(a.d)), _p(np.ascontiguousarray(a.qs, np.int8)),
                               _p(y))
     return y
+
+
+def matvec_q6k_act_mt(w, rows: int, k: int, a: Q8K, nthreads: int) -> tuple[np.ndarray, int]:
+    """matvec_q6k_act over nthreads host threads (same bits): (y, threads used)."""
+    w = _u8(w)
+    y = np.empty(rows, np.float32)
+    used = _lib().orc_matvec_q6k_act_mt(_p(w), rows, k, _p(_f32(a.d)),
+                                        _p(np.ascontiguousarray(a.qs, np.int8)), _p(y), nthreads)
+    return y, int(used)
 
 
 def matvec_q6k(w, rows: int, k: int, x) -> np.ndarray:
