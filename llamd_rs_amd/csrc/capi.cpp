@@ -1205,13 +1205,16 @@ extern "C" {
 
 void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq) {
     WInfo wi;
-    if (!lookup(d_w, KIND_Q6K, &wi) || wi.n_expert != 1 || wi.rows != rows || wi.blocks != blocks) {
+    if (lookup(d_w, KIND_Q6K, &wi) && (wi.n_expert != 1 || wi.rows != rows || wi.blocks != blocks)) {
         fail("lmhead_create: weight handle does not match rows=%d blocks=%d", rows, blocks);
         return nullptr;
     }
+    Q6kView v;
+    if (resolve_q6k(d_w, nullptr, rows, blocks, false, &v)) return nullptr;
     if (max_seq <= 0) { fail("lmhead_create: max_seq must be positive"); return nullptr; }
     LmHead *l = new LmHead();
-    l->w = d_w; l->rows = rows; l->blocks = blocks; l->cap = max_seq;
+    l->w = v.tiled; l->rows = rows; l->blocks = blocks; l->cap = max_seq;
+
     // per-tile arg-max candidates written by the matvec epilogue
     const int parts = (rows + 15) / 16;
     const size_t nq = (size_t)max_seq * blocks * QK;

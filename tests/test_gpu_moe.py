@@ -439,3 +439,35 @@ def test_decode_waits_that_give_up_still_route_exactly(gpu, qwen_layer):
     finally:
         lib().llamd_hip_tune(b"moe_polls", prev)
     assert lib().llamd_hip_tune(b"moe_polls", prev) == prev
+
+
+def test_lm_head_b1_repeats_and_all_nan(gpu):
+    """The b = 1 call quantizes x inside the matvec launch: calls in a row on
+    changing inputs each get their own logits and answer, and a vocabulary of
+    NaN logits gives 0 as the reference's scan does."""
+    rows, k = 4000, 512
+    w = H.weights(rows, 2, 23)
+    dw = gpu.DeviceWeights.upload(w, rows, 2)
+    head = gpu.LmHead(dw, max_seq=1)
+    try:
+        for seed in range(6):
+            x = H.sample(k, 40 + seed) * (1 + seed)
+            logits, ids = head.forward(x)
+            want = O.matvec_q6k(w, rows, k, x)
+            assert bits_equal(logits[0], want), seed
+            assert ids[0] == O.argmax(want), (seed, ids[0], O.argmax(want))
+    finally:
+        head.close()
+        dw.close()
+    wn = H.weights(rows, 2, 24).reshape(rows * 2, 210).copy()
+    wn[:, 208:210] = (0x00, 0x7E)  # every f16 scale NaN: every logit NaN
+    dw = gpu.DeviceWeights.upload(wn.reshape(-1), rows, 2)
+    head = gpu.LmHead(dw, max_seq=1)
+    try:
+        logits, ids = head.forward(H.sample(k, 3))
+        assert np.isnan(logits[0]).all() and ids[0] == 0
+        logits, ids = head.forward(H.sample(k, 4))
+        assert ids[0] == 0
+    finally:
+        head.close()
+        dw.close()
