@@ -58,13 +58,21 @@ int llamd_rocm_device_info(int dev, char *name, int name_len, char *arch, int ar
 size_t llamd_rocm_free_mem(void);
 /* Not in the reference: message for the last -1/NULL returned on this thread. */
 const char *llamd_hip_last_error(void);
-/* Not in the reference: tuning overrides for measurement. Returns the previous
- * value, -1 for an unknown key. "mv_ks": waves per 16-row tile of the Q6_K
- * matvec (1, 2 or 4; 0 = chosen from the shape); "batched_twin": the
- * prefill GEMM's waves take two 16-token chunks of one expert (1, default)
- * or one (0); "moe_polls": loads a wait inside the MoE decode kernel makes
- * before the waiting wave computes the awaited router logit itself (default
- * 2^18; 0 = at once; the results are the same bits). */
+/* Not in the reference: overrides that pin one of the library's live code
+ * paths, for tests and measurement (every path gives the same bits). Returns
+ * the previous value, -1 for an unknown key or value.
+ *   "mv_ks": waves per 16-row tile of the Q6_K matvec, 1, 4 or 8 (0: by
+ *     shape, the default; all three are chosen by shape somewhere);
+ *   "batched_twin": the grouped prefill GEMM's waves take two 16-token
+ *     chunks of one expert (1, default) or one (0, the kernel ungrouped
+ *     batches always use);
+ *   "moe_fused": the MoE decode schedule, 2 (default) or the fallbacks that
+ *     shapes outside the two-launch kernel's limits take, 1 and 0;
+ *   "moe_polls": loads a wait inside the MoE decode kernel makes before the
+ *     waiting wave computes the awaited router logit itself (default 2^18;
+ *     0 = at once);
+ *   "batch_decode_max", "model_graph", "model_fused_attn",
+ *     "model_fused_norm": batched-decode threshold and decode-step choices. */
 int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */

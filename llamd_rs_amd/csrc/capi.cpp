@@ -250,6 +250,8 @@ int llamd_hip_tune(const char *key, int value) {
         return prev;
     }
     if (!strcmp(key, "mv_ks")) {
+        if (value != 0 && value != 1 && value != 4 && value != 8)
+            return fail("tune: mv_ks takes 0 (by shape), 1, 4 or 8");
         const int prev = g_tune_mv_ks;
         g_tune_mv_ks = value;
         return prev;

@@ -748,11 +748,9 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
     // 2048: 4.14 -> 3.82 us -- and lose from ~1000 tiles on (LM head 41 ->
     // 52 us), where four waves already fill the machine.
     const int ks = g_tune_mv_ks ? g_tune_mv_ks : (p.blocks > 4 && items <= 384 ? 8 : 0);
-    if (p.blocks <= 16 && (ks == 2 || ks == 4 || ks == 8 || ks == 0)) {
+    if (p.blocks <= 16 && (ks == 4 || ks == 8 || ks == 0)) {
         if (ks == 8)
             hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX>), dim3(items), dim3(512), 0, st, p);
-        else if (ks == 2)
-            hipLaunchKernelGGL((q6k_mv_b1<2, false, NSEG, AMAX>), dim3((items + 1) / 2), dim3(256), 0, st, p);
         else
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
