@@ -1203,6 +1203,18 @@ struct LmHead {
 };
 }  // namespace
 
+int llamd::lmhead_forward_q8k(void *h, const int8_t *xq, const float *xd, float *d_logits,
+                              int32_t *d_ids) {
+    LmHead *l = (LmHead *)h;
+    if (!l || !xq || !xd || !d_logits || !d_ids) return fail("lmhead_forward_q8k: bad arguments");
+    hipStream_t st = stream();
+    int rc = launch_q6k_mv_b1(l->w, 0, nullptr, xq, xd, d_logits, l->rows, l->blocks, 1, 0, st,
+                              nullptr, l->pv.as<float>(), l->pi.as<int>());
+    rc |= launch_argmax_final(d_logits, l->rows, 1, l->pv.as<float>(), l->pi.as<int>(),
+                              (l->rows + 15) / 16, d_ids, st);
+    return rc ? fail("lmhead_forward_q8k: launch failed") : 0;
+}
+
 extern "C" {
 
 void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq) {

@@ -296,5 +296,8 @@ size_t lmhead_chunk_q_bytes(int nseq, int blocks);
 size_t lmhead_chunk_d_bytes(int nseq, int blocks);
 int lmhead_enqueue(const void *w, int rows, int blocks, const float *d_x, int nseq,
                    float *d_logits, int32_t *d_ids, const LmHeadScratch &sc);
+// One sequence whose activation is already Q8_K (xq [blocks*256], xd
+// [blocks]) through an LM-head handle: matvec + arg-max.
+int lmhead_forward_q8k(void *h, const int8_t *xq, const float *xd, float *d_logits, int32_t *d_ids);
 
 }  // namespace llamd

@@ -120,8 +120,10 @@ bool enqueue_step(Model *m, hipStream_t st) {
         }
     }
     if (rc || llamd_fwd_last_error()) return set_error("model: a launch failed (%s)", llamd_hip_last_error()) == 0;
-    llamd_fwd_rms_norm_mul(m->x, m->output_norm, m->xn, E, m->eps);
-    return llamd_hip_lmhead_forward(m->lmhead, m->xn, 1, m->logits, m->next) == 0;
+    // output norm and the LM head's Q8_K in one launch (the bits of
+    // rms_norm * w followed by quantize_q8_k), then matvec + arg-max
+    llamd_fwd_rms_norm_quant(m->x, m->output_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
+    return llamd::lmhead_forward_q8k(m->lmhead, m->aq, m->ad, m->logits, m->next) == 0;
 }
 
 void destroy(Model *m) {

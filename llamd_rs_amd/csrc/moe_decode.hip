@@ -396,18 +396,21 @@ __device__ void router_workgroup(const DecodeParams &p, DecodeLds &sm, int lane,
     if (lane == 0 && late && p.stats) p.stats[3] = 1;
 }
 
+// NORM: the fused FFN norm's buffers exist only in this instance (9 KB of
+// LDS the other launches would otherwise carry).
+template <bool NORM>
 __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
     asm volatile("" ::"s"(p.w_gate), "s"(p.w_up), "s"(p.rw), "s"(p.x), "s"(p.slots),
                  "s"(p.gu_stride), "s"(p.k), "s"(p.n_expert), "s"(p.n_used), "s"(p.n_chain));
     __shared__ DecodeLds sm;
-    __shared__ __align__(16) float xs[KMAX];  // the fused norm's output
-    __shared__ ExactSumLds xl;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // all sequences' chain workgroups first (the gate/up ones wait on them),
     // then the gate/up tiles, then one router workgroup per sequence
     const int b = blockIdx.x, chains = p.n_chain * p.nseq, gus = p.n_gu * p.nseq;
-    if (p.norm_w) {
+    if constexpr (NORM) {
+        __shared__ __align__(16) float xs[KMAX];  // the fused norm's output
+        __shared__ ExactSumLds xl;
         // one sequence: every workgroup forms x itself (the router
         // workgroup for the fallback folds of wait_logits); chain waves 0-3
         // stage their router rows under it
@@ -601,7 +604,12 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st) {
     if (p.norm_w && (l.nseq != 1 || !l.norm_a || !l.norm_b || !l.norm_sum || l.res != l.norm_sum ||
                      l.k > KMAX || l.k > XSUM_M * 512))
         return -1;
-    hipLaunchKernelGGL(moe_router_gateup, dim3((p.n_chain + p.n_gu + 1) * l.nseq), dim3(512), 0, st, p);
+    if (p.norm_w)
+        hipLaunchKernelGGL(moe_router_gateup<true>, dim3((p.n_chain + p.n_gu + 1) * l.nseq), dim3(512),
+                           0, st, p);
+    else
+        hipLaunchKernelGGL(moe_router_gateup<false>, dim3((p.n_chain + p.n_gu + 1) * l.nseq), dim3(512),
+                           0, st, p);
     hipLaunchKernelGGL(moe_down_route, dim3(p.down_tiles, l.nseq), dim3(64 * l.n_used), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
