@@ -139,23 +139,26 @@ def test_moe_layer_near_tied_router_stays_exact(gpu):
 @pytest.mark.parametrize("twin", [1, 0])
 def test_prefill_grouped_equals_token_major(gpu, twin):
     """R14: expert-grouped prefill == per-token moe_ffn, EXACT, including a
-    1-token case and experts of 1 to 5 16-token chunks (twin = 1: two chunks of
-    one expert per wave, with a lone chunk where the count is odd)."""
+    1-token case and experts of 1 to 13 16-token chunks (twin = 1: two chunks
+    of one expert per wave, with a lone chunk where the count is odd; twin =
+    0: one chunk per wave)."""
     from llamd_rs_amd import synth
     n_embd, n_ff, n_expert, n_used = 512, 256, 16, 4
     router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 700)
     layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
     prev = lib().llamd_hip_tune(b"batched_twin", twin)
     try:
-        for n_tok in (1, 5, 37, 80):
+        for n_tok in (1, 5, 37, 80, 200):
             x = synth.normal(10 + n_tok, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
             ids, w = synth.zipf_routing(20 + n_tok, 1.1, n_tok, n_expert, n_used)
             got = layer.prefill(x, ids.astype(np.int32), w)
             want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
             assert bits_equal(got, want), n_tok
-        if n_tok == 80:
             chunks = -(-np.bincount(ids.ravel(), minlength=n_expert) // 16)
-            assert chunks.max() >= 3 and (chunks % 2 == 1).any() and (chunks == 2).any()
+            if n_tok == 80:
+                assert chunks.max() >= 3 and (chunks % 2 == 1).any() and (chunks == 2).any()
+            if n_tok == 200:
+                assert chunks.max() > 8
     finally:
         lib().llamd_hip_tune(b"batched_twin", prev)
     layer.close()
@@ -258,12 +261,13 @@ def test_prefill_full_config_512_tokens(gpu, qwen_layer):
     want = np.concatenate(parts)
     bad = [t for t in range(n_tok) if not bits_equal(got[t], want[t])]
     assert not bad, bad[:10]
-    prev = lib().llamd_hip_tune(b"batched_twin", 0)
-    try:
-        single = layer.prefill(x, ids.astype(np.int32), w)
-    finally:
-        lib().llamd_hip_tune(b"batched_twin", prev)
-    assert bits_equal(single, want)
+    for alt in (0,):  # the one-chunk wave kernel gives the same bits
+        prev = lib().llamd_hip_tune(b"batched_twin", alt)
+        try:
+            other = layer.prefill(x, ids.astype(np.int32), w)
+        finally:
+            lib().llamd_hip_tune(b"batched_twin", prev)
+        assert bits_equal(other, want), alt
 
 
 def _host_bound(router, x):
