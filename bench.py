@@ -142,6 +142,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="plain launches everywhere, no graph replay: for rocprofv3 kernel traces, "
                          "which space graph-replayed kernels tens of microseconds apart")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="set a kernel tune key (llamd_hip_tune) before measuring, e.g. mv_dot=1")
     args = ap.parse_args()
     global EAGER_ONLY
     EAGER_ONLY = args.eager
@@ -155,6 +157,12 @@ def main():
     L = lib()
     if not rocm.available():
         raise SystemExit("no ROCm device visible")
+    tune = {}
+    for kv in args.tune:
+        key, val = kv.split("=")
+        if L.llamd_hip_tune(key.encode(), int(val)) < 0:
+            raise SystemExit(f"unknown tune key or value: {kv}")
+        tune[key] = int(val)
     info = rocm.device_info(0)
     log(f"device: {info.name} {info.arch} CUs={info.compute_units}")
     K, W = args.steps, args.warmup
@@ -295,7 +303,8 @@ def main():
         "config": {"workload": "configs[1]: Q6_K expert-FFN matvecs at batch 1, gate+up [768x2048] "
                                "and down [2048x768], one launch each per step, >=1 GiB of weight "
                                "copies in rotation",
-                   "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2)},
+                   "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2),
+                   **({"tune": tune} if tune else {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,

@@ -249,6 +249,11 @@ int llamd_hip_tune(const char *key, int value) {
         g_tune_batched_twin = value ? 1 : 0;
         return prev;
     }
+    if (!strcmp(key, "mv_dot")) {
+        const int prev = g_tune_mv_dot;
+        g_tune_mv_dot = value ? 1 : 0;
+        return prev;
+    }
     if (!strcmp(key, "mv_ks")) {
         if (value != 0 && value != 1 && value != 4 && value != 8)
             return fail("tune: mv_ks takes 0 (by shape), 1, 4 or 8");

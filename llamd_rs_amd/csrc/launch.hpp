@@ -12,6 +12,7 @@ namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
 extern int g_tune_batched_twin;  // grouped q6k_mv_batched: two chunks of one expert per wave
+extern int g_tune_mv_dot;  // 1: q6k_mv_b1's integer part on v_dot2 instead of MFMA (one matrix)
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step

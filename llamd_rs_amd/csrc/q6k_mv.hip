@@ -79,11 +79,12 @@ struct MvParams {
 // meet in LDS and are folded in block order -- the same additions in the same
 // order as a single wave walking every block, so splitting K changes the
 // latency, never the bits.
-template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false>
+template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false, bool DOT = false>
 __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) {
     constexpr int IPW = KS >= 4 ? 1 : 4 / KS;   // items per workgroup
     constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
     __shared__ float terms[KS > 1 ? IPW : 1][KS > 1 ? MAXB : 1][TILE_ROWS][8];
+    __shared__ __align__(16) int16_t a16s[DOT ? IPW * KS : 1][DOT ? QK_K : 1];  // DOT: per wave
     const int lane = threadIdx.x & 63;
     // every kernarg field the common path reads, fetched in one batch up front
     asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.y), "s"(p.seg0.rows), "s"(p.seg0.tiles),
@@ -148,15 +149,23 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
         // two register sets in ping-pong: the next block's loads are in
         // flight while the current block is computed, with no copies
         BlockRegs ra, rb;
-        load_block(ra, seg0 + (size_t)b0 * SEG_BYTES, aq, ad, b0, lane, n);
+        auto load = [&](BlockRegs &r, int bb) {
+            if constexpr (DOT) load_block_dot(r, seg0 + (size_t)bb * SEG_BYTES, aq, ad, bb, lane, n);
+            else load_block(r, seg0 + (size_t)bb * SEG_BYTES, aq, ad, bb, lane, n);
+        };
+        auto terms_of = [&](const BlockRegs &r, float &te, float &to) {
+            if constexpr (DOT) block_terms_dot(r, a16s[DOT ? wave : 0], lane, n, s, te, to);
+            else block_terms(r, msel, te, to);
+        };
+        load(ra, b0);
         for (int b = b0; b < b1; b += 2) {
-            if (b + 1 < b1) load_block(rb, seg0 + (size_t)(b + 1) * SEG_BYTES, aq, ad, b + 1, lane, n);
+            if (b + 1 < b1) load(rb, b + 1);
             float te, to;
-            block_terms(ra, msel, te, to);
+            terms_of(ra, te, to);
             consume_terms<KS>(b, te, to, se, so, terms[local], n, s);
             if (b + 1 >= b1) break;
-            if (b + 2 < b1) load_block(ra, seg0 + (size_t)(b + 2) * SEG_BYTES, aq, ad, b + 2, lane, n);
-            block_terms(rb, msel, te, to);
+            if (b + 2 < b1) load(ra, b + 2);
+            terms_of(rb, te, to);
             consume_terms<KS>(b + 1, te, to, se, so, terms[local], n, s);
         }
     }
@@ -717,6 +726,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 }  // namespace
 
 int g_tune_mv_ks = 0;
+int g_tune_mv_dot = 0;
 int g_tune_batched_twin = 1;
 
 namespace {
@@ -740,7 +750,7 @@ void set_segments(MvParams &p, int n, const void *const *w, float *const *y, con
     p.n_slots = n_slots;
 }
 
-template <int NSEG, bool AMAX = false>
+template <int NSEG, bool AMAX = false, bool DOT = false>
 void launch_b1_n(const MvParams &p, hipStream_t st) {
     const int items = p.items;
     // Measured on MI355X: eight waves per tile (one block each at k = 2048)
@@ -750,20 +760,22 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
     const int ks = g_tune_mv_ks ? g_tune_mv_ks : (p.blocks > 4 && items <= 384 ? 8 : 0);
     if (p.blocks <= 16 && (ks == 4 || ks == 8 || ks == 0)) {
         if (ks == 8)
-            hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX>), dim3(items), dim3(512), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX, DOT>), dim3(items), dim3(512), 0, st, p);
         else
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
             // tile at every size -- more loads in flight per tile and shorter
             // per-wave chains.
-            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX>), dim3(items), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX, DOT>), dim3(items), dim3(256), 0, st, p);
     } else {
-        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX>), dim3((items + 3) / 4), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX, DOT>), dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
 }
 
 int launch_b1(const MvParams &p, hipStream_t st) {
-    if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
+    if (p.amax_v && g_tune_mv_dot) launch_b1_n<1, true, true>(p, st);
+    else if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
+    else if (p.n_seg == 1 && g_tune_mv_dot) launch_b1_n<1, false, true>(p, st);  // VALU dot products
     else if (p.n_seg == 1) launch_b1_n<1>(p, st);
     else if (p.n_seg == 2) launch_b1_n<2>(p, st);
     else launch_b1_n<3>(p, st);

@@ -181,7 +181,7 @@ def test_q8_0_matvec_within_reduction(gpu):
 
 @pytest.mark.parametrize("rows,blocks", [(48, 8), (768, 8), (40, 5), (64, 16), (33, 3)])
 def test_every_k_split_is_bit_identical(gpu, rows, blocks):
-    """The matvec splits K over 1, 2, 4 or 8 waves per 16-row tile (chosen by
+    """The matvec splits K over 1, 4 or 8 waves per 16-row tile (chosen by
     grid size); every split folds the per-block terms in block order, so all
     of them give the reference's bits (dot.rs:190-195)."""
     from llamd_rs_amd._lib import lib
@@ -197,5 +197,27 @@ def test_every_k_split_is_bit_identical(gpu, rows, blocks):
             assert bits_equal(dw.matvec(act), want), ks
         assert L.llamd_hip_tune(b"mv_ks", 2) == -1  # retired: lost to 4 and 8 at every shape
     finally:
+        L.llamd_hip_tune(b"mv_ks", 0)
+        dw.close()
+
+
+@pytest.mark.parametrize("rows,blocks", [(48, 8), (40, 5), (33, 3), (2048, 8), (768, 16), (1, 1)])
+def test_valu_dot_variant_is_bit_identical(gpu, rows, blocks):
+    """The batch-1 kernel with its integer part on v_dot2 (tune key mv_dot)
+    instead of the matrix cores gives the same bits at every K split."""
+    from llamd_rs_amd._lib import lib
+    w = H.weights(rows, blocks, 90 + blocks)
+    x = H.sample(blocks * QK_K, 91 + rows)
+    act = gpu.quantize_q8k_on_device(x)
+    want = cpu_rows(w, rows, blocks, act)
+    dw = gpu.DeviceWeights.upload(w, rows, blocks)
+    L = lib()
+    try:
+        assert L.llamd_hip_tune(b"mv_dot", 1) == 0
+        for ks in (1, 4, 8, 0):
+            L.llamd_hip_tune(b"mv_ks", ks)
+            assert bits_equal(dw.matvec(act), want), ks
+    finally:
+        L.llamd_hip_tune(b"mv_dot", 0)
         L.llamd_hip_tune(b"mv_ks", 0)
         dw.close()

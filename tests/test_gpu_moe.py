@@ -211,11 +211,21 @@ def test_lm_head_b16_argmax_exact(gpu, lm_head):
         assert ids[s] == O.argmax(want[s]), s
 
 
-@pytest.mark.parametrize("nseq", [1, 16])
-def test_lm_head_argmax_ties_and_nan(gpu, nseq):               # device_forward.rs:23-37
+@pytest.mark.parametrize("nseq,dot", [(1, 0), (16, 0), (1, 1)])
+def test_lm_head_argmax_ties_and_nan(gpu, nseq, dot):          # device_forward.rs:23-37
     """The per-tile arg-max candidates of the matvec epilogue, reduced: a
     duplicated winning row loses to its lower-index copy across tiles, a NaN
-    logit never wins, and a NaN at index 0 makes the answer 0."""
+    logit never wins, and a NaN at index 0 makes the answer 0. dot = 1 runs
+    the batch-1 kernel's v_dot2 variant (tune key mv_dot)."""
+    from llamd_rs_amd._lib import lib
+    lib().llamd_hip_tune(b"mv_dot", dot)
+    try:
+        _lm_head_ties_and_nan(gpu, nseq)
+    finally:
+        lib().llamd_hip_tune(b"mv_dot", 0)
+
+
+def _lm_head_ties_and_nan(gpu, nseq):
     rows, k = 64, 256
     x = H.sample(nseq * k, 5).reshape(nseq, k)
     w = H.weights(rows, 1, 17).reshape(rows, 210).copy()
