@@ -485,3 +485,24 @@ def test_lm_head_b1_repeats_and_all_nan(gpu):
     finally:
         head.close()
         dw.close()
+
+
+@pytest.mark.parametrize("rows,blocks", [(4000, 8), (1000, 5), (333, 3), (2000, 16), (50, 13), (700, 17)])
+def test_lm_head_b1_block_counts(gpu, rows, blocks):
+    """The b = 1 LM head at block counts that split unevenly over the matvec's
+    four waves per tile and at row counts that leave a partial last tile:
+    the CPU's logits and id bit for bit, over calls in a row."""
+    k = blocks * QK_K
+    w = H.weights(rows, blocks, 500 + blocks)
+    dw = gpu.DeviceWeights.upload(w, rows, blocks)
+    head = gpu.LmHead(dw, max_seq=1)
+    try:
+        for j in range(3):
+            x = H.sample(k, 600 + j) * (1 + j)
+            want = O.matvec_q6k(w, rows, k, x)
+            logits, ids = head.forward(x)
+            assert bits_equal(logits[0], want), j
+            assert ids[0] == O.argmax(want), (j, ids[0])
+    finally:
+        head.close()
+        dw.close()
