@@ -65,7 +65,7 @@ struct DecodeParams {
     const float *norm_a, *norm_b, *norm_w;  // fused FFN norm (norm_w null: x is given)
     float norm_eps;
     float *norm_sum;
-    int polls;  // bound of every wait on another workgroup (slot_wait)
+    int polls;  // bound of every wait on another workgroup (slots_wait)
 };
 
 // The parameters of sequence `seq` of a batch: every per-token array offset
@@ -107,12 +107,16 @@ union DecodeLds {
 __device__ void wait_logits(const DecodeParams &p, float l[RW], bool &late) {
     const int lane = threadIdx.x & 63;
     bool lt = false;
+    bool live[RW];
+    unsigned long long vs[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) live[j] = lane + WAVE * j < p.n_expert;
+    slots_wait(p.slots + p.n_expert, live, vs, p.polls);
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         const int i = lane + WAVE * j;
-        unsigned long long v = 0;
-        if (i < p.n_expert) {
-            v = slot_wait(&p.slots[p.n_expert + i], p.polls);
+        unsigned long long v = vs[j];
+        if (live[j]) {
             if (v == SLOT_EMPTY) {
                 lt = true;
                 const float *w = p.rw + (size_t)i * p.k;
@@ -137,15 +141,14 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     double T[RW], E[RW];
     float key[RW];
     bool live[RW], lt = false;
+    unsigned long long vs[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) live[j] = lane + WAVE * j < p.n_expert;
+    slots_wait(p.slots, live, vs, p.polls);
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
-        const int i = lane + WAVE * j;
-        live[j] = i < p.n_expert;
-        unsigned long long v = 0;
-        if (live[j]) {
-            v = slot_wait(&p.slots[i], p.polls);
-            lt = lt || v == SLOT_EMPTY;
-        }
+        const unsigned long long v = vs[j];
+        lt = lt || (live[j] && v == SLOT_EMPTY);
         key[j] = __uint_as_float((unsigned)v);
         T[j] = key[j];
         E[j] = __uint_as_float((unsigned)(v >> 32));

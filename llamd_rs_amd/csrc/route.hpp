@@ -288,19 +288,30 @@ __device__ __forceinline__ void slot_store(unsigned long long *slot, unsigned lo
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Bounded wait for a slot to be filled: at most `polls` loads (about a
-// quarter of a second at the default 2^18). A producer normally has a lower
-// workgroup index and is already placed, but HIP does not promise dispatch
-// order, so every caller must survive SLOT_EMPTY: the MoE decode kernel then
-// computes the value it waited for itself (wait_logits), the same bits.
-__device__ __forceinline__ unsigned long long slot_wait(const unsigned long long *slot, int polls) {
+// Bounded wait for the lane's RW slots (base + lane + 64 j, j < RW, those
+// with live[j]) to be filled: at most `polls` passes (about a quarter of a
+// second at the default 2^18). Every pass loads all slots still empty
+// together, so one round trip to memory serves all of them. A producer
+// normally has a lower workgroup index and is already placed, but HIP does
+// not promise dispatch order, so every caller must survive a slot left
+// SLOT_EMPTY: the MoE decode kernel then computes the value it waited for
+// itself (wait_logits), the same bits.
+__device__ __forceinline__ void slots_wait(const unsigned long long *base, const bool live[RW],
+                                           unsigned long long v[RW], int polls) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < RW; ++j) v[j] = live[j] ? SLOT_EMPTY : 0ull;
     for (int it = 0; it < polls; ++it) {
-        const unsigned long long v =
-            __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v != SLOT_EMPTY) return v;
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+            if (v[j] == SLOT_EMPTY)
+                v[j] = __hip_atomic_load(base + lane + WAVE * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool pending = false;
+#pragma unroll
+        for (int j = 0; j < RW; ++j) pending = pending || v[j] == SLOT_EMPTY;
+        if (!pending) break;
         __builtin_amdgcn_s_sleep(2);
     }
-    return SLOT_EMPTY;
 }
 
 }  // namespace llamd
