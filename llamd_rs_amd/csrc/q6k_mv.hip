@@ -553,7 +553,7 @@ __device__ __forceinline__ void fold_digits(uint64_t codes, const FoldScales &f,
 // folded once per class and feed the MFMAs of all NC chunks, so a second
 // chunk costs only its MFMAs and its float epilogue. Each chunk's class plane
 // of a block is one contiguous 512-byte load for the wave.
-template <int NC>
+template <int NC, bool PF = false>
 __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int t, int sub0,
                                              int st0, int cnt, int start, int expert) {
     const int n = lane & 15, s = lane >> 4;
@@ -570,34 +570,44 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
 #pragma unroll
             for (int v = 0; v < 4; ++v) sums[u][c][v] = 0.0f;
 
-    for (int b = 0; b < p.blocks; ++b, seg += SEG_BYTES) {
-        const uint4 q0 = *(const uint4 *)(seg + 16 * lane);
-        const uint4 q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
-        const uint4 q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
-        const uint32_t scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
-        const uint2 dw = *(const uint2 *)(seg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
+    // one block's operands: the lane's weight words and its chunks' class
+    // planes and scales
+    struct Regs {
+        uint4 q0, q1, q2;
+        uint32_t scw;
+        uint2 dw;
         float adb[NC];
         long act[NC][8];
+    };
+    auto load = [&](Regs &r, int b) {
+        const uint8_t *sg = seg + (size_t)b * SEG_BYTES;
+        r.q0 = *(const uint4 *)(sg + 16 * lane);
+        r.q1 = *(const uint4 *)(sg + SEG_PART + 16 * lane);
+        r.q2 = *(const uint4 *)(sg + 2 * SEG_PART + 16 * lane);
+        r.scw = *(const uint32_t *)(sg + SEG_SC + 4 * lane);
+        r.dw = *(const uint2 *)(sg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
 #pragma unroll
         for (int u = 0; u < NC; ++u) {
-            adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
+            r.adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
 #pragma unroll
             for (int c = 0; c < 8; ++c)
-                act[u][c] = *(const long *)(aq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
+                r.act[u][c] = *(const long *)(aq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
         }
-        const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
-        const FoldScales fs = fold_scales(scw);
+    };
+    auto compute = [&](const Regs &r) {
+        const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
+        const FoldScales fs = fold_scales(r.scw);
         // f16(d) of the lane's 4 rows (D rows 4s..4s+3) times the token's scale
-        const float d4[4] = {f16_bits_to_f32((uint16_t)(dw.x & 0xFFFF)),
-                             f16_bits_to_f32((uint16_t)(dw.x >> 16)),
-                             f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)),
-                             f16_bits_to_f32((uint16_t)(dw.y >> 16))};
+        const float d4[4] = {f16_bits_to_f32((uint16_t)(r.dw.x & 0xFFFF)),
+                             f16_bits_to_f32((uint16_t)(r.dw.x >> 16)),
+                             f16_bits_to_f32((uint16_t)(r.dw.y & 0xFFFF)),
+                             f16_bits_to_f32((uint16_t)(r.dw.y >> 16))};
         float dd[NC][4];
 #pragma unroll
         for (int u = 0; u < NC; ++u)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dd[u][v] = d4[v] * adb[u];
+            for (int v = 0; v < 4; ++v) dd[u][v] = d4[v] * r.adb[u];
         // software-pipelined by one class: the MFMAs of class c+1 are issued
         // before the epilogue of class c reads its results
         const v4i zero = {0, 0, 0, 0};
@@ -607,8 +617,8 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
             fold_digits((uint64_t)unpack_codes(nib, hb, 0), fs, a_lo, a_hi);
 #pragma unroll
             for (int u = 0; u < NC; ++u) {
-                dh[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[u][0], zero, 0, 0, 0);
-                dl[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[u][0], zero, 0, 0, 0);
+                dh[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, r.act[u][0], zero, 0, 0, 0);
+                dl[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, r.act[u][0], zero, 0, 0, 0);
             }
         }
 #pragma unroll
@@ -618,8 +628,8 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
                 fold_digits((uint64_t)unpack_codes(nib, hb, c + 1), fs, a_lo, a_hi);
 #pragma unroll
                 for (int u = 0; u < NC; ++u) {
-                    dh[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[u][c + 1], zero, 0, 0, 0);
-                    dl[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[u][c + 1], zero, 0, 0, 0);
+                    dh[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, r.act[u][c + 1], zero, 0, 0, 0);
+                    dl[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, r.act[u][c + 1], zero, 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -629,6 +639,28 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
                     const int aux = dh[c & 1][u][v] * 256 + dl[c & 1][u][v];
                     sums[u][c][v] = sums[u][c][v] + dd[u][v] * (float)aux;
                 }
+        }
+    };
+    if constexpr (PF) {
+        // two register sets in ping-pong: the next block's loads are in
+        // flight while the current block is computed. The loads are
+        // unconditional (past the last block they re-read it, unused), so
+        // the compiler waits for each block's own loads only.
+        Regs ra, rb;
+        const int last = p.blocks - 1;
+        load(ra, 0);
+        for (int b = 0; b < p.blocks; b += 2) {
+            load(rb, min(b + 1, last));
+            compute(ra);
+            if (b + 1 >= p.blocks) break;
+            load(ra, min(b + 2, last));
+            compute(rb);
+        }
+    } else {
+        for (int b = 0; b < p.blocks; ++b) {
+            Regs r;
+            load(r, b);
+            compute(r);
         }
     }
 #pragma unroll
@@ -691,7 +723,7 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
         cnt = p.single_count;
         if (sub >= (cnt + 15) / 16) return;
     }
-    batched_tile<1>(p, lane, t, sub, st, cnt, start, expert);
+    batched_tile<1, true>(p, lane, t, sub, st, cnt, start, expert);
 }
 
 // One wave per (group, twin, 16-row tile): a twin is two consecutive chunks
