@@ -240,14 +240,6 @@ def main():
     bytes_step = sum(per_shape_bytes.values())
     value = bytes_step * K / (ms * 1e-3) / 1e9
     log(f"configs[1] step: {ms / K * 1e3:.2f} us, {value:.1f} GB/s")
-    graph_res = None
-    if not EAGER_ONLY:
-        msg = time_region(L, step, K, W)
-        graph_res = {"us_per_step": msg / K * 1e3, "gbs": bytes_step * K / (msg * 1e-3) / 1e9,
-                     "pct_of_hbm_peak": round(100 * bytes_step * K / (msg * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
-                     "how": "the same K steps captured once into a HIP graph and replayed"}
-        log(f"  configs[1] graph replay: {graph_res}")
-
     shape_res = {}
     for name, rows, k, _ in shapes:
         msn = time_many([name], K, W)
@@ -257,6 +249,45 @@ def main():
             "gbs_back_to_back": per_shape_bytes[name] * K / (msn * 1e-3) / 1e9,
         }
         log(f"  {name}: {shape_res[name]}")
+    # what a launch costs here with no work, and with only the reads of one
+    # configs[1] matrix (same rotating copies, same back-to-back enqueue)
+    def time_reads(nbytes, grid, steps, warmup):
+        arr = lambda i0, n: (C.c_void_p * n)(*[copies["gate"][i % ncopies].ptr for i in range(i0, i0 + n)])
+        srcs, srcs_t = arr(0, warmup), arr(warmup, steps)
+        if L.llamd_hip_read_many(srcs, nbytes, grid, warmup):
+            raise RuntimeError("read_many")
+        sync(L)
+        t = Timer(L)
+        t.rec(0)
+        if L.llamd_hip_read_many(srcs_t, nbytes, grid, steps):
+            raise RuntimeError("read_many")
+        t.rec(1)
+        sync(L)
+        ms_ = t.ms(0, 1)
+        t.close()
+        return ms_ / steps * 1e3
+    wbytes = q6k_bytes(768, 2048) // 16 * 16
+    launch_floor = {
+        "empty_kernel_us": round(time_reads(0, 48, K, W), 3),
+        "read_only_us": {f"grid{g}": round(time_reads(wbytes, g, K, W), 3) for g in (48, 128, 512)},
+        "read_bytes": wbytes,
+        "how": "llamd_hip_read_many: back-to-back launches of an empty kernel, and of a kernel that "
+               "only reads one 768x2048 Q6_K matrix (256-thread workgroups), from the headline's "
+               "rotating weight copies",
+    }
+    log(f"  launch floor: {launch_floor}")
+
+    # The graph-replay figure comes last: the plain-launch regions timed
+    # right after a graph's replay ran slower (5.5 instead of 3.3 us per
+    # launch for the first one).
+    graph_res = None
+    if not EAGER_ONLY:
+        msg = time_region(L, step, K, W)
+        graph_res = {"us_per_step": msg / K * 1e3, "gbs": bytes_step * K / (msg * 1e-3) / 1e9,
+                     "pct_of_hbm_peak": round(100 * bytes_step * K / (msg * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+                     "how": "the same K steps captured once into a HIP graph and replayed"}
+        log(f"  configs[1] graph replay: {graph_res}")
+
     # dominant kernel for the roofline: q6k_mv_b1, the step's three launches.
     # Average launch duration = HIP-event time of the timed region (plain
     # launches on the library stream) / launches in it.
@@ -276,6 +307,7 @@ def main():
     copies = None
 
     extra = {"configs1_per_shape": shape_res, "configs1_graph_replay": graph_res,
+             "configs1_launch_floor": launch_floor,
              "copy_calibration": bench_copy(L, rocm)}
 
     # ---- extra configs ---------------------------------------------------------

@@ -498,6 +498,12 @@ float llamd_hip_event_elapsed_ms(void *start, void *stop);
  * multiple of 16) on the library stream, asynchronous. Its known traffic
  * (bytes read, bytes written) calibrates the profiler's HBM counters. */
 int llamd_hip_copy_calibration(void *d_dst, const void *d_src, size_t bytes);
+/* Not in the reference: n launches of a read-only kernel (grid workgroups of
+ * 256 threads) over `bytes` at d_src[i], back to back on the library stream,
+ * asynchronous; bytes = 0 launches an empty kernel (d_src may be NULL). The
+ * launch-cost reference for short kernels: what a launch costs with no work,
+ * and with only the reads. */
+int llamd_hip_read_many(const void *const *d_src, size_t bytes, int grid, int n);
 /* Not in the reference: n launches of llamd_fwd_matvec (w[i], aq[i], ad[i],
  * out[i], blocks[i], rows[i]) enqueued by one call, for timing short launches
  * back to back without the caller's per-call overhead. 0, or -1 at the first

@@ -127,6 +127,7 @@ SIGNATURES = {
     "llamd_hip_event_record": (i32, [vp]),
     "llamd_hip_event_elapsed_ms": (f, [vp, vp]),
     "llamd_hip_copy_calibration": (i32, [vp, vp, sz]),
+    "llamd_hip_read_many": (i32, [vp, sz, i32, i32]),
     "llamd_rocm_matvec_bench": (i32, [vp, vp, vp, i32, i32, i32, f32p]),
     "llamd_rocm_matvec_grouped_bench": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32p]),
     "llamd_fwd_memset": (i32, [vp, i32, sz]),

@@ -1324,6 +1324,15 @@ static int bench_common(const void *d_w, const int32_t *eid, const int8_t *aq, c
     return rc ? fail("bench: timing failed") : 0;
 }
 
+int llamd_hip_read_many(const void *const *d_src, size_t bytes, int grid, int n) {
+    if (n < 0 || grid < 1 || bytes % 16 || (n && bytes && !d_src))
+        return fail("read_many: bad arguments (bytes a multiple of 16, grid >= 1)");
+    for (int i = 0; i < n; ++i)
+        if (launch_read_calibration(bytes ? d_src[i] : nullptr, bytes, grid, stream()))
+            return fail("read_many: launch %d failed", i);
+    return 0;
+}
+
 int llamd_hip_copy_calibration(void *d_dst, const void *d_src, size_t bytes) {
     if (!d_dst || !d_src || bytes % 16) return fail("copy_calibration: bytes must be a multiple of 16");
     return launch_copy_calibration(d_dst, d_src, bytes, stream()) ? fail("copy_calibration: launch") : 0;

@@ -170,6 +170,7 @@ int launch_add_rms_norm_mul(const float *x, const float *o, const float *w, floa
 // The reference's router logits (sequential f32 fold per expert) and, in the
 // same launch, Q8_K of x for the expert matvecs. k % 256 == 0, k <= 2048.
 int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_t st);
+int launch_read_calibration(const void *src, size_t bytes, int grid, hipStream_t st);
 struct RouterLaunch {
     const float *w, *x;
     int n_expert, k;

@@ -109,7 +109,30 @@ __global__ __launch_bounds__(256) void copy_calibration(uint4 *dst, const uint4 
         dst[i] = src[i];
 }
 
+// Read-only pass over n16 16-byte words (four independent loads in flight
+// per thread), the launch-cost reference for short kernels: with n16 = 0 it
+// is an empty kernel. The sink store never happens in practice; it keeps the
+// loads.
+__global__ __launch_bounds__(256) void read_calibration(const uint4 *src, size_t n16, uint32_t *sink) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        acc ^= a.x ^ b.y ^ c.z ^ d.w ^ a.w ^ b.x ^ c.y ^ d.z;
+    }
+    for (; i < n16; i += stride) acc ^= src[i].x ^ src[i].w;
+    if (acc == 0x9E3779B9u && sink) sink[0] = acc;
+}
+
 }  // namespace
+
+int launch_read_calibration(const void *src, size_t bytes, int grid, hipStream_t st) {
+    if (bytes % 16 || grid < 1) return -1;
+    hipLaunchKernelGGL(read_calibration, dim3(grid), dim3(256), 0, st, (const uint4 *)src, bytes / 16,
+                       nullptr);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_copy_calibration(void *dst, const void *src, size_t bytes, hipStream_t st) {
     if (bytes % 16) return -1;
