@@ -195,8 +195,11 @@ __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, con
 // ROWS_PER_WAVE rows; lane l owns Q8_0 blocks l, l+64, ... and loads each
 // block's 32 activations once for all its rows. Products are d*q rounded
 // (the dequantized weight, exact) times x, accumulated with FMA; within
-// REDUCTION of the reference's sequential sum.
-constexpr int Q80_ROWS_PER_WAVE = 4;
+// REDUCTION of the reference's sequential sum. Two rows per wave measured
+// best at 4096 x 2048 on MI355X (per launch, graph replay: 1 row 6.3 us,
+// 2 rows 4.7, 4 rows 4.8, 8 rows 6.4; loading all rows' words before the
+// arithmetic was slower, 5.3).
+constexpr int Q80_ROWS_PER_WAVE = 2;
 
 __global__ __launch_bounds__(256) void q8_0_mv(const int8_t *qs, const uint16_t *dp, const float *x,
                                                float *y, int rows, int k) {
