@@ -193,3 +193,26 @@ def test_moe_layer_256_experts_top16(gpu):
         assert bits_equal(got, O.moe_ffn_tokens(xs, n_embd, n_ff, n_expert, gate, up, down, pids, pw))
     finally:
         layer.close()
+
+
+def test_measurement_helpers(gpu):
+    """The calibration entry points bench.py times with: the copy moves the
+    bytes, the read-only and empty launches run and refuse bad arguments."""
+    import ctypes as C
+    from llamd_rs_amd._lib import lib
+    L = lib()
+    n = 1 << 20
+    src = gpu.DeviceBuffer.from_array(np.arange(n // 4, dtype=np.int32))
+    dst = gpu.DeviceBuffer(n)
+    assert L.llamd_hip_copy_calibration(dst.ptr, src.ptr, n) == 0
+    assert np.array_equal(dst.download(np.empty(n // 4, np.int32)), np.arange(n // 4, dtype=np.int32))
+    assert L.llamd_hip_copy_calibration(dst.ptr, src.ptr, n - 4) == -1
+    ptrs = (C.c_void_p * 3)(src.ptr, dst.ptr, src.ptr)
+    assert L.llamd_hip_read_many(ptrs, n, 48, 3) == 0
+    assert L.llamd_hip_read_many(None, 0, 48, 5) == 0       # empty kernels
+    assert L.llamd_hip_read_many(ptrs, n - 8, 48, 3) == -1  # not a multiple of 16
+    assert L.llamd_hip_read_many(ptrs, n, 0, 3) == -1       # no workgroups
+    assert L.llamd_hip_read_many(None, n, 48, 3) == -1      # bytes but no sources
+    assert L.llamd_fwd_sync() == 0
+    src.close()
+    dst.close()
