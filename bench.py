@@ -344,6 +344,28 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def moe_margin(layers):
+    """Routing diagnostics over the timed calls: how many calls started
+    gate/up on a certified top-k set, whether any wait gave up, and for the
+    last call of each layer the certification margin min(T - E | chosen) -
+    max(T + E | others) and the gap between the 8th and 9th logit estimate."""
+    calls = certified = gave_up = 0
+    margins, gaps = [], []
+    for layer in layers:
+        c, est = layer.counters()
+        calls += int(c[0])
+        certified += int(c[2])
+        gave_up = max(gave_up, int(c[3]))
+        T, E = est[0], est[1]
+        order = np.argsort(-T, kind="stable")
+        chosen, others = order[:8], order[8:]
+        margins.append(float(np.min(T[chosen] - E[chosen]) - np.max(T[others] + E[others])))
+        gaps.append(float(T[order[7]] - T[order[8]]))
+    return {"calls": calls, "certified": certified, "waits_gave_up": gave_up,
+            "last_call_margin": [round(m, 6) for m in margins],
+            "last_call_gap_8_9": [round(g, 6) for g in gaps]}
+
+
 def bench_copy(L, rocm, mib=512, reps=5):
     """A plain device copy of known size: the achievable-bandwidth reference
     and the calibration kernel for the profiler's FETCH_SIZE / WRITE_SIZE."""
@@ -483,7 +505,8 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     by = n_expert * n_embd * 4 + 24 * q6k_bytes(n_ff, n_embd) + 3 * n_embd * 4
     out["moe_layer"] = {"us_per_token": ms / steps * 1e3, "tok_s": steps / (ms * 1e-3),
                         "bytes_per_token": by, "gbs": by / (ms / steps * 1e-3) / 1e9,
-                        "routing": "bit-exact (sequential router fold every call)"}
+                        "routing": "bit-exact (sequential router fold every call)",
+                        "routing_margin": moe_margin(layers)}
     if moe_cpu_seconds > 0:
         # the reference's CPU layer (the oracle, 1 thread) on a bounded sample
         from oracle import oracle as O
