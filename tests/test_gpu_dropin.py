@@ -689,3 +689,47 @@ def test_backend_ops_exact(gpu):
     assert "outside" in err()
     assert L().llamd_fwd_free_mem() > 0
     assert L().llamd_batch_max_seq() == 16
+
+
+def test_host_calls_from_several_threads(gpu):
+    """Host-in/host-out calls from 6 threads at once (ctypes drops the GIL, so
+    they overlap in the library): raw ggml uploads, two threads sharing one
+    pointer's first use (one tiled copy is made), every result the oracle's
+    bits, on every repetition."""
+    import threading
+    shapes = [(768, 8), (2048, 3), (100, 3)]
+    ws = [H.weights(r, b, 900 + r + b) for r, b in shapes]
+    ptrs = [L().llamd_rocm_upload(w.ctypes.data, w.nbytes) for w in ws]
+    assert all(ptrs), err()
+    work = [0, 1, 2, 0, 1, 2]  # threads 3-5 share their pointer with 0-2
+    wants, inputs = [], []
+    for t, i in enumerate(work):
+        rows, blocks = shapes[i]
+        qa, q, d = acts(1, blocks, 70 + t)
+        inputs.append((q, d))
+        wants.append(O.matvec_q6k_act(ws[i], rows, blocks * QK_K, qa[0]))
+    failures = []
+
+    def run(t):
+        i = work[t]
+        rows, blocks = shapes[i]
+        q, d = inputs[t]
+        y = np.empty(rows, np.float32)
+        for rep in range(20):
+            rc = L().llamd_rocm_matvec_q6k_resident(ptrs[i], q.ctypes.data, d.ctypes.data,
+                                                     y.ctypes.data, blocks, rows)
+            if rc != 0 or not bits_equal(y, wants[t]):
+                failures.append((t, rep, rc))
+                return
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(len(work))]
+    try:
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(timeout=60)
+        assert not any(th.is_alive() for th in threads)
+        assert not failures, failures
+    finally:
+        for p in ptrs:
+            L().llamd_rocm_release(p)
