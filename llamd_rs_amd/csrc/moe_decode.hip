@@ -133,9 +133,27 @@ __device__ void wait_logits(const DecodeParams &p, float l[RW], bool &late) {
     late = late || __any(lt);
 }
 
-// The routed experts, by one whole wave, into rsh.sorted[0..n_used): from the
-// estimates when they certify the exact top-k set, else by exact routing.
-// Returns whether the estimate was used.
+// Slot order: the n_used routed experts sit in rsh.sorted[0..n_used) by
+// ascending expert index, whichever way they were chosen. Every gate/up
+// workgroup and the down launch then agree on which act row holds which
+// expert even if one workgroup had to route exactly (a wait that gave up)
+// while the others used the certified estimate: the two give the same set.
+// By one whole wave; `id` holds the set on lanes < n_used.
+__device__ void slots_by_index(int id, int n_used, int *sorted) {
+    const int lane = threadIdx.x & 63;
+    int rank = 0;
+    for (int q = 0; q < n_used; ++q) {
+        const int other = __shfl(id, q, WAVE);
+        rank += (q != lane && other < id) ? 1 : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane < n_used) sorted[rank] = id;
+}
+
+// The routed experts, by one whole wave, into rsh.sorted[0..n_used) (slot
+// order above): from the estimates when they certify the exact top-k set,
+// else by exact routing. Returns whether the estimate was used.
 __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed_out) {
     const int lane = threadIdx.x & 63;
     double T[RW], E[RW];
@@ -178,10 +196,23 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     // lies 80 or more below the maximum, so none underflows to a tie at 0.
     const double mag = fmax(fabs(top), fabs(lo));
     const bool certain = !late && fin && (lo - hi > 0x1p-20 * (1.0 + mag)) && (lo > top - 80.0);
-    if (!certain) {
+    if (certain) {
+        // the chosen set (the lane's `taken` bits) in index order: column j
+        // holds experts 64 j + lane
+        int before = 0;
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const unsigned long long m = __ballot((taken >> j) & 1u);
+            if ((m >> lane) & 1ull) rsh.sorted[before + __popcll(m & ((1ull << lane) - 1ull))] = lane + WAVE * j;
+            before += __popcll(m);
+        }
+    } else {
         float l[RW];
         wait_logits(p, l, timed_out);
         route_finish(l, p.n_expert, p.n_used, true, rsh, nullptr, nullptr, nullptr);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        slots_by_index(lane < p.n_used ? rsh.sorted[lane] : 0x7FFFFFFF, p.n_used, rsh.sorted);
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
