@@ -111,7 +111,7 @@ __device__ void wait_logits(const DecodeParams &p, float l[RW], bool &late) {
     unsigned long long vs[RW];
 #pragma unroll
     for (int j = 0; j < RW; ++j) live[j] = lane + WAVE * j < p.n_expert;
-    slots_wait(p.slots + p.n_expert, live, vs, p.polls);
+    slots_wait(p.slots + p.n_expert, live, vs, p.polls, p.n_expert - 1);
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         const int i = lane + WAVE * j;
@@ -151,6 +151,40 @@ __device__ void slots_by_index(int id, int n_used, int *sorted) {
     if (lane < n_used) sorted[rank] = id;
 }
 
+// The candidate set for the certification in select_experts: n_used rounds
+// of a wave-wide max on a composite key, the order-preserving key of the
+// estimate with its low 8 bits replaced by 255 - index. The keys are
+// distinct, so the max names its expert directly (no ballot search for the
+// lowest index holding it), which halves each round's dependent chain. Any
+// choice among estimates that differ only in those low bits is as good as
+// another: the certification accepts a set only if every member's interval
+// lies above every other expert's, which the exact top-k set alone
+// satisfies. Bit j of the result: expert lane + 64 j is chosen.
+__device__ unsigned estimate_topk(const float T[RW], const bool live[RW], int n_used) {
+    const int lane = threadIdx.x & 63;
+    unsigned ck[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j)
+        ck[j] = live[j] ? ((sort_key(T[j]) & ~0xFFu) | (255u - (unsigned)(lane + WAVE * j))) : 0u;
+    unsigned taken = 0;
+    for (int r = 0; r < n_used; ++r) {
+        unsigned b = 0u;
+#pragma unroll
+        for (int j = 0; j < RW; ++j) b = max(b, ck[j]);
+        const unsigned m = (unsigned)wave_reduce((int)b, 0, [](int x, int y) {
+            return (int)max((unsigned)x, (unsigned)y);
+        });
+        if (m == 0u) break;
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+            if (ck[j] == m) {
+                taken |= 1u << j;
+                ck[j] = 0u;
+            }
+    }
+    return taken;
+}
+
 // The routed experts, by one whole wave, into rsh.sorted[0..n_used) (slot
 // order above): from the estimates when they certify the exact top-k set,
 // else by exact routing. Returns whether the estimate was used.
@@ -162,7 +196,7 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     unsigned long long vs[RW];
 #pragma unroll
     for (int j = 0; j < RW; ++j) live[j] = lane + WAVE * j < p.n_expert;
-    slots_wait(p.slots, live, vs, p.polls);
+    slots_wait(p.slots, live, vs, p.polls, p.n_expert - 1);
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         const unsigned long long v = vs[j];
@@ -173,29 +207,37 @@ __device__ bool select_experts(const DecodeParams &p, RouteLds &rsh, bool &timed
     }
     const bool late = __any(lt);
     timed_out = timed_out || late;
-    unsigned taken = 0;
-    wave_select(key, live, p.n_used, taken, rsh.sorted);
-    // lo = min chosen (T - E), hi = max other (T + E), top = max (T + E)
-    double lo = INFINITY, hi = -INFINITY, top = -INFINITY;
+    const unsigned taken = estimate_topk(key, live, p.n_used);
+    // lo = min chosen (T - E), hi = max other (T + E), top = max (T + E):
+    // each formed in double and rounded outward to float, so the 32-bit
+    // reductions keep the test below conservative
+    float lo = INFINITY, hi = -INFINITY, top = -INFINITY;
     bool fin = true;
+    int n_taken = 0;
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         if (!live[j]) continue;
         fin = fin && isfinite(T[j]) && isfinite(E[j]);
-        top = fmax(top, T[j] + E[j]);
-        if (taken & (1u << j)) lo = fmin(lo, T[j] - E[j]);
-        else hi = fmax(hi, T[j] + E[j]);
+        const float up = __double2float_ru(T[j] + E[j]);
+        top = fmaxf(top, up);
+        if (taken & (1u << j)) {
+            lo = fminf(lo, __double2float_rd(T[j] - E[j]));
+            ++n_taken;
+        } else {
+            hi = fmaxf(hi, up);
+        }
     }
-    lo = wave_reduce(lo, (double)INFINITY, [](double a, double b) { return fmin(a, b); });
-    hi = wave_reduce(hi, -(double)INFINITY, [](double a, double b) { return fmax(a, b); });
-    top = wave_reduce(top, -(double)INFINITY, [](double a, double b) { return fmax(a, b); });
-    fin = __all(fin);
+    lo = wave_reduce(lo, INFINITY, [](float a, float b) { return fminf(a, b); });
+    hi = wave_reduce(hi, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    top = wave_reduce(top, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    fin = __all(fin) && wave_reduce(n_taken, 0, [](int a, int b) { return a + b; }) == p.n_used;
     // The chosen logits exceed the others by more than 2^-20 (1 + max |logit|):
     // after l - max, expf and the division by the total every chosen
     // probability stays strictly above every other one. And no chosen logit
     // lies 80 or more below the maximum, so none underflows to a tie at 0.
-    const double mag = fmax(fabs(top), fabs(lo));
-    const bool certain = !late && fin && (lo - hi > 0x1p-20 * (1.0 + mag)) && (lo > top - 80.0);
+    const double dlo = lo, dhi = hi, dtop = top;
+    const double mag = fmax(fabs(dtop), fabs(dlo));
+    const bool certain = !late && fin && (dlo - dhi > 0x1p-20 * (1.0 + mag)) && (dlo > dtop - 80.0);
     if (certain) {
         // the chosen set (the lane's `taken` bits) in index order: column j
         // holds experts 64 j + lane

@@ -296,11 +296,28 @@ __device__ __forceinline__ void slot_store(unsigned long long *slot, unsigned lo
 // not promise dispatch order, so every caller must survive a slot left
 // SLOT_EMPTY: the MoE decode kernel then computes the value it waited for
 // itself (wait_logits), the same bits.
+//
+// While the producers are still at work, one lane watches one slot (the
+// last one, `watch`, normally among the last filled) and the others wait:
+// hundreds of waiting workgroups polling every slot would put tens of
+// thousands of uncached loads per microsecond on the few lines that hold the
+// slots. The passes spent watching count against `polls`.
 __device__ __forceinline__ void slots_wait(const unsigned long long *base, const bool live[RW],
-                                           unsigned long long v[RW], int polls) {
+                                           unsigned long long v[RW], int polls, int watch = -1) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < RW; ++j) v[j] = live[j] ? SLOT_EMPTY : 0ull;
+    if (watch >= 0) {
+        int used = 0;
+        if (lane == 0) {
+            while (used < polls &&
+                   __hip_atomic_load(base + watch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == SLOT_EMPTY) {
+                ++used;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        polls -= __shfl(used, 0, WAVE);
+    }
     for (int it = 0; it < polls; ++it) {
 #pragma unroll
         for (int j = 0; j < RW; ++j)
