@@ -102,6 +102,32 @@ def test_moe_layer_bit_identical(gpu, qwen_layer):
     assert calls - calls0 == 8 and exact_calls == calls
 
 
+def test_moe_layer_sweep_certified_path(gpu, qwen_layer):
+    """48 more calls over input scales from 1e-3 to 1e3: every call's logits,
+    ids, weights and output are the CPU path's bits, and the calls that
+    started gate/up on the certified estimate (the composite-key top-k and
+    its outward-rounded bounds) are counted."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    c0, _ = layer.counters()
+    for t in range(48):
+        scale = np.float32(10.0 ** (t % 7 - 3))
+        x = synth.normal(5000 + t, 1.0, n_embd) * scale
+        res = synth.normal(6000 + t, 1.0, n_embd)
+        want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+        out, r, lg_used = layer.forward(x, res)
+        assert bits_equal(lg_used, lg), t
+        assert list(r.experts) == list(ids), t
+        assert bits_equal(r.weights, w), t
+        assert bits_equal(out, want), t
+    c1, est = layer.counters()
+    assert c1[0] - c0[0] == 48
+    # the estimate certifies unless the chosen logits spread over 80 or more
+    # (probabilities that could underflow to a tie): scales 1e2 and 1e3 do
+    assert c1[2] - c0[2] >= 30, (c1, c0)
+    assert c1[3] == 0                       # no wait gave up
+
+
 def test_moe_layer_without_residual(gpu, qwen_layer):
     from llamd_rs_amd import synth
     layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
