@@ -481,10 +481,32 @@ def test_decode_waits_that_give_up_still_route_exactly(gpu, qwen_layer):
     assert lib().llamd_hip_tune(b"moe_polls", prev) == prev
 
 
+@pytest.mark.parametrize("polls", [2, 6, 20])
+def test_decode_some_waits_give_up(gpu, qwen_layer, polls):
+    """A small bound on every wait makes some workgroups give up (and route
+    on the exact logits, computing those not yet published) while others,
+    placed later, still find the estimates and use the certified set: the
+    slots hold the set in expert-index order either way, so every act row
+    belongs to one expert and the results stay the CPU's bits."""
+    from llamd_rs_amd import synth
+    layer, (router, gate, up, down, n_embd, n_ff, n_expert, n_used) = qwen_layer
+    prev = lib().llamd_hip_tune(b"moe_polls", polls)
+    try:
+        for t in range(6):
+            x = synth.normal(6300 + 10 * polls + t, 1.0, n_embd)
+            res = synth.normal(6400 + t, 1.0, n_embd)
+            want, lg, ids, w = O.moe_layer(x, res, n_embd, n_ff, n_expert, n_used, router, gate, up, down)
+            out, r, lgd = layer.forward(x, res)
+            assert bits_equal(lgd, lg) and list(r.experts) == list(ids), t
+            assert bits_equal(r.weights, w) and bits_equal(out, want), t
+    finally:
+        lib().llamd_hip_tune(b"moe_polls", prev)
+
+
 def test_lm_head_b1_repeats_and_all_nan(gpu):
-    """The b = 1 call quantizes x inside the matvec launch: calls in a row on
-    changing inputs each get their own logits and answer, and a vocabulary of
-    NaN logits gives 0 as the reference's scan does."""
+    """The b = 1 call (quantize, matvec with per-tile candidates, arg-max):
+    calls in a row on changing inputs each get their own logits and answer,
+    and a vocabulary of NaN logits gives 0 as the reference's scan does."""
     rows, k = 4000, 512
     w = H.weights(rows, 2, 23)
     dw = gpu.DeviceWeights.upload(w, rows, 2)
