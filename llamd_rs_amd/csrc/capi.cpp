@@ -1031,7 +1031,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
         bool ok = m->p_xq.alloc((size_t)chunks * m->be * CHUNK_BLOCK) &&
                   m->p_xd.alloc((size_t)chunks * m->be * CHUNK * 4) &&
                   m->p_grp_e.alloc(m->n_expert * 4) && m->p_grp_s.alloc(m->n_expert * 4) &&
-                  m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc(2 * (m->n_expert + 1) * 4) &&
+                  m->p_grp_c.alloc(m->n_expert * 4) && m->p_sub.alloc((group_items_offset(m->n_expert) + 2 * (size_t)chunks * 8) * 4) &&
                   m->p_slot.alloc(NP * 4) && m->p_idx.alloc(NP * 4) &&
                   m->p_g.alloc(NP * m->n_ff * 4) && m->p_u.alloc(NP * m->n_ff * 4) &&
                   m->p_aq.alloc((size_t)chunks * m->bf * CHUNK_BLOCK) &&
@@ -1046,7 +1046,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
     rc |= launch_moe_group(d_ids, np, m->n_used, m->n_expert, m->p_grp_e.as<int32_t>(),
                            m->p_grp_s.as<int32_t>(), m->p_grp_c.as<int32_t>(),
                            m->p_sub.as<int32_t>(), m->p_slot.as<int32_t>(), m->p_idx.as<int32_t>(),
-                           st);
+                           st, max_chunks);
     // Q8_K of every token, written to the chunk slot of each of its n_used pairs
     rc |= launch_q8k_quantize_chunks(d_x, n_tok, m->be, m->p_slot.as<int32_t>(), m->n_used,
                                      m->p_xq.as<int8_t>(), m->p_xd.as<float>(), st);
@@ -1054,11 +1054,13 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
     rc |= launch_q6k_mv_batched(m->gate, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
-                                m->p_g.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st);
+                                m->p_g.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st,
+                                nullptr, nullptr, true);
     rc |= launch_q6k_mv_batched(m->upw, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
-                                m->p_u.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st);
+                                m->p_u.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st,
+                                nullptr, nullptr, true);
     // SwiGLU + Q8_K per pair, into the pair's chunk slot
     rc |= launch_swiglu_q8k_chunks(m->p_g.as<float>(), m->p_u.as<float>(), np, m->bf,
                                    m->p_slot.as<int32_t>(), m->p_aq.as<int8_t>(),
@@ -1068,7 +1070,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_aq.as<int8_t>(), m->p_ad.as<float>(),
                                 m->p_dn.as<float>(), m->n_embd, m->n_embd, m->bf, m->n_expert,
-                                max_chunks, st);
+                                max_chunks, st, nullptr, nullptr, true);
     rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, d_res, d_out, m->n_used, m->n_embd, n_tok, st,
                              m->p_slot.as<int32_t>());
     return rc ? fail("moe_prefill: launch failed") : 0;

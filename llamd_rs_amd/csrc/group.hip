@@ -18,6 +18,10 @@
 //   one expert, the work items of the twin batched kernel), slot_of_pair[p] = the chunk slot of pair p
 //   (chunk sub_start[e] + j / 16, token j % 16 for the j-th pair of expert
 //   e), pair_idx[i] = the pair index t * n_used + k at sorted position i.
+// With max_chunks > 0, sub_start continues with a record per chunk,
+// sub_info[max_chunks], then one per twin, twin_info[max_chunks] (GroupItem,
+// launch.hpp): a wave of the batched kernels reads its work item in one load
+// instead of a binary search of dependent loads and the group's fields.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -30,12 +34,13 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
                                                   int n_expert, int32_t *grp_expert,
                                                   int32_t *grp_start, int32_t *grp_count,
                                                   int32_t *sub_start, int32_t *slot_of_pair,
-                                                  int32_t *pair_idx) {
+                                                  int32_t *pair_idx, int max_chunks) {
     __shared__ int sub_lds[GROUP_MAX_EXPERTS];
     __shared__ int start_lds[GROUP_MAX_EXPERTS];
     (void)n_used;
     __shared__ int hist[GROUP_MAX_EXPERTS];
     __shared__ int cursor[GROUP_MAX_EXPERTS];
+    __shared__ int totals[2];  // chunks, twins
     const int tid = threadIdx.x;
     for (int e = tid; e < n_expert; e += blockDim.x) hist[e] = 0;
     __syncthreads();
@@ -77,9 +82,29 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
         if (tid == n_expert - 1) {
             sub_start[n_expert] = sub + ch;
             sub_start[2 * n_expert + 1] = tst + tw;
+            totals[0] = sub + ch;
+            totals[1] = tst + tw;
+        }
+        if (max_chunks > 0) {
+            GroupItem *sub_info = (GroupItem *)(sub_start + group_items_offset(n_expert));
+            GroupItem *twin_info = sub_info + max_chunks;
+            for (int j = 0; j < ch; ++j)
+                sub_info[sub + j] = GroupItem{tid, j, sub + j, c, start, 0, 0, 0};
+            for (int j = 0; j < tw; ++j)
+                twin_info[tst + j] = GroupItem{tid, 2 * j, sub + 2 * j, c, start, 2 * j + 1 < ch, 0, 0};
         }
     }
     __syncthreads();
+    if (max_chunks > 0) {
+        // the records past the last chunk / twin: no work (expert -1), so a
+        // wave of the grid's spare items needs no other load to know it
+        GroupItem *sub_info = (GroupItem *)(sub_start + group_items_offset(n_expert));
+        GroupItem *twin_info = sub_info + max_chunks;
+        for (int i = totals[0] + tid; i < max_chunks; i += blockDim.x)
+            sub_info[i] = GroupItem{-1, 0, 0, 0, 0, 0, 0, 0};
+        for (int i = totals[1] + tid; i < max_chunks; i += blockDim.x)
+            twin_info[i] = GroupItem{-1, 0, 0, 0, 0, 0, 0, 0};
+    }
     for (int p = tid; p < n_pairs; p += blockDim.x) {
         const int e = ids[p];
         if ((unsigned)e >= (unsigned)n_expert) {
@@ -98,10 +123,11 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
 int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
                      int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
                      int32_t *sub_start, int32_t *slot_of_pair, int32_t *pair_idx,
-                     hipStream_t st) {
-    if (n_expert > GROUP_MAX_EXPERTS || n_expert <= 0) return -1;
+                     hipStream_t st, int max_chunks) {
+    if (n_expert > GROUP_MAX_EXPERTS || n_expert <= 0 || max_chunks < 0) return -1;
     hipLaunchKernelGGL(moe_group, dim3(1), dim3(1024), 0, st, ids, n_pairs, n_used, n_expert,
-                       grp_expert, grp_start, grp_count, sub_start, slot_of_pair, pair_idx);
+                       grp_expert, grp_start, grp_count, sub_start, slot_of_pair, pair_idx,
+                       max_chunks);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

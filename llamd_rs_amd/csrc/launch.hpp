@@ -103,7 +103,9 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v = nullptr,
-                          int *amax_i = nullptr);
+                          int *amax_i = nullptr, bool group_tables = false);
+// group_tables: sub_start carries launch_moe_group's sub_info / twin_info
+// records (written with the same max_chunks).
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 
 // q8k.hip
@@ -119,13 +121,29 @@ int launch_swiglu_q8k_chunks(const float *gate, const float *up, int rows, int b
                              const int32_t *slot_of, int8_t *cq, float *cd, hipStream_t st);
 // moe grouping (group.hip): counting sort of the (token, k) pairs by expert.
 // Outputs grp_* per expert, sub_start (prefix of ceil(count/16), then the
-// twin prefix of ceil(chunks/2): 2 * (n_expert + 1) entries), for each
+// twin prefix of ceil(chunks/2): 2 * (n_expert + 1) entries; with
+// max_chunks > 0 then a GroupItem per chunk and per twin, from
+// group_items_offset(n_expert), 2 * max_chunks records), for each
 // pair p = token * n_used + k its chunk slot slot_of_pair[p], and for each
 // sorted position its pair index pair_idx.
+// One work item of the expert-grouped batched kernels: a 16-token chunk, or a
+// twin (two consecutive chunks of one expert), with its group's fields.
+struct __attribute__((aligned(32))) GroupItem {
+    int32_t expert;  // = its group
+    int32_t st;      // first chunk's index within the group
+    int32_t sub;     // first chunk's global index (its activation chunk)
+    int32_t count;   // pairs in the group
+    int32_t start;   // the group's first sorted pair
+    int32_t twin2;   // twins: 1 when the second chunk exists
+    int32_t pad0, pad1;
+};
+// The records start at this int32 offset of sub_start (32-byte aligned
+// when sub_start is).
+constexpr size_t group_items_offset(int n_expert) { return ((2 * (size_t)(n_expert + 1)) + 7) & ~(size_t)7; }
 int launch_moe_group(const int32_t *ids, int n_pairs, int n_used, int n_expert,
                      int32_t *grp_expert, int32_t *grp_start, int32_t *grp_count,
                      int32_t *sub_start, int32_t *slot_of_pair, int32_t *pair_idx,
-                     hipStream_t st);
+                     hipStream_t st, int max_chunks = 0);
 int launch_silu_mul(const float *gate, const float *up, float *out, int n, hipStream_t st);
 
 // norm.hip: CpuBackend::rms_norm (+ weight), bit-exact. rows of n; the

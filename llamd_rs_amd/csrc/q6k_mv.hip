@@ -498,6 +498,8 @@ struct BatchParams {
     int *amax_i;                 //   [token][tiles] (single group only)
     int ldy, rows, tiles, blocks, n_groups;
     int single_count;            // grp_expert == nullptr: one group, expert 0, this many tokens
+    const GroupItem *sub_info;   // optional: each chunk's / twin's record
+    const GroupItem *twin_info;  //   (launch_moe_group), else a binary search
 };
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -709,16 +711,25 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
     if (p.grp_expert) {
         // find the group whose chunk range holds `sub` (sub_start has
         // n_groups + 1 entries)
-        if (sub >= p.sub_start[p.n_groups]) return;
-        int lo = 0, hi = p.n_groups;
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (p.sub_start[mid] <= sub) lo = mid; else hi = mid;
+        if (p.sub_info) {
+            const GroupItem it = p.sub_info[sub];  // expert -1: a spare item
+            if (it.expert < 0) return;
+            st = it.st;
+            cnt = it.count;
+            start = it.start;
+            expert = it.expert;
+        } else {
+            if (sub >= p.sub_start[p.n_groups]) return;
+            int lo = 0, hi = p.n_groups;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (p.sub_start[mid] <= sub) lo = mid; else hi = mid;
+            }
+            st = sub - p.sub_start[lo];
+            cnt = p.grp_count[lo];
+            start = p.grp_start[lo];
+            expert = p.grp_expert[lo];
         }
-        st = sub - p.sub_start[lo];
-        cnt = p.grp_count[lo];
-        start = p.grp_start[lo];
-        expert = p.grp_expert[lo];
     } else {
         cnt = p.single_count;
         if (sub >= (cnt + 15) / 16) return;
@@ -740,16 +751,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int t = item % p.tiles;
     const int tw = item / p.tiles;
     const int32_t *twin_start = p.sub_start + p.n_groups + 1;
-    if (tw >= twin_start[p.n_groups]) return;
-    int lo = 0, hi = p.n_groups;
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (twin_start[mid] <= tw) lo = mid; else hi = mid;
+    int st, sub, cnt, start, expert;
+    bool two;
+    if (p.twin_info) {
+        const GroupItem it = p.twin_info[tw];  // expert -1: a spare item
+        if (it.expert < 0) return;
+        st = it.st;
+        sub = it.sub;
+        cnt = it.count;
+        start = it.start;
+        expert = it.expert;
+        two = it.twin2 != 0;
+    } else {
+        if (tw >= twin_start[p.n_groups]) return;
+        int lo = 0, hi = p.n_groups;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (twin_start[mid] <= tw) lo = mid; else hi = mid;
+        }
+        st = 2 * (tw - twin_start[lo]);
+        sub = p.sub_start[lo] + st;
+        cnt = p.grp_count[lo];
+        start = p.grp_start[lo];
+        expert = p.grp_expert[lo];
+        two = sub + 1 < p.sub_start[lo + 1];
     }
-    const int st = 2 * (tw - twin_start[lo]);
-    const int sub = p.sub_start[lo] + st;
-    const int cnt = p.grp_count[lo], start = p.grp_start[lo], expert = p.grp_expert[lo];
-    if (sub + 1 < p.sub_start[lo + 1])
+    if (two)
         batched_tile<2>(p, lane, t, sub, st, cnt, start, expert);
     else
         batched_tile<1>(p, lane, t, sub, st, cnt, start, expert);
@@ -920,9 +947,14 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v,
-                          int *amax_i) {
+                          int *amax_i, bool group_tables) {
     if (amax_v && grp_expert) return -1;
+    // every item of the grids below indexes a record below max_chunks when
+    // max_chunks >= n_groups (twins: ceil((max_chunks + n_groups) / 2) items)
+    if (group_tables && (!grp_expert || max_chunks < n_groups || max_chunks <= 0)) return -1;
     BatchParams p;
+    p.sub_info = group_tables ? (const GroupItem *)(sub_start + group_items_offset(n_groups)) : nullptr;
+    p.twin_info = group_tables ? p.sub_info + max_chunks : nullptr;
     p.single_count = n_groups;  // only read when grp_expert == nullptr
     p.w = (const uint8_t *)w;
     p.expert_stride = expert_stride;
