@@ -60,6 +60,17 @@ int fail(const char *fmt, ...) {
 
 void llamd::fwd_refused() { g_fwd_refused = true; }
 
+namespace {
+// A void launcher's launch: a refusal (the launcher's -1) or a failed launch
+// is recorded for llamd_fwd_last_error, with the reason.
+void checked(int rc, const char *what) {
+    if (rc) {
+        fail("%s: arguments refused or launch failed", what);
+        llamd::fwd_refused();
+    }
+}
+}  // namespace
+
 // The error text of the calling thread, for the other host files of the
 // library (errors.hpp).
 int llamd::set_error(const char *fmt, ...) {
@@ -639,7 +650,8 @@ void llamd_fwd_matvec_grouped(const void *d_w, const int32_t *d_ids, const int8_
     size_t stride = 0;
     int ne = 0;
     if (n_used <= 0 || expert_view(d_w, rows, blocks, &stride, &ne, &d_w)) return fwd_refused();
-    launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 0, stream());
+    checked(launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 0, stream()),
+            "matvec_grouped");
 }
 
 void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const int8_t *d_aq,
@@ -648,15 +660,16 @@ void llamd_fwd_matvec_grouped_pa(const void *d_w, const int32_t *d_ids, const in
     size_t stride = 0;
     int ne = 0;
     if (n_used <= 0 || expert_view(d_w, rows, blocks, &stride, &ne, &d_w)) return fwd_refused();
-    launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 1, stream());
+    checked(launch_q6k_mv_b1(d_w, stride, d_ids, d_aq, d_ad, d_out, rows, blocks, n_used, 1, stream()),
+            "matvec_grouped_pa");
 }
 
 void llamd_fwd_quantize(const float *d_x, int8_t *d_qs, float *d_d, int nblocks) {
-    quantize_dev(d_x, d_qs, d_d, nullptr, nblocks);
+    checked(quantize_dev(d_x, d_qs, d_d, nullptr, nblocks), "quantize");
 }
 
 void llamd_fwd_silu_mul(const float *gate, const float *upv, float *out, int n) {
-    launch_silu_mul(gate, upv, out, n, stream());
+    checked(launch_silu_mul(gate, upv, out, n, stream()), "silu_mul");
 }
 
 void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *ids,
@@ -665,7 +678,7 @@ void llamd_fwd_router(const float *logits, int n_expert, int n_used, int32_t *id
         fail("router: n_expert %d, n_used %d", n_expert, n_used);
         return fwd_refused();
     }
-    launch_route_logits(logits, n_expert, n_used, ids, weights, stream(), 1, probs);
+    checked(launch_route_logits(logits, n_expert, n_used, ids, weights, stream(), 1, probs), "router");
 }
 
 void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
@@ -679,7 +692,7 @@ void llamd_fwd_matvec_x3(const void *w0, const void *w1, const void *w2, const i
         if (resolve_q6k(w[i], nullptr, rows[i], blocks, false, &v)) return fwd_refused();
         w[i] = v.tiled;
     }
-    launch_q6k_mv_x3(w, y, rows, 3, d_aq, d_ad, blocks, stream());
+    checked(launch_q6k_mv_x3(w, y, rows, 3, d_aq, d_ad, blocks, stream()), "matvec_x3");
 }
 
 void llamd_fwd_matvec_x3_splitk(const void *w0, const void *w1, const void *w2, const int8_t *d_aq,
@@ -701,7 +714,8 @@ void llamd_fwd_matvec_grouped_x2(const void *wa, const void *wb, const int32_t *
         fail("matvec_grouped_x2: the two expert tensors differ in shape");
         return fwd_refused();
     }
-    launch_q6k_mv_grouped_x2(wa, wb, sa, d_ids, d_aq, d_ad, oa, ob, rows, blocks, n_used, stream());
+    checked(launch_q6k_mv_grouped_x2(wa, wb, sa, d_ids, d_aq, d_ad, oa, ob, rows, blocks, n_used, stream()),
+            "matvec_grouped_x2");
 }
 
 void llamd_fwd_matvec_grouped_x2_splitk(const void *wa, const void *wb, const int32_t *d_ids,
@@ -719,44 +733,52 @@ void llamd_fwd_matvec_grouped_pa_splitk(const void *d_w, const int32_t *d_ids, c
 }
 
 void llamd_fwd_rms_norm_mul(const float *x, const float *w, float *out, int n, float eps) {
-    if (launch_rms_norm_mul(x, w, out, 1, n, n, eps, stream()))
+    if (launch_rms_norm_mul(x, w, out, 1, n, n, eps, stream())) {
         fail("rms_norm_mul: n must be in 1..8192");
+        fwd_refused();
+    }
 }
 
 void llamd_fwd_head_rms_norm_mul(const float *x, const float *w, float *out, int n_head, int hd,
                                  float eps) {
-    if (launch_rms_norm_mul(x, w, out, n_head, hd, hd, eps, stream()))
+    if (launch_rms_norm_mul(x, w, out, n_head, hd, hd, eps, stream())) {
         fail("head_rms_norm_mul: need n_head > 0 and hd in 1..8192");
+        fwd_refused();
+    }
 }
 
 void llamd_fwd_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
                               float *inv_scratch, int n, float eps) {
-    if (launch_rms_norm_quant(x, w, out, qs, d, inv_scratch, n, eps, stream()))
+    if (launch_rms_norm_quant(x, w, out, qs, d, inv_scratch, n, eps, stream())) {
         fail("rms_norm_quant: n must be a multiple of 256, at most 8192");
+        fwd_refused();
+    }
 }
 
 void llamd_fwd_moe_combine(const float *d, const float *weights, float *out, int n_used,
                            int n_embd) {
-    launch_moe_combine(d, weights, nullptr, out, n_used, n_embd, 1, stream());
+    checked(launch_moe_combine(d, weights, nullptr, out, n_used, n_embd, 1, stream()),
+            "moe_combine (n_used 1..16)");
 }
 
 void llamd_fwd_moe_combine_add(const float *d, const float *weights, const float *residual,
                                float *out, int n_used, int n_embd) {
-    launch_moe_combine(d, weights, residual, out, n_used, n_embd, 1, stream());
+    checked(launch_moe_combine(d, weights, residual, out, n_used, n_embd, 1, stream()),
+            "moe_combine_add (n_used 1..16)");
 }
 
 void llamd_fwd_argmax(const float *x, int n, float *scratch_v, int32_t *scratch_i, int32_t *out,
                       int nblocks) {
     (void)nblocks;  // partial count is chosen from n (argmax_parts); scratch must hold it
-    launch_argmax(x, n, n, 1, scratch_v, (int *)scratch_i, out, stream());
+    checked(launch_argmax(x, n, n, 1, scratch_v, (int *)scratch_i, out, stream()), "argmax");
 }
 
 void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int rows) {
-    launch_f32_mv(w, x, out, rows, k, stream());
+    checked(launch_f32_mv(w, x, out, rows, k, stream()), "matvec_f32");
 }
 
 void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, int rows, int k) {
-    launch_q8_0_mv(d_w, d_x, d_out, rows, k, stream());
+    checked(launch_q8_0_mv(d_w, d_x, d_out, rows, k, stream()), "matvec_q8_0");
 }
 
 }  // extern "C"

@@ -115,13 +115,26 @@ __global__ void moe_combine(const float *down, const float *weights, const float
     if (skip) skip += tok * n_used;
     if (res) res += tok * n_embd;
     out += tok * n_embd;
-    float acc = 0.0f;
-    for (int e = 0; e < n_used; ++e) {
-        if (skip && skip[e] < 0) continue;
-        const float p = weights[e] * down[(size_t)e * n_embd + i];
-        acc = acc + p;
+    // every operand is loaded before the first add (a pair with no expert
+    // still has a row in `down`, unused), so the loads are one round trip
+    // instead of one per expert; the adds keep the routing order
+    constexpr int E = 16;  // n_used <= 16
+    float wv[E], dv[E];
+    bool live[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        live[e] = e < n_used && !(skip && skip[e] < 0);
+        wv[e] = e < n_used ? weights[e] : 0.0f;
+        dv[e] = e < n_used ? down[(size_t)e * n_embd + i] : 0.0f;
     }
-    out[i] = res ? res[i] + acc : acc;
+    const float r = res ? res[i] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float p = wv[e] * dv[e];
+        acc = live[e] ? acc + p : acc;
+    }
+    out[i] = res ? r + acc : acc;
 }
 
 // ---- 4. argmax: strict '>', lowest index wins (device_forward.rs:23-37) -----
@@ -286,6 +299,7 @@ int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *
 
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
                        int n_used, int n_embd, int n_tok, hipStream_t st, const int32_t *skip) {
+    if (n_used < 1 || n_used > 16) return -1;
     hipLaunchKernelGGL(moe_combine, dim3((n_embd + 255) / 256, n_tok), dim3(256), 0, st, down,
                        weights, res, out, n_used, n_embd, skip);
     return hipGetLastError() == hipSuccess ? 0 : -1;

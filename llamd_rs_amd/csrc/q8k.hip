@@ -43,12 +43,15 @@ __global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int r
     const int r = item / blocks, b = item - r * blocks;
     const float4 xv = *(const float4 *)(x + (size_t)item * QK_K + 4 * lane);
     const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    // lane k < fan holds the k-th slot, loaded beside x (one round trip,
+    // not one per slot)
+    const int my_slot = slot_of ? (lane < fan ? slot_of[(size_t)r * fan + lane] : -1) : r;
     int q[4];
     float dv;
     quantize_wave_q(v, lane, q, dv);
     const uint32_t dw = chunk_dword(q, lane);
     for (int k = 0; k < fan; ++k)
-        store_chunk(dw, dv, lane, cq, cd, slot_of ? slot_of[(size_t)r * fan + k] : r, b, blocks);
+        store_chunk(dw, dv, lane, cq, cd, slot_of ? __shfl(my_slot, k, WAVE) : r, b, blocks);
 }
 
 // act[i] = silu(gate[i]) * up[i], then Q8_K of act. Optionally stores act.
@@ -152,6 +155,7 @@ int launch_q8k_quantize(const float *x, int8_t *qs, float *d, int16_t *bsums, in
 int launch_q8k_quantize_chunks(const float *x, int rows, int blocks, const int32_t *slot_of,
                                int fan, int8_t *cq, float *cd, hipStream_t st) {
     if (rows <= 0 || blocks <= 0) return 0;
+    if (fan < 1 || fan > WAVE) return -1;
     hipLaunchKernelGGL(q8k_quantize_chunks, dim3((rows * blocks + 3) / 4), dim3(256), 0, st, x,
                        rows, blocks, slot_of, fan, cq, cd);
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -216,3 +216,30 @@ def test_measurement_helpers(gpu):
     assert L.llamd_fwd_sync() == 0
     src.close()
     dst.close()
+
+
+def test_void_launchers_report_refusals(gpu):
+    """The llamd_fwd_* launchers return nothing; one that refuses its
+    arguments queues nothing, and the next llamd_fwd_last_error says -1
+    once (the reference's wrappers check it after their synchronise)."""
+    from llamd_rs_amd._lib import lib, last_error
+    L = lib()
+    x = gpu.DeviceBuffer(4 * 8192)
+    out = gpu.DeviceBuffer(4 * 8192)
+    wts = gpu.DeviceBuffer(4 * 64)
+    assert L.llamd_fwd_sync() == 0 and L.llamd_fwd_last_error() == 0
+    cases = [
+        lambda: L.llamd_fwd_moe_combine(x.ptr, wts.ptr, out.ptr, 17, 256),     # n_used > 16
+        lambda: L.llamd_fwd_moe_combine_add(x.ptr, wts.ptr, x.ptr, out.ptr, 0, 256),
+        lambda: L.llamd_fwd_rms_norm_mul(x.ptr, x.ptr, out.ptr, 0, 1e-6),      # n = 0
+        lambda: L.llamd_fwd_rms_norm_quant(x.ptr, x.ptr, out.ptr, out.ptr, out.ptr, out.ptr, 100, 1e-6),
+    ]
+    try:
+        for i, call in enumerate(cases):
+            call()
+            assert L.llamd_fwd_sync() == 0, i
+            assert L.llamd_fwd_last_error() == -1, i
+            assert last_error(), i
+            assert L.llamd_fwd_last_error() == 0, i   # reported once
+    finally:
+        x.close(); out.close(); wts.close()
