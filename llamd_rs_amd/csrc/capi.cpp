@@ -1073,16 +1073,12 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
     rc |= launch_q8k_quantize_chunks(d_x, n_tok, m->be, m->p_slot.as<int32_t>(), m->n_used,
                                      m->p_xq.as<int8_t>(), m->p_xd.as<float>(), st);
     // gate / up: output row = the pair index
+    // gate and up in one launch (same shapes, same activations)
     rc |= launch_q6k_mv_batched(m->gate, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
                                 m->p_g.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st,
-                                nullptr, nullptr, true);
-    rc |= launch_q6k_mv_batched(m->upw, m->sgu, m->p_grp_e.as<int32_t>(), m->p_grp_s.as<int32_t>(),
-                                m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
-                                m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
-                                m->p_u.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st,
-                                nullptr, nullptr, true);
+                                nullptr, nullptr, true, m->upw, m->p_u.as<float>());
     // SwiGLU + Q8_K per pair, into the pair's chunk slot
     rc |= launch_swiglu_q8k_chunks(m->p_g.as<float>(), m->p_u.as<float>(), np, m->bf,
                                    m->p_slot.as<int32_t>(), m->p_aq.as<int8_t>(),

@@ -103,9 +103,11 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v = nullptr,
-                          int *amax_i = nullptr, bool group_tables = false);
+                          int *amax_i = nullptr, bool group_tables = false,
+                          const void *w2 = nullptr, float *y2 = nullptr);
 // group_tables: sub_start carries launch_moe_group's sub_info / twin_info
-// records (written with the same max_chunks).
+// records (written with the same max_chunks). w2 / y2: a second matrix of
+// the same shape on the same activations, in the same launch.
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 
 // q8k.hip

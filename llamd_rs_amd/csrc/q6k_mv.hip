@@ -500,7 +500,25 @@ struct BatchParams {
     int single_count;            // grp_expert == nullptr: one group, expert 0, this many tokens
     const GroupItem *sub_info;   // optional: each chunk's / twin's record
     const GroupItem *twin_info;  //   (launch_moe_group), else a binary search
+    // optional second matrix of the same shape on the same activations (gate
+    // and up in one launch): items from items_per_mat on use w2 / y2
+    const uint8_t *w2;
+    float *y2;
+    int items_per_mat;
 };
+
+// The work item of this wave and the parameters it runs with: the second
+// matrix's items are the first's, offset by items_per_mat.
+__device__ __forceinline__ int batch_item(const BatchParams &p, BatchParams &q) {
+    int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+    q = p;
+    if (p.w2 && item >= p.items_per_mat) {
+        item -= p.items_per_mat;
+        q.w = p.w2;
+        q.y = p.y2;
+    }
+    return item;
+}
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
@@ -702,9 +720,10 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
 // One wave per (group, 16-token chunk, 16-row tile). The chunk index is the
 // global sub-tile number, which is also where the activations of its 16
 // tokens sit in the token-chunked layout.
-__global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
+__global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams pk) {
     const int lane = threadIdx.x & 63;
-    const int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+    BatchParams p;
+    const int item = batch_item(pk, p);
     const int t = item % p.tiles;
     const int sub = item / p.tiles;
     int st = sub, cnt, start = 0, expert = 0;
@@ -745,9 +764,10 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams p) {
 // capped at 3 waves per SIMD (168 VGPRs, a few spilled), which measured 20%
 // faster than the uncapped 178 VGPRs at 2 waves and 5% faster than one chunk
 // per wave.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void q6k_mv_batched_twin(BatchParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void q6k_mv_batched_twin(BatchParams pk) {
     const int lane = threadIdx.x & 63;
-    const int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+    BatchParams p;
+    const int item = batch_item(pk, p);
     const int t = item % p.tiles;
     const int tw = item / p.tiles;
     const int32_t *twin_start = p.sub_start + p.n_groups + 1;
@@ -947,12 +967,15 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v,
-                          int *amax_i, bool group_tables) {
+                          int *amax_i, bool group_tables, const void *w2, float *y2) {
     if (amax_v && grp_expert) return -1;
     // every item of the grids below indexes a record below max_chunks when
     // max_chunks >= n_groups (twins: ceil((max_chunks + n_groups) / 2) items)
     if (group_tables && (!grp_expert || max_chunks < n_groups || max_chunks <= 0)) return -1;
     BatchParams p;
+    if (w2 && (!y2 || amax_v)) return -1;
+    p.w2 = (const uint8_t *)w2;
+    p.y2 = y2;
     p.sub_info = group_tables ? (const GroupItem *)(sub_start + group_items_offset(n_groups)) : nullptr;
     p.twin_info = group_tables ? p.sub_info + max_chunks : nullptr;
     p.single_count = n_groups;  // only read when grp_expert == nullptr
@@ -977,12 +1000,16 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
         // twins: sum of ceil(ch/2) <= (sum of ch + n_groups) / 2
         const long items = (long)p.tiles * ((max_chunks + n_groups + 1) / 2);
         if (items <= 0) return 0;
-        hipLaunchKernelGGL(q6k_mv_batched_twin, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);
+        p.items_per_mat = (int)items;
+        const long all = w2 ? 2 * items : items;
+        hipLaunchKernelGGL(q6k_mv_batched_twin, dim3((unsigned)((all + 3) / 4)), dim3(256), 0, st, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     const long items = (long)p.tiles * max_chunks;
     if (items <= 0) return 0;
-    hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, p);
+    p.items_per_mat = (int)items;
+    const long all = w2 ? 2 * items : items;
+    hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((all + 3) / 4)), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
