@@ -149,7 +149,7 @@ def main():
     EAGER_ONLY = args.eager
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no "
-              "multi-GPU path; see DESIGN.md for how the path would shard.", file=sys.stderr)
+              "multi-GPU path.", file=sys.stderr)
         sys.exit(2)
 
     from llamd_rs_amd import rocm, synth
