@@ -251,6 +251,35 @@ def test_lm_head_argmax_ties_and_nan(gpu, nseq, dot):          # device_forward.
         lib().llamd_hip_tune(b"mv_dot", 0)
 
 
+def test_lm_head_b1_argmax_keys_across_buckets_and_calls(gpu):
+    """b = 1 reduces the tiles' candidates through 64 atomically maxed keys
+    (tile t into key t % 64). A winner copied into a later tile of the same
+    key and of another key still resolves to the lowest row; all-negative
+    logits pick the least negative; and the keys start empty on every call
+    (a second call whose maximum is smaller than the first's)."""
+    rows, k = 130 * 16, 256                      # 130 tiles: keys hold 2-3 tiles
+    x = H.sample(k, 23)
+    w = H.weights(rows, 1, 29).reshape(rows, 210).copy()
+    logits = O.matvec_q6k(w.reshape(-1), rows, k, x)
+    m = int(np.argmax(logits))
+    t = m // 16
+    for dst_tile in (t + 64 if t + 64 < 130 else t - 64, (t + 1) % 130):
+        w[dst_tile * 16 + 5] = w[m]
+    neg = w.copy()
+    pos = O.matvec_q6k(w.reshape(-1), rows, k, x) > 0
+    neg[pos, 209] ^= 0x80                        # d's sign flipped: every logit <= 0 at x
+    for case, wc in (("copies", w), ("negative", neg)):
+        dw = gpu.DeviceWeights.upload(wc.reshape(-1), rows, 1)
+        head = gpu.LmHead(dw, max_seq=1)
+        for xs in (x, x * 0.25, -x):             # later calls with smaller maxima
+            got_logits, ids = head.forward(xs.reshape(1, k))
+            want = O.matvec_q6k(wc.reshape(-1), rows, k, xs)
+            assert bits_equal(got_logits[0], want), case
+            assert ids[0] == O.argmax(want), (case, ids[0], O.argmax(want))
+        head.close()
+        dw.close()
+
+
 def _lm_head_ties_and_nan(gpu, nseq):
     rows, k = 64, 256
     x = H.sample(nseq * k, 5).reshape(nseq, k)
