@@ -604,7 +604,6 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
         uint32_t scw;
         uint2 dw;
         float adb[NC];
-        long act[NC][8];
     };
     auto load = [&](Regs &r, int b) {
         const uint8_t *sg = seg + (size_t)b * SEG_BYTES;
@@ -616,12 +615,20 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
 #pragma unroll
         for (int u = 0; u < NC; ++u) {
             r.adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                r.act[u][c] = *(const long *)(aq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + 512 * c);
         }
     };
-    auto compute = [&](const Regs &r) {
+    // the class planes run BQ classes ahead of their MFMAs, across block
+    // boundaries (8 % BQ == 0, so a class keeps its ring slot); past the
+    // last block the loads re-read it, unused
+    constexpr int BQ = 2;
+    const int last = p.blocks - 1;
+    long act[BQ][NC];
+    auto aload = [&](int b, int c) {
+#pragma unroll
+        for (int u = 0; u < NC; ++u)
+            act[c % BQ][u] = *(const long *)(aq + u * chunk_q + (size_t)min(b, last) * CHUNK_BLOCK_BYTES + 512 * c);
+    };
+    auto compute = [&](const Regs &r, int b) {
         const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
         const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
         const FoldScales fs = fold_scales(r.scw);
@@ -644,9 +651,10 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
             fold_digits((uint64_t)unpack_codes(nib, hb, 0), fs, a_lo, a_hi);
 #pragma unroll
             for (int u = 0; u < NC; ++u) {
-                dh[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, r.act[u][0], zero, 0, 0, 0);
-                dl[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, r.act[u][0], zero, 0, 0, 0);
+                dh[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[0][u], zero, 0, 0, 0);
+                dl[0][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[0][u], zero, 0, 0, 0);
             }
+            aload(BQ < 8 ? b : b + 1, BQ % 8);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -655,9 +663,10 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
                 fold_digits((uint64_t)unpack_codes(nib, hb, c + 1), fs, a_lo, a_hi);
 #pragma unroll
                 for (int u = 0; u < NC; ++u) {
-                    dh[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, r.act[u][c + 1], zero, 0, 0, 0);
-                    dl[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, r.act[u][c + 1], zero, 0, 0, 0);
+                    dh[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[(c + 1) % BQ][u], zero, 0, 0, 0);
+                    dl[(c + 1) & 1][u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[(c + 1) % BQ][u], zero, 0, 0, 0);
                 }
+                aload(c + 1 + BQ < 8 ? b : b + 1, (c + 1 + BQ) % 8);
             }
 #pragma unroll
             for (int u = 0; u < NC; ++u)
@@ -674,20 +683,23 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
         // unconditional (past the last block they re-read it, unused), so
         // the compiler waits for each block's own loads only.
         Regs ra, rb;
-        const int last = p.blocks - 1;
         load(ra, 0);
+#pragma unroll
+        for (int c = 0; c < BQ; ++c) aload(0, c);
         for (int b = 0; b < p.blocks; b += 2) {
             load(rb, min(b + 1, last));
-            compute(ra);
+            compute(ra, b);
             if (b + 1 >= p.blocks) break;
             load(ra, min(b + 2, last));
-            compute(rb);
+            compute(rb, b + 1);
         }
     } else {
+#pragma unroll
+        for (int c = 0; c < BQ; ++c) aload(0, c);
         for (int b = 0; b < p.blocks; ++b) {
             Regs r;
             load(r, b);
-            compute(r);
+            compute(r, b);
         }
     }
 #pragma unroll
