@@ -1185,9 +1185,8 @@ namespace {
 }  // namespace
 
 // The LM-head call's launches on the library stream: Q8_K of x, the Q6_K
-// matvec whose epilogue leaves one arg-max candidate per 16-row tile (b=1:
-// maxed into AMAX_BUCKETS keys as the tiles finish), and the reduction of the
-// candidates.
+// matvec whose epilogue leaves one arg-max candidate per 16-row tile, and
+// the reduction of the candidates.
 int llamd::lmhead_enqueue(const void *w, int rows, int blocks, const float *d_x, int nseq,
                           float *d_logits, int32_t *d_ids, const LmHeadScratch &sc) {
     hipStream_t st = stream();
@@ -1196,9 +1195,7 @@ int llamd::lmhead_enqueue(const void *w, int rows, int blocks, const float *d_x,
     if (nseq == 1) {
         rc |= launch_q8k_quantize(d_x, sc.xq, sc.xd, nullptr, blocks, st);
         rc |= launch_q6k_mv_b1(w, 0, nullptr, sc.xq, sc.xd, d_logits, rows, blocks, 1, 0, st,
-                               nullptr, nullptr, nullptr, sc.bk);
-        rc |= launch_argmax_buckets(d_logits, sc.bk, d_ids, st);
-        return rc;
+                               nullptr, sc.pv, sc.pi);
     } else {
         rc |= launch_q8k_quantize_chunks(d_x, nseq, blocks, nullptr, 1, sc.cq, sc.cd, st);
         rc |= launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, sc.cq, sc.cd,
@@ -1228,7 +1225,6 @@ struct LmHead {
     const void *w;
     int rows, blocks, cap;
     DevBuf xq, xd, cq, cd, pv, pi;  // cq, cd: chunked activations for nseq > 1
-    DevBuf bk;                      // b=1 arg-max keys, zero between calls
 };
 }  // namespace
 
@@ -1237,10 +1233,10 @@ int llamd::lmhead_forward_q8k(void *h, const int8_t *xq, const float *xd, float 
     LmHead *l = (LmHead *)h;
     if (!l || !xq || !xd || !d_logits || !d_ids) return fail("lmhead_forward_q8k: bad arguments");
     hipStream_t st = stream();
-    unsigned long long *bk = l->bk.as<unsigned long long>();
     int rc = launch_q6k_mv_b1(l->w, 0, nullptr, xq, xd, d_logits, l->rows, l->blocks, 1, 0, st,
-                              nullptr, nullptr, nullptr, bk);
-    rc |= launch_argmax_buckets(d_logits, bk, d_ids, st);
+                              nullptr, l->pv.as<float>(), l->pi.as<int>());
+    rc |= launch_argmax_final(d_logits, l->rows, 1, l->pv.as<float>(), l->pi.as<int>(),
+                              (l->rows + 15) / 16, d_ids, st);
     return rc ? fail("lmhead_forward_q8k: launch failed") : 0;
 }
 
@@ -1263,9 +1259,7 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
     const size_t nq = (size_t)max_seq * blocks * QK;
     if (!l->xq.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
         !l->cq.alloc(chunk_q_bytes(max_seq, blocks)) || !l->cd.alloc(chunk_d_bytes(max_seq, blocks)) ||
-        !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4) ||
-        !l->bk.alloc(AMAX_BUCKETS * 8) ||
-        hipMemset(l->bk.p, 0, AMAX_BUCKETS * 8) != hipSuccess) {
+        !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4)) {
         delete l;
         fail("lmhead_create: allocation failed");
         return nullptr;
@@ -1284,7 +1278,7 @@ int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logit
     if (!l || !d_x || !d_logits || !d_ids || nseq <= 0 || nseq > l->cap)
         return fail("lmhead_forward: bad arguments");
     LmHeadScratch sc{l->xq.as<int8_t>(), l->xd.as<float>(), l->cq.as<int8_t>(), l->cd.as<float>(),
-                     l->pv.as<float>(), l->pi.as<int>(), l->bk.as<unsigned long long>()};
+                     l->pv.as<float>(), l->pi.as<int>()};
     return lmhead_enqueue(l->w, l->rows, l->blocks, d_x, nseq, d_logits, d_ids, sc)
                ? fail("lmhead_forward: launch failed") : 0;
 }

@@ -135,15 +135,6 @@ __device__ __forceinline__ void wave_argmax(T &v, int &i, T vidn) {
     i = readlane63(i);
 }
 
-// A (value, row) arg-max candidate as one unsigned key whose order is the
-// arg-max order: the larger value first, the lower row on ties; -0.0 keys as
-// +0.0 (the two compare equal). 0 lies below every key (no candidate).
-__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
-    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
-    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)k << 32) | (0xFFFFFFFFu - (uint32_t)row);
-}
-
 // Inclusive prefix sum over the wave (lane order).
 __device__ __forceinline__ double wave_inclusive_sum(double v) {
     v += dpp<DPP_ROW_SHR1, 0xF, true>(0.0, v);

@@ -10,8 +10,6 @@
 
 namespace llamd {
 
-constexpr int AMAX_BUCKETS = 64;  // arg-max keys the LM head's b=1 matvec maxes into
-
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
 extern int g_tune_batched_twin;  // grouped q6k_mv_batched: two chunks of one expert per wave
 extern int g_tune_mv_dot;  // 1: q6k_mv_b1's integer part on v_dot2 instead of MFMA (one matrix)
@@ -27,7 +25,7 @@ extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode la
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
                      hipStream_t st, const void *w_b = nullptr, float *amax_v = nullptr,
-                     int *amax_i = nullptr, unsigned long long *amax_bk = nullptr);
+                     int *amax_i = nullptr);
 // Down projection of n_slots routed experts (activation e for slot e) and the
 // routing-weighted combine (+ residual) into out, one workgroup per 16 rows.
 // One launch over up to three matrices sharing the activation (Q, K, V):
@@ -217,10 +215,6 @@ int argmax_parts(int n);
 // reference's arg-max of row x[seq * ld ..] (index 0 wins if x[0] is NaN).
 int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
                         int nparts, int32_t *out, hipStream_t st);
-// One sequence: the arg-max from AMAX_BUCKETS keys (launch_q6k_mv_b1's
-// amax_bk), with x[0] for the reference's NaN-at-index-0 rule; the keys are
-// reset to 0 for the next call.
-int launch_argmax_buckets(const float *x, unsigned long long *bk, int32_t *out, hipStream_t st);
 // pv, pi hold [nseq][parts] candidates, parts = argmax_parts(n) capped at
 // max_parts (> 0)
 int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, int32_t *out,
@@ -310,9 +304,8 @@ int shadow_q6k(const void *w, const size_t *planar_off, int rows, int blocks, co
 int q6k_handle_shape(const void *p, int *rows, int *blocks, int *n_expert);
 // Device scratch of one LM-head call (capi.cpp lmhead_enqueue): Q8_K of x
 // (nseq == 1: xq [blocks*256], xd [blocks]; nseq > 1: the token-chunked cq,
-// cd of lmhead_chunk_*_bytes), the per-tile arg-max candidates pv, pi
-// [nseq][ceil(rows/16)] (nseq > 1) and the AMAX_BUCKETS arg-max keys bk
-// (nseq == 1; zero between calls: the arg-max launch resets them).
+// cd of lmhead_chunk_*_bytes) and the per-tile arg-max candidates pv, pi
+// [nseq][ceil(rows/16)].
 struct LmHeadScratch {
     int8_t *xq;
     float *xd;
@@ -320,7 +313,6 @@ struct LmHeadScratch {
     float *cd;
     float *pv;
     int *pi;
-    unsigned long long *bk;
 };
 size_t lmhead_chunk_q_bytes(int nseq, int blocks);
 size_t lmhead_chunk_d_bytes(int nseq, int blocks);

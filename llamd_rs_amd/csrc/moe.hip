@@ -321,29 +321,6 @@ int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, i
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// The arg-max of one sequence from the AMAX_BUCKETS keys the LM head's b=1
-// matvec maxed its tiles' candidates into; the keys are then reset to 0.
-__global__ __launch_bounds__(64) void argmax_buckets(const float *x, unsigned long long *bk,
-                                                      int32_t *out) {
-    const int lane = threadIdx.x;
-    const float v0 = x[0];
-    unsigned long long k = bk[lane];
-#pragma unroll
-    for (int o = 32; o; o >>= 1) {
-        const unsigned long long ok = __shfl_xor(k, o, WAVE);
-        k = ok > k ? ok : k;
-    }
-    // the reference's incumbent is index 0: a NaN there is never beaten, and
-    // no key at all (every logit NaN) leaves 0
-    if (lane == 0) out[0] = (isnan(v0) || k == 0) ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)k);
-    bk[lane] = 0;
-}
-
-int launch_argmax_buckets(const float *x, unsigned long long *bk, int32_t *out, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_buckets, dim3(1), dim3(AMAX_BUCKETS), 0, st, x, bk, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
 int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
                         int nparts, int32_t *out, hipStream_t st) {
     hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(1024), 0, st, x, ld, pv, pi, nparts, out);

@@ -15,11 +15,9 @@
 // hipGetSymbolAddress and kept, and only that address reaches a kernel.
 //
 // Every call on one GPU shares that GPU's array and leaves its contents
-// behind. Only the b=1 arg-max keys must start at zero (every tile maxes its
-// candidate into them); the array starts zeroed and each call's last launch
-// clears them after reading. Everything else is written before it is read.
-// Two calls that overlap on one GPU (two host threads, two streams) race on
-// the array.
+// behind. Nothing in it needs to start at zero (every tile writes its
+// candidate, the quantizer writes every block), so nothing is cleared; two
+// calls that overlap on one GPU (two host threads, two streams) race on it.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -44,8 +42,7 @@ constexpr size_t NA_CQ = align256((size_t)NA_MAX_BLOCKS * 4096);         // one 
 constexpr size_t NA_CD = align256((size_t)NA_MAX_BLOCKS * 16 * 4);
 constexpr size_t NA_PV = align256(NA_TILES * NA_MAX_SEQ * 4);
 constexpr size_t NA_PI = align256(NA_TILES * NA_MAX_SEQ * 4);
-constexpr size_t NA_BK = align256((size_t)llamd::AMAX_BUCKETS * 8);  // b=1 arg-max keys
-constexpr size_t NA_BYTES = NA_XQ + NA_XD + NA_CQ + NA_CD + NA_PV + NA_PI + NA_BK;  // about 2.3 MB
+constexpr size_t NA_BYTES = NA_XQ + NA_XD + NA_CQ + NA_CD + NA_PV + NA_PI;  // about 2.3 MB
 
 __device__ __align__(256) unsigned char scratch[NA_BYTES];
 
@@ -103,9 +100,6 @@ int llamd_hip_lmhead_forward_noalloc(const void *d_w, int rows, int blocks, cons
     sc.cd = (float *)(base + NA_XQ + NA_XD + NA_CQ);
     sc.pv = (float *)(base + NA_XQ + NA_XD + NA_CQ + NA_CD);
     sc.pi = (int *)(base + NA_XQ + NA_XD + NA_CQ + NA_CD + NA_PV);
-    // zero at load (a __device__ array starts zeroed) and after every call
-    // (the arg-max launch resets them)
-    sc.bk = (unsigned long long *)(base + NA_XQ + NA_XD + NA_CQ + NA_CD + NA_PV + NA_PI);
     if (llamd::lmhead_chunk_q_bytes(nseq, blocks) > NA_CQ ||
         llamd::lmhead_chunk_d_bytes(nseq, blocks) > NA_CD)
         return llamd::set_error("lmhead_forward_noalloc: internal scratch layout too small");

@@ -71,9 +71,6 @@ struct MvParams {
     // optional per-tile arg-max candidates (one segment): [n_slots][tiles]
     float *amax_v;
     int *amax_i;
-    // or (one slot): AMAX_BUCKETS keys (argmax_key) each tile maxes its
-    // candidate into, tile t into bucket t % AMAX_BUCKETS
-    unsigned long long *amax_bk;
 };
 
 // One (slot, 16-row tile) item per KS waves of a 4-wave (KS = 8: 8-wave) workgroup; wave kc of
@@ -205,11 +202,7 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
         argmax_step(bv, bi, dpp<DPP_XOR2>(-INFINITY, bv), dpp<DPP_XOR2>(0x7FFFFFFF, bi));
         argmax_step(bv, bi, dpp<DPP_HALF_MIRROR>(-INFINITY, bv), dpp<DPP_HALF_MIRROR>(0x7FFFFFFF, bi));
         argmax_step(bv, bi, dpp<DPP_MIRROR>(-INFINITY, bv), dpp<DPP_MIRROR>(0x7FFFFFFF, bi));
-        if (p.amax_bk) {
-            // fire and forget: no wave waits for the atomic's return
-            if (lane == 0 && bi != 0x7FFFFFFF)
-                atomicMax(&p.amax_bk[t % AMAX_BUCKETS], argmax_key(bv, bi));
-        } else if (lane == 0) {
+        if (lane == 0) {
             p.amax_v[(size_t)slot * sgm.tiles + t] = bv;
             p.amax_i[(size_t)slot * sgm.tiles + t] = bi;
         }
@@ -871,9 +864,8 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
 }
 
 int launch_b1(const MvParams &p, hipStream_t st) {
-    const bool amax = p.amax_v || p.amax_bk;
-    if (amax && g_tune_mv_dot) launch_b1_n<1, true, true>(p, st);
-    else if (amax) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
+    if (p.amax_v && g_tune_mv_dot) launch_b1_n<1, true, true>(p, st);
+    else if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
     else if (p.n_seg == 1 && g_tune_mv_dot) launch_b1_n<1, false, true>(p, st);  // VALU dot products
     else if (p.n_seg == 1) launch_b1_n<1>(p, st);
     else if (p.n_seg == 2) launch_b1_n<2>(p, st);
@@ -885,14 +877,11 @@ int launch_b1(const MvParams &p, hipStream_t st) {
 
 int launch_q6k_mv_b1(const void *w, size_t expert_stride, const int32_t *ids, const int8_t *aq,
                      const float *ad, float *y, int rows, int blocks, int n_slots, int act_per_slot,
-                     hipStream_t st, const void *w_b, float *amax_v, int *amax_i,
-                     unsigned long long *amax_bk) {
-    if ((amax_v || amax_bk) && w_b) return -1;
-    if (amax_bk && (amax_v || n_slots != 1)) return -1;
+                     hipStream_t st, const void *w_b, float *amax_v, int *amax_i) {
+    if (amax_v && w_b) return -1;
     MvParams p = {};
     p.amax_v = amax_v;
     p.amax_i = amax_i;
-    p.amax_bk = amax_bk;
     // with a second weight, its outputs follow the first's: y = [w | w_b]
     const void *ws[2] = {w, w_b};
     float *ys[2] = {y, y + (size_t)n_slots * rows};

@@ -251,13 +251,12 @@ def test_lm_head_argmax_ties_and_nan(gpu, nseq, dot):          # device_forward.
         lib().llamd_hip_tune(b"mv_dot", 0)
 
 
-def test_lm_head_b1_argmax_keys_across_buckets_and_calls(gpu):
-    """b = 1 reduces the tiles' candidates through 64 atomically maxed keys
-    (tile t into key t % 64). A winner copied into a later tile of the same
-    key and of another key still resolves to the lowest row; all-negative
-    logits pick the least negative; and the keys start empty on every call
-    (a second call whose maximum is smaller than the first's)."""
-    rows, k = 130 * 16, 256                      # 130 tiles: keys hold 2-3 tiles
+def test_lm_head_b1_argmax_across_tiles_and_calls(gpu):
+    """b = 1 over 130 tiles: copies of the winner in a tile 64 apart and in
+    the next tile resolve to the lowest row; all-negative logits pick the
+    least negative; repeated calls on one head (later maxima smaller) each
+    give the oracle's id."""
+    rows, k = 130 * 16, 256
     x = H.sample(k, 23)
     w = H.weights(rows, 1, 29).reshape(rows, 210).copy()
     logits = O.matvec_q6k(w.reshape(-1), rows, k, x)
