@@ -105,9 +105,11 @@ __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_ex
 // blockIdx.y = token (prefill); down is [n_tok][n_used][n_embd].
 // skip (optional): pair slots of the grouped prefill; a pair with slot < 0
 // had an out-of-range expert id and adds no term.
+template <int V>
 __global__ void moe_combine(const float *down, const float *weights, const float *res, float *out,
                             int n_used, int n_embd, const int32_t *skip) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const int i = V * (blockIdx.x * blockDim.x + threadIdx.x);  // this thread's first element
     if (i >= n_embd) return;
     const size_t tok = blockIdx.y;
     down += tok * n_used * n_embd;
@@ -117,24 +119,33 @@ __global__ void moe_combine(const float *down, const float *weights, const float
     out += tok * n_embd;
     // every operand is loaded before the first add (a pair with no expert
     // still has a row in `down`, unused), so the loads are one round trip
-    // instead of one per expert; the adds keep the routing order
+    // instead of one per expert; the adds keep the routing order. V = 4:
+    // four consecutive elements per thread, 16-byte loads.
     constexpr int E = 16;  // n_used <= 16
-    float wv[E], dv[E];
+    float wv[E];
+    fv dv[E];
     bool live[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         live[e] = e < n_used && !(skip && skip[e] < 0);
         wv[e] = e < n_used ? weights[e] : 0.0f;
-        dv[e] = e < n_used ? down[(size_t)e * n_embd + i] : 0.0f;
+        dv[e] = e < n_used ? *(const fv *)(down + (size_t)e * n_embd + i) : fv{};
     }
-    const float r = res ? res[i] : 0.0f;
-    float acc = 0.0f;
+    const fv r = res ? *(const fv *)(res + i) : fv{};
+    fv acc = fv{};
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const float p = wv[e] * dv[e];
-        acc = live[e] ? acc + p : acc;
+#pragma unroll
+        for (int c = 0; c < V; ++c) {
+            const float p = wv[e] * dv[e][c];
+            acc[c] = live[e] ? acc[c] + p : acc[c];
+        }
     }
-    out[i] = res ? r + acc : acc;
+    if (res) {
+#pragma unroll
+        for (int c = 0; c < V; ++c) acc[c] = r[c] + acc[c];
+    }
+    *(fv *)(out + i) = acc;
 }
 
 // ---- 4. argmax: strict '>', lowest index wins (device_forward.rs:23-37) -----
@@ -300,8 +311,14 @@ int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *
 int launch_moe_combine(const float *down, const float *weights, const float *res, float *out,
                        int n_used, int n_embd, int n_tok, hipStream_t st, const int32_t *skip) {
     if (n_used < 1 || n_used > 16) return -1;
-    hipLaunchKernelGGL(moe_combine, dim3((n_embd + 255) / 256, n_tok), dim3(256), 0, st, down,
-                       weights, res, out, n_used, n_embd, skip);
+    // 16-byte vectors when every row starts 16-byte aligned
+    const bool vec = n_embd % 4 == 0 && ((uintptr_t)down | (uintptr_t)out | (uintptr_t)res) % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(moe_combine<4>, dim3((n_embd / 4 + 255) / 256, n_tok), dim3(256), 0, st,
+                           down, weights, res, out, n_used, n_embd, skip);
+    else
+        hipLaunchKernelGGL(moe_combine<1>, dim3((n_embd + 255) / 256, n_tok), dim3(256), 0, st, down,
+                           weights, res, out, n_used, n_embd, skip);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

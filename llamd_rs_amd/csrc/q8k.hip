@@ -86,6 +86,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k_chunks(const float *gate, cons
     if (item >= rows * blocks) return;
     const int r = item / blocks, b = item - r * blocks;
     const size_t o = (size_t)item * QK_K + 4 * lane;
+    const int slot = slot_of[r];  // loaded with the operands, not after the math
     const float4 gv = *(const float4 *)(gate + o);
     const float4 uv = *(const float4 *)(up + o);
     expf_ref_tab_fill(tab);
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k_chunks(const float *gate, cons
     int q[4];
     float dv;
     quantize_wave_q(v, lane, q, dv);
-    store_chunk(chunk_dword(q, lane), dv, lane, cq, cd, slot_of[r], b, blocks);
+    store_chunk(chunk_dword(q, lane), dv, lane, cq, cd, slot, b, blocks);
 }
 
 __global__ void silu_mul_f32(const float *gate, const float *up, float *out, int n) {
