@@ -46,9 +46,19 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     __syncthreads();
     // a pair whose id is outside [0, n_expert) joins no group: its slot is -1,
     // which the chunk quantizers skip and the combine counts as no term
-    for (int p = tid; p < n_pairs; p += blockDim.x) {
-        const int e = ids[p];
-        if ((unsigned)e < (unsigned)n_expert) atomicAdd(&hist[e], 1);
+    // ids in batches of PB per thread, all of a batch's loads in flight
+    // before its first atomic (one memory round trip per batch, not per id)
+    constexpr int PB = 8;
+    for (int base = 0; base < n_pairs; base += PB * (int)blockDim.x) {
+        int eid[PB];
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+            const int p = base + k * (int)blockDim.x + tid;
+            eid[k] = p < n_pairs ? ids[p] : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < PB; ++k)
+            if ((unsigned)eid[k] < (unsigned)n_expert) atomicAdd(&hist[eid[k]], 1);
     }
     __syncthreads();
     // exclusive prefix sums over experts (thread e owns expert e) of the
@@ -105,16 +115,27 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
         for (int i = totals[1] + tid; i < max_chunks; i += blockDim.x)
             twin_info[i] = GroupItem{-1, 0, 0, 0, 0, 0, 0, 0};
     }
-    for (int p = tid; p < n_pairs; p += blockDim.x) {
-        const int e = ids[p];
-        if ((unsigned)e >= (unsigned)n_expert) {
-            slot_of_pair[p] = -1;
-            continue;
+    for (int base = 0; base < n_pairs; base += PB * (int)blockDim.x) {
+        int eid[PB];
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+            const int p = base + k * (int)blockDim.x + tid;
+            eid[k] = p < n_pairs ? ids[p] : -1;
         }
-        const int pos = atomicAdd(&cursor[e], 1);
-        const int j = pos - start_lds[e];
-        slot_of_pair[p] = (sub_lds[e] + j / 16) * 16 + j % 16;
-        pair_idx[pos] = p;
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+            const int p = base + k * (int)blockDim.x + tid;
+            if (p >= n_pairs) continue;
+            const int e = eid[k];
+            if ((unsigned)e >= (unsigned)n_expert) {
+                slot_of_pair[p] = -1;
+                continue;
+            }
+            const int pos = atomicAdd(&cursor[e], 1);
+            const int j = pos - start_lds[e];
+            slot_of_pair[p] = (sub_lds[e] + j / 16) * 16 + j % 16;
+            pair_idx[pos] = p;
+        }
     }
 }
 
