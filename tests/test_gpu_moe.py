@@ -190,6 +190,34 @@ def test_prefill_grouped_equals_token_major(gpu, twin):
     layer.close()
 
 
+@pytest.mark.parametrize("twin", [1, 0])
+def test_prefill_chunk_boundary_groups(gpu, twin):
+    """Groups at the 16-token chunk boundaries: one expert taking every token
+    (4 full chunks), one with exactly 16 pairs, one with 17 (a chunk and a
+    lone token), one with 15, the rest spread thin; EXACT against
+    token-major moe_ffn with and without twins."""
+    n_embd, n_ff, n_expert, n_used, n_tok = 512, 256, 16, 4, 64
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 760)
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    t = np.arange(n_tok)
+    ids = np.stack([np.zeros(n_tok, int), np.where(t < 16, 1, 5), np.where(t < 17, 2, 6),
+                    np.where(t < 15, 3, 7 + t % 9)], axis=1).astype(np.int32)
+    counts = np.bincount(ids.ravel(), minlength=n_expert)
+    assert (counts[0], counts[1], counts[2], counts[3]) == (64, 16, 17, 15)
+    rng = np.random.default_rng(761)
+    w = rng.random((n_tok, n_used)).astype(np.float32) + 0.1
+    w /= w.sum(axis=1, keepdims=True)
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    prev = lib().llamd_hip_tune(b"batched_twin", twin)
+    try:
+        got = layer.prefill(x, ids, w)
+        want = O.moe_ffn_tokens(x, n_embd, n_ff, n_expert, gate, up, down, ids, w)
+        assert bits_equal(got, want)
+    finally:
+        lib().llamd_hip_tune(b"batched_twin", prev)
+    layer.close()
+
+
 def test_prefill_config_shape_sample(gpu, qwen_layer):
     """configs[3] shapes (hidden 2048, 128 experts, top-8, Zipf 1.1) on 48 tokens."""
     from llamd_rs_amd import synth
