@@ -521,6 +521,38 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
         out["moe_layer"]["vs_cpu"] = out["moe_layer"]["tok_s"] / (n / dt)
     log(f"  moe layer: {out['moe_layer']}")
 
+    # configs[1] shapes without the launch floor: all 128 experts' gate
+    # [768 x 2048] (and down [2048 x 768]) matrices in ONE grouped launch,
+    # each on the same activation, 3 copies of each expert tensor in rotation
+    # (3 x 167 MB, beyond the 256 MB Infinity Cache)
+    QB = lambda k: tuple(rocm.DeviceBuffer.from_array(a) for a in
+                         (lambda q: (q.qs, q.d))(rocm.quantize_q8k_on_device(synth.normal(23 + k, 1.0, k))))
+    ids_all = rocm.DeviceBuffer.from_array(np.arange(n_expert, dtype=np.int32))
+    grouped = {}
+    for name, host, rows, k in (("gate", gate, n_ff, n_embd), ("down", down, n_embd, n_ff)):
+        cps = [rocm.DeviceWeights.upload_experts(host, n_expert, rows, k // QK_K) for _ in range(3)]
+        gq, gd = QB(k)
+        gy = rocm.DeviceBuffer(n_expert * rows * 4)
+        def fg(i, cps=cps, gq=gq, gd=gd, gy=gy, rows=rows, k=k):
+            L.llamd_fwd_matvec_grouped(cps[i % 3].ptr, ids_all.ptr, gq.ptr, gd.ptr, gy.ptr, k // QK_K,
+                                       rows, n_expert)
+        gsteps = max(20, K // 4)
+        msg = time_region(L, fg, gsteps, 6, graph=False)
+        by = n_expert * q6k_bytes(rows, k)
+        us = msg / gsteps * 1e3
+        grouped[name] = {"rows": rows, "k": k, "matrices_per_launch": n_expert, "bytes": by,
+                         "us_per_launch": round(us, 2), "gbs": round(by / (us * 1e-6) / 1e9, 1),
+                         "pct_of_hbm_peak": round(100 * by / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 2)}
+        for c in cps:
+            c.close()
+        for b in (gq, gd, gy):
+            b.close()
+    grouped["how"] = ("q6k_mv_b1 over all 128 experts of one expert tensor in one launch "
+                      "(llamd_fwd_matvec_grouped, ids 0..127, one activation), 3 tensors in rotation")
+    out["configs1_grouped"] = grouped
+    ids_all.close()
+    log(f"  configs[1] shapes, 128 matrices per launch: {grouped}")
+
     # batched decode: 16 sequences, each routed by its own logits, experts
     # grouped across the batch (one layer call per 16 tokens)
     OB = rocm.DeviceBuffer(16 * n_embd * 4)

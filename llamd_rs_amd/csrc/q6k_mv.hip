@@ -848,15 +848,21 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
     // win while the grid is small -- 768 x 2048: 3.46 -> 3.17 us, 4096 x
     // 2048: 4.14 -> 3.82 us -- and lose from ~1000 tiles on (LM head 41 ->
     // 52 us), where four waves already fill the machine.
-    const int ks = g_tune_mv_ks ? g_tune_mv_ks : (p.blocks > 4 && items <= 384 ? 8 : 0);
+    // Short rows (at most 4 blocks, down's k = 768) in a large grid go the
+    // other way: one wave per tile walks all of its blocks. 128 down
+    // matrices [2048 x 768] in one grouped launch: 44.0 -> 29.9 us with one
+    // wave per tile; 8 of them (1024 tiles): 3.80 -> 3.48 us; below ~1000
+    // tiles four waves stay ahead (512 tiles: 2.98 vs 3.12 us).
+    const int ks = g_tune_mv_ks ? g_tune_mv_ks
+                                : (p.blocks > 4 && items <= 384 ? 8 : (p.blocks <= 4 && items >= 1024 ? 1 : 0));
     if (p.blocks <= 16 && (ks == 4 || ks == 8 || ks == 0)) {
         if (ks == 8)
             hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX, DOT>), dim3(items), dim3(512), 0, st, p);
         else
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
-            // tile at every size -- more loads in flight per tile and shorter
-            // per-wave chains.
+            // tile -- more loads in flight per tile and shorter per-wave
+            // chains -- except for short rows in large grids (above).
             hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX, DOT>), dim3(items), dim3(256), 0, st, p);
     } else {
         hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX, DOT>), dim3((items + 3) / 4), dim3(256), 0, st, p);
