@@ -104,7 +104,8 @@ __device__ float exact_sum_nonneg(const float (&vin)[XSUM_M], int n, ExactSumLds
     // pass 1: prefix sums of the terms in double
     double s = 0.0;
 #pragma unroll
-    for (int k = 0; k < M; ++k) s += (double)v[k];
+    for (int k = 0; k < M; ++k)
+        if (k < m) s += (double)v[k];  // m is uniform: runs shorter than M skip the rest
     const double incl = wave_inclusive_sum(s);
     if (lane == WAVE - 1) L.wtot[wave] = incl;
     __syncthreads();
@@ -154,6 +155,7 @@ __device__ float exact_sum_nonneg(const float (&vin)[XSUM_M], int n, ExactSumLds
         int flag = 0, cnt = 0;
 #pragma unroll
         for (int k = 0; k < M; ++k) {
+            if (k >= m) break;  // uniform; the skipped terms are zeros (certain, no increment)
             const float p = v[k];
             const double tj = tprev + (double)p;
             const bool above = tprev >= thr_b;
@@ -196,6 +198,7 @@ __device__ float exact_sum_nonneg(const float (&vin)[XSUM_M], int n, ExactSumLds
             float carry = ef ? ev : wc + ev;
 #pragma unroll
             for (int k = 0; k < M; ++k) {
+                if (k >= m) break;
                 if (v[k] < 0.0f) {
                     L.list[off++] = make_float2(carry, -v[k]);
                     carry = 0.0f;
