@@ -105,9 +105,12 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v = nullptr,
                           int *amax_i = nullptr, bool group_tables = false,
                           const void *w2 = nullptr, float *y2 = nullptr);
-// group_tables: sub_start carries launch_moe_group's sub_info / twin_info
-// records (written with the same max_chunks). w2 / y2: a second matrix of
-// the same shape on the same activations, in the same launch.
+// Grouped (grp_expert set): sub_start holds 2 * (n_groups + 1) entries, the
+// chunk prefix sub_start[0..n_groups] and the twin prefix after it
+// (launch_moe_group's layout); group_tables: the GroupItem records follow
+// (written with the same max_chunks). act_q / act_d: the token-chunked
+// activations (q8k_wave.hpp). w2 / y2: a second matrix of the same shape on
+// the same activations, in the same launch.
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 
 // q8k.hip
