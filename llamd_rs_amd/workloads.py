@@ -8,6 +8,9 @@ Infinity Cache) and prints one line when done. Meant to be run under
 rocprofv3 (--kernel-trace, --pmc) so a profile covers exactly one workload:
 
     configs1     Q6_K gate/up/down matvecs at batch 1 (768x2048, 2048x768)
+    configs1_grouped  the same shapes 128 matrices per launch (all experts
+                 of one expert tensor, one grouped launch each), 3 tensors
+                 rotating
     lm_head_b1   the LM head call (151936x2048), batch 1 and 16
     lm_head_b16
     moe_decode   one MoE decode layer per call, 4 layers rotating
@@ -47,6 +50,24 @@ def configs1(L, iters):
             q, d = dq[k]
             L.llamd_fwd_matvec(ws[j][i % n].ptr, q.ptr, d.ptr, outs[j].ptr, k // QK_K, r)
     _sync(L)
+
+
+def configs1_grouped(L, iters):
+    n_expert = 128
+    shapes = [(768, 2048, 501), (2048, 768, 503)]
+    ids = rocm.DeviceBuffer.from_array(np.arange(n_expert, dtype=np.int32))
+    for rows, k, seed in shapes:
+        host = synth.q6k_matrix(seed, 0.02, n_expert * rows, k)
+        cps = [rocm.DeviceWeights.upload_experts(host, n_expert, rows, k // QK_K) for _ in range(3)]
+        a = rocm.quantize_q8k_on_device(synth.normal(23 + k, 1.0, k))
+        q, d = rocm.DeviceBuffer.from_array(a.qs), rocm.DeviceBuffer.from_array(a.d)
+        y = rocm.DeviceBuffer(n_expert * rows * 4)
+        for i in range(iters):
+            L.llamd_fwd_matvec_grouped(cps[i % 3].ptr, ids.ptr, q.ptr, d.ptr, y.ptr, k // QK_K, rows,
+                                       n_expert)
+        _sync(L)
+        for c in cps:
+            c.close()
 
 
 def lm_head(L, iters, nseq):
@@ -120,6 +141,7 @@ def decode(L, iters):
 
 WORKLOADS = {
     "configs1": configs1,
+    "configs1_grouped": configs1_grouped,
     "lm_head_b1": lambda L, n: lm_head(L, n, 1),
     "lm_head_b16": lambda L, n: lm_head(L, n, 16),
     "moe_decode": moe_decode,
