@@ -37,8 +37,10 @@ hipStream_t g_stream = nullptr;
 // 1 router, gate/up + SwiGLU, down + combine; 0 unfused (separate SwiGLU).
 int g_tune_moe_fused = 2;
 // batched decode: up to this many sequences through the decode kernels, more
-// through the expert-grouped (prefill) kernels
-int g_tune_batch_decode_max = 16;
+// through the expert-grouped (prefill) kernels. Measured on MI355X (configs[2]
+// layer, us per token, decode / grouped): 12 sequences 9.06 / 9.31, 16
+// sequences 8.89 / 8.05.
+int g_tune_batch_decode_max = 12;
 // loads per cross-workgroup wait in the MoE decode kernel before the waiting
 // wave computes the value itself (0: always)
 int g_tune_moe_polls = 1 << 18;
