@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int r
     quantize_wave_q(v, lane, q, dv);
     const uint32_t dw = chunk_dword(q, lane);
     for (int k = 0; k < fan; ++k)
-        store_chunk(dw, dv, lane, cq, cd, slot_of ? __shfl(my_slot, k, WAVE) : r, b, blocks);
+        store_chunk(dw, dv, lane, cq, cd, slot_of ? __builtin_amdgcn_readlane(my_slot, k) : r, b, blocks);
 }
 
 // act[i] = silu(gate[i]) * up[i], then Q8_K of act. Optionally stores act.
