@@ -449,8 +449,10 @@ int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, cons
  * reference's sequential fold, all nseq x n_expert folds at once; then
  * softmax / top-k / renormalise per sequence), then the experts grouped
  * across the sequences so an expert's weights are read once per 16 tokens
- * routed to it; out = res + moe_ffn per sequence (res optional).
- * Bit-identical to nseq calls of llamd_hip_moe_forward. Device pointers. */
+ * routed to it; out = res + moe_ffn per sequence (res optional). Up to
+ * llamd_hip_tune("batch_decode_max") sequences (12 by default) the decode
+ * kernels run for every sequence instead. Bit-identical to nseq calls of
+ * llamd_hip_moe_forward either way. Device pointers. */
 int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, float *d_out,
                                 int nseq);
 /* Host in/out; ids / weights [nseq][n_used] and logits [nseq][n_expert] optional. */
