@@ -525,13 +525,16 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     # [768 x 2048] (and down [2048 x 768]) matrices in ONE grouped launch,
     # each on the same activation, 3 copies of each expert tensor in rotation
     # (3 x 167 MB, beyond the 256 MB Infinity Cache)
-    QB = lambda k: tuple(rocm.DeviceBuffer.from_array(a) for a in
-                         (lambda q: (q.qs, q.d))(rocm.quantize_q8k_on_device(synth.normal(23 + k, 1.0, k))))
+    def q8k_act(k):
+        """Q8_K of a seeded N(0,1) activation of length k, on the device."""
+        a = rocm.quantize_q8k_on_device(synth.normal(23 + k, 1.0, k))
+        return rocm.DeviceBuffer.from_array(a.qs), rocm.DeviceBuffer.from_array(a.d)
+
     ids_all = rocm.DeviceBuffer.from_array(np.arange(n_expert, dtype=np.int32))
     grouped = {}
     for name, host, rows, k in (("gate", gate, n_ff, n_embd), ("down", down, n_embd, n_ff)):
         cps = [rocm.DeviceWeights.upload_experts(host, n_expert, rows, k // QK_K) for _ in range(3)]
-        gq, gd = QB(k)
+        gq, gd = q8k_act(k)
         gy = rocm.DeviceBuffer(n_expert * rows * 4)
         def fg(i, cps=cps, gq=gq, gd=gd, gy=gy, rows=rows, k=k):
             L.llamd_fwd_matvec_grouped(cps[i % 3].ptr, ids_all.ptr, gq.ptr, gd.ptr, gy.ptr, k // QK_K,
@@ -553,8 +556,8 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
     ids_all.close()
     log(f"  configs[1] shapes, 128 matrices per launch: {grouped}")
 
-    # batched decode: 16 sequences, each routed by its own logits, experts
-    # grouped across the batch (one layer call per 16 tokens)
+    # batched decode: 16 sequences, each routed by its own logits (past
+    # batch_decode_max the experts are grouped across the batch)
     OB = rocm.DeviceBuffer(16 * n_embd * 4)
     def fb(i):
         xo = X.ptr + (i % 4) * 16 * n_embd * 4
