@@ -492,8 +492,12 @@ __global__ __launch_bounds__(512) void moe_router_gateup(DecodeParams p) {
         // stage their router rows under it
         const int row = b * CHAIN_EXPERTS + (wave & 3);
         const bool stage = b < chains && wave < CHAIN_EXPERTS && row < p.n_expert;
+        // the chain workgroups' norm leads to the router folds, the longest
+        // chain of the launch: their waves go first in issue on shared SIMDs
+        if (b < chains) __builtin_amdgcn_s_setprio(2);
         norm_prologue(p, xs, xl, b == 0, stage ? p.rw + (size_t)row * p.k : nullptr,
                       sm.prod[wave & 3]);
+        if (b < chains) __builtin_amdgcn_s_setprio(0);
         p.x = xs;
     }
     if (b < chains) {
