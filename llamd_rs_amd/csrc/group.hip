@@ -49,8 +49,11 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
     // ids in batches of PB per thread, all of a batch's loads in flight
     // before its first atomic (one memory round trip per batch, not per id)
     constexpr int PB = 8;
+    // the last batch's ids stay in registers for the scatter below (with up
+    // to PB * blockDim.x pairs, the only batch: no second round trip)
+    int eid[PB];
+    int last_base = 0;
     for (int base = 0; base < n_pairs; base += PB * (int)blockDim.x) {
-        int eid[PB];
 #pragma unroll
         for (int k = 0; k < PB; ++k) {
             const int p = base + k * (int)blockDim.x + tid;
@@ -59,6 +62,7 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
 #pragma unroll
         for (int k = 0; k < PB; ++k)
             if ((unsigned)eid[k] < (unsigned)n_expert) atomicAdd(&hist[eid[k]], 1);
+        last_base = base;
     }
     __syncthreads();
     // exclusive prefix sums over experts (thread e owns expert e) of the
@@ -115,12 +119,14 @@ __global__ __launch_bounds__(1024) void moe_group(const int32_t *ids, int n_pair
         for (int i = totals[1] + tid; i < max_chunks; i += blockDim.x)
             twin_info[i] = GroupItem{-1, 0, 0, 0, 0, 0, 0, 0};
     }
-    for (int base = 0; base < n_pairs; base += PB * (int)blockDim.x) {
-        int eid[PB];
+    // batches in reverse, the one still in registers first
+    for (int base = last_base; base >= 0 && n_pairs > 0; base -= PB * (int)blockDim.x) {
+        if (base != last_base) {
 #pragma unroll
-        for (int k = 0; k < PB; ++k) {
-            const int p = base + k * (int)blockDim.x + tid;
-            eid[k] = p < n_pairs ? ids[p] : -1;
+            for (int k = 0; k < PB; ++k) {
+                const int p = base + k * (int)blockDim.x + tid;
+                eid[k] = p < n_pairs ? ids[p] : -1;
+            }
         }
 #pragma unroll
         for (int k = 0; k < PB; ++k) {

@@ -190,6 +190,28 @@ def test_prefill_grouped_equals_token_major(gpu, twin):
     layer.close()
 
 
+def test_prefill_grouping_past_one_id_batch(gpu):
+    """The grouping kernel takes the expert ids in batches of 8 per thread of
+    its 1024 (8192 pairs); the last batch stays in registers for the scatter
+    and the others are loaded again. 1040 tokens x top-8 = 8320 pairs cross
+    that line: every token is checked bit for bit against the CPU."""
+    from llamd_rs_amd import synth
+    n_embd, n_ff, n_expert, n_used, n_tok = 512, 256, 16, 8, 1040
+    router, gate, up, down = make_layer(n_embd, n_ff, n_expert, 910)
+    layer = gpu.MoeLayer(router, gate, up, down, n_embd, n_ff, n_expert, n_used)
+    x = synth.normal(911, 1.0, n_tok * n_embd).reshape(n_tok, n_embd)
+    ids, w = synth.zipf_routing(912, 1.1, n_tok, n_expert, n_used)
+    assert ids.size > 8192
+    got = layer.prefill(x, ids.astype(np.int32), w)
+    parts = H.par_map(lambda s: O.moe_ffn_tokens(x[s:s + 16], n_embd, n_ff, n_expert, gate, up,
+                                                 down, ids[s:s + 16], w[s:s + 16]),
+                      range(0, n_tok, 16))
+    want = np.concatenate(parts)
+    bad = [t for t in range(n_tok) if not bits_equal(got[t], want[t])]
+    assert not bad, bad[:10]
+    layer.close()
+
+
 @pytest.mark.parametrize("twin", [1, 0])
 def test_prefill_chunk_boundary_groups(gpu, twin):
     """Groups at the 16-token chunk boundaries: one expert taking every token
