@@ -454,6 +454,22 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                                    "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
                                    "call": "Q8_K quantize + Q6_K matvec + argmax"}
         log(f"  lm_head b{nseq}: {out[f'lm_head_b{nseq}']}")
+
+    def fr(i):
+        h = heads[i % 4][1]
+        if L.llamd_hip_lmhead_forward_ex(h.handle, xb.ptr, 16, logits.ptr, ids.ptr, 1):
+            raise RuntimeError("lmhead (REDUCTION)")
+    steps = max(10, K // 4)
+    ms = time_region(L, fr, steps, 3, graph=False)
+    by = q6k_bytes(rows, k) + 16 * k * 4 + 16 * rows * 4
+    out["lm_head_b16_reduction"] = {
+        "us_per_call": ms / steps * 1e3, "bytes": by, "gbs": by / (ms / steps * 1e-3) / 1e9,
+        "pct_of_hbm_peak": round(100 * by / (ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+        "call": "Q8_K quantize + REDUCTION-tolerance Q6_K matvec + certified exact argmax "
+                "(LLAMD_HIP_REDUCTION)",
+        "parity": "logits within tolerance::REDUCTION, ids bit-exact "
+                  "(tests/test_gpu_moe.py::test_lm_head_b16_argmax_exact, ::test_lm_head_b16_reduction_near_ties)"}
+    log(f"  lm_head b16 (REDUCTION): {out['lm_head_b16_reduction']}")
     # the LM-head matvec kernel alone (activation already quantized)
     a1 = rocm.quantize_q8k_on_device(synth.normal(31, 1.0, k))
     q1, d1 = rocm.DeviceBuffer.from_array(a1.qs), rocm.DeviceBuffer.from_array(a1.d)
@@ -592,6 +608,18 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                               "int_tops": ops / (ms / steps * 1e-3) / 1e12,
                               "experts_used": used, "weight_bytes": wbytes,
                               "weight_gbs": wbytes / (ms / steps * 1e-3) / 1e9}
+
+    def fpr(i):
+        if L.llamd_hip_moe_prefill_ex(layers[i % 4].handle, xs.ptr, ids_d.ptr, w_d.ptr, po.ptr, n_tok, 1):
+            raise RuntimeError("prefill (REDUCTION)")
+    ms_r = time_region(L, fpr, steps, 4, graph=False)
+    out["prefill_grouped_reduction"] = {
+        "tokens": n_tok, "ms_per_pass": ms_r / steps, "tok_s": n_tok * steps / (ms_r * 1e-3),
+        "int_tops": ops / (ms_r / steps * 1e-3) / 1e12,
+        "weight_gbs": wbytes / (ms_r / steps * 1e-3) / 1e9,
+        "parity": "within tolerance::REDUCTION x rms per token (LLAMD_HIP_REDUCTION; "
+                  "tests/test_gpu_moe.py::test_prefill_full_config_512_tokens)"}
+    log(f"  prefill (REDUCTION): {out['prefill_grouped_reduction']}")
     if moe_cpu_seconds > 0:
         # the reference's CPU path runs moe_ffn token by token: time a sample
         # of 16 tokens (1 thread) and scale to the 512-token pass

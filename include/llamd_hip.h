@@ -444,6 +444,19 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
                           float *d_out, int n_tok);
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
                                float *out, int n_tok);
+/* Not in the reference. flags 0: llamd_hip_moe_prefill. flags
+ * LLAMD_HIP_REDUCTION: the grouped GEMMs accumulate a block's eight classes
+ * in the matrix-core accumulators and fold one float term per (row, token,
+ * block), instead of the reference's eight ordered class sums. Outputs are
+ * then within tolerance::REDUCTION (rms-scaled, grouped_expert.rs:147-175) of
+ * the CPU path, not bit-identical; the Q8_K bytes of x and of the SwiGLU
+ * activations are the exact path's whenever the gate/up outputs round the
+ * same way. Any other flag bit is an error. */
+#define LLAMD_HIP_REDUCTION 1
+int llamd_hip_moe_prefill_ex(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
+                             float *d_out, int n_tok, int flags);
+int llamd_hip_moe_prefill_host_ex(void *h, const float *x, const int32_t *ids, const float *w,
+                                  float *out, int n_tok, int flags);
 /* Batched decode (device.rs:741-962, forward_batch's MoE block): nseq
  * sequences x [nseq][n_embd], each routed by ITS OWN router logits (the
  * reference's sequential fold, all nseq x n_expert folds at once; then
@@ -477,6 +490,16 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
 void llamd_hip_lmhead_destroy(void *h);
 int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logits,
                              int32_t *d_ids);
+/* flags 0: llamd_hip_lmhead_forward. flags LLAMD_HIP_REDUCTION with nseq > 1:
+ * the logits come from the matrix-core kernel that folds one float term per
+ * (row, token, block) and are within tolerance::REDUCTION of the CPU's
+ * (rows whose tile could hold the maximum are recomputed exactly and carry
+ * the CPU's bits); d_ids are still the reference's arg-max of the EXACT
+ * logits, bit for bit: a rounding bound certifies which 16-row tiles can hold
+ * the maximum, and only those are recomputed exactly. At nseq == 1 the call
+ * is the exact one. Any other flag bit is an error. */
+int llamd_hip_lmhead_forward_ex(void *h, const float *d_x, int nseq, float *d_logits,
+                                int32_t *d_ids, int flags);
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc): llamd_hip_lmhead_forward without a handle, allocating nothing.

@@ -95,6 +95,8 @@ SIGNATURES = {
     "llamd_hip_moe_forward_host": (i32, [vp, vp, vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_prefill": (i32, [vp, vp, vp, vp, vp, i32]),
     "llamd_hip_moe_prefill_host": (i32, [vp, vp, vp, vp, vp, i32]),
+    "llamd_hip_moe_prefill_ex": (i32, [vp, vp, vp, vp, vp, i32, i32]),
+    "llamd_hip_moe_prefill_host_ex": (i32, [vp, vp, vp, vp, vp, i32, i32]),
     "llamd_hip_moe_stats": (i32, [vp, i32p, i32p]),
     "llamd_hip_moe_forward_batch": (i32, [vp, vp, vp, vp, i32]),
     "llamd_hip_moe_forward_batch_host": (i32, [vp, vp, vp, vp, vp, vp, vp, i32]),
@@ -120,6 +122,7 @@ SIGNATURES = {
     "llamd_hip_lmhead_create": (vp, [vp, i32, i32, i32]),
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),
+    "llamd_hip_lmhead_forward_ex": (i32, [vp, vp, i32, vp, vp, i32]),
     "llamd_hip_lmhead_forward_noalloc": (i32, [vp, i32, i32, vp, i32, vp, vp]),
     "llamd_hip_lmhead_noalloc_scratch_bytes": (sz, []),
     "llamd_hip_event_create": (vp, []),

@@ -262,6 +262,18 @@ int llamd_hip_tune(const char *key, int value) {
         g_tune_batched_twin = value ? 1 : 0;
         return prev;
     }
+    if (!strcmp(key, "fast_lds")) {
+        const int prev = g_tune_fast_lds;
+        g_tune_fast_lds = value ? 1 : 0;
+        return prev;
+    }
+    if (!strcmp(key, "fast_ks")) {
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return fail("tune: fast_ks takes 0 (by shape), 1, 2 or 4");
+        const int prev = g_tune_fast_ks;
+        g_tune_fast_ks = value;
+        return prev;
+    }
     if (!strcmp(key, "mv_dot")) {
         const int prev = g_tune_mv_dot;
         g_tune_mv_dot = value ? 1 : 0;
@@ -1044,7 +1056,7 @@ namespace {
 // The expert-grouped FFN of n_tok tokens with routing ids / weights
 // [n_tok][n_used] on the device; out = res + moe_ffn (res optional).
 int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float *d_w,
-                const float *d_res, float *d_out, int n_tok) {
+                const float *d_res, float *d_out, int n_tok, bool fast = false) {
     const int np = n_tok * m->n_used;
     if (n_tok > m->cap_tok) {
         // grown outside any capture; the stream is drained first so no queued
@@ -1080,7 +1092,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_xq.as<int8_t>(), m->p_xd.as<float>(),
                                 m->p_g.as<float>(), m->n_ff, m->n_ff, m->be, m->n_expert, max_chunks, st,
-                                nullptr, nullptr, true, m->upw, m->p_u.as<float>());
+                                nullptr, nullptr, true, m->upw, m->p_u.as<float>(), fast);
     // SwiGLU + Q8_K per pair, into the pair's chunk slot
     rc |= launch_swiglu_q8k_chunks(m->p_g.as<float>(), m->p_u.as<float>(), np, m->bf,
                                    m->p_slot.as<int32_t>(), m->p_aq.as<int8_t>(),
@@ -1090,7 +1102,7 @@ int moe_grouped(MoeLayer *m, const float *d_x, const int32_t *d_ids, const float
                                 m->p_grp_c.as<int32_t>(), m->p_sub.as<int32_t>(),
                                 m->p_idx.as<int32_t>(), m->p_aq.as<int8_t>(), m->p_ad.as<float>(),
                                 m->p_dn.as<float>(), m->n_embd, m->n_embd, m->bf, m->n_expert,
-                                max_chunks, st, nullptr, nullptr, true);
+                                max_chunks, st, nullptr, nullptr, true, nullptr, nullptr, fast);
     rc |= launch_moe_combine(m->p_dn.as<float>(), d_w, d_res, d_out, m->n_used, m->n_embd, n_tok, st,
                              m->p_slot.as<int32_t>());
     return rc ? fail("moe_prefill: launch failed") : 0;
@@ -1105,6 +1117,14 @@ int llamd_hip_moe_prefill(void *h, const float *d_x, const int32_t *d_ids, const
     MoeLayer *m = (MoeLayer *)h;
     if (!m || !d_x || !d_ids || !d_w || !d_out || n_tok <= 0) return fail("moe_prefill: bad arguments");
     return moe_grouped(m, d_x, d_ids, d_w, nullptr, d_out, n_tok);
+}
+
+int llamd_hip_moe_prefill_ex(void *h, const float *d_x, const int32_t *d_ids, const float *d_w,
+                             float *d_out, int n_tok, int flags) {
+    MoeLayer *m = (MoeLayer *)h;
+    if (!m || !d_x || !d_ids || !d_w || !d_out || n_tok <= 0 || (flags & ~LLAMD_HIP_REDUCTION))
+        return fail("moe_prefill_ex: bad arguments");
+    return moe_grouped(m, d_x, d_ids, d_w, nullptr, d_out, n_tok, (flags & LLAMD_HIP_REDUCTION) != 0);
 }
 
 int llamd_hip_moe_forward_batch(void *h, const float *d_x, const float *d_res, float *d_out,
@@ -1163,8 +1183,14 @@ int llamd_hip_moe_forward_batch_host(void *h, const float *x, const float *res, 
 
 int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, const float *w,
                                float *out, int n_tok) {
+    return llamd_hip_moe_prefill_host_ex(h, x, ids, w, out, n_tok, 0);
+}
+
+int llamd_hip_moe_prefill_host_ex(void *h, const float *x, const int32_t *ids, const float *w,
+                                  float *out, int n_tok, int flags) {
     MoeLayer *m = (MoeLayer *)h;
-    if (!m || !x || !ids || !w || !out || n_tok <= 0) return fail("moe_prefill_host: bad arguments");
+    if (!m || !x || !ids || !w || !out || n_tok <= 0 || (flags & ~LLAMD_HIP_REDUCTION))
+        return fail("moe_prefill_host: bad arguments");
     const int np = n_tok * m->n_used;
     for (int i = 0; i < np; ++i)
         if (ids[i] < 0 || ids[i] >= m->n_expert) return fail("moe_prefill_host: bad expert id %d", ids[i]);
@@ -1173,8 +1199,8 @@ int llamd_hip_moe_prefill_host(void *h, const float *x, const int32_t *ids, cons
     DevBuf dx(nx), di((size_t)np * 4), dw((size_t)np * 4), dout(nx);
     if (!dx.p || !di.p || !dw.p || !dout.p) return fail("hipMalloc");
     if (!up(dx.p, x, nx) || !up(di.p, ids, (size_t)np * 4) || !up(dw.p, w, (size_t)np * 4)) return -1;
-    if (llamd_hip_moe_prefill(m, dx.as<float>(), di.as<int32_t>(), dw.as<float>(), dout.as<float>(),
-                              n_tok))
+    if (llamd_hip_moe_prefill_ex(m, dx.as<float>(), di.as<int32_t>(), dw.as<float>(), dout.as<float>(),
+                                 n_tok, flags))
         return -1;
     if (!down(out, dout.p, nx) || !sync()) return -1;
     return 0;
@@ -1198,6 +1224,15 @@ int llamd::lmhead_enqueue(const void *w, int rows, int blocks, const float *d_x,
         rc |= launch_q8k_quantize(d_x, sc.xq, sc.xd, nullptr, blocks, st);
         rc |= launch_q6k_mv_b1(w, 0, nullptr, sc.xq, sc.xd, d_logits, rows, blocks, 1, 0, st,
                                nullptr, sc.pv, sc.pi);
+    } else if (sc.mt) {
+        // REDUCTION-tolerance logits; the arg-max is certified and exact
+        rc |= launch_q8k_quantize_chunks(d_x, nseq, blocks, nullptr, 1, sc.cq, sc.cd, st, sc.xq, sc.xd);
+        rc |= launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, sc.cq, sc.cd,
+                                    d_logits, rows, rows, blocks, nseq, (nseq + CHUNK - 1) / CHUNK,
+                                    st, sc.pv, sc.pi, false, nullptr, nullptr, true);
+        rc |= launch_lmhead_certify(w, rows, blocks, nseq, sc.xq, sc.xd, sc.pv, sc.pi, sc.mt,
+                                    d_logits, d_ids, st);
+        return rc;
     } else {
         rc |= launch_q8k_quantize_chunks(d_x, nseq, blocks, nullptr, 1, sc.cq, sc.cd, st);
         rc |= launch_q6k_mv_batched(w, 0, nullptr, nullptr, nullptr, nullptr, nullptr, sc.cq, sc.cd,
@@ -1227,6 +1262,7 @@ struct LmHead {
     const void *w;
     int rows, blocks, cap;
     DevBuf xq, xd, cq, cd, pv, pi;  // cq, cd: chunked activations for nseq > 1
+    DevBuf mt;                      // per-tile weight bound (LLAMD_HIP_REDUCTION)
 };
 }  // namespace
 
@@ -1261,9 +1297,16 @@ void *llamd_hip_lmhead_create(const void *d_w, int rows, int blocks, int max_seq
     const size_t nq = (size_t)max_seq * blocks * QK;
     if (!l->xq.alloc(nq) || !l->xd.alloc((size_t)max_seq * blocks * 4) ||
         !l->cq.alloc(chunk_q_bytes(max_seq, blocks)) || !l->cd.alloc(chunk_d_bytes(max_seq, blocks)) ||
-        !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4)) {
+        !l->pv.alloc((size_t)parts * max_seq * 4) || !l->pi.alloc((size_t)parts * max_seq * 4) ||
+        !l->mt.alloc((size_t)parts * 4)) {
         delete l;
         fail("lmhead_create: allocation failed");
+        return nullptr;
+    }
+    // the weights' per-tile bound, once (read by the certified arg-max)
+    if (launch_q6k_tile_bound(l->w, rows, blocks, l->mt.as<float>(), stream()) || !sync()) {
+        delete l;
+        fail("lmhead_create: tile bound failed");
         return nullptr;
     }
     return l;
@@ -1276,11 +1319,17 @@ void llamd_hip_lmhead_destroy(void *h) {
 }
 
 int llamd_hip_lmhead_forward(void *h, const float *d_x, int nseq, float *d_logits, int32_t *d_ids) {
+    return llamd_hip_lmhead_forward_ex(h, d_x, nseq, d_logits, d_ids, 0);
+}
+
+int llamd_hip_lmhead_forward_ex(void *h, const float *d_x, int nseq, float *d_logits, int32_t *d_ids,
+                                int flags) {
     LmHead *l = (LmHead *)h;
-    if (!l || !d_x || !d_logits || !d_ids || nseq <= 0 || nseq > l->cap)
+    if (!l || !d_x || !d_logits || !d_ids || nseq <= 0 || nseq > l->cap || (flags & ~LLAMD_HIP_REDUCTION))
         return fail("lmhead_forward: bad arguments");
     LmHeadScratch sc{l->xq.as<int8_t>(), l->xd.as<float>(), l->cq.as<int8_t>(), l->cd.as<float>(),
                      l->pv.as<float>(), l->pi.as<int>()};
+    if ((flags & LLAMD_HIP_REDUCTION) && nseq > 1) sc.mt = l->mt.as<float>();
     return lmhead_enqueue(l->w, l->rows, l->blocks, d_x, nseq, d_logits, d_ids, sc)
                ? fail("lmhead_forward: launch failed") : 0;
 }

@@ -11,7 +11,9 @@
 namespace llamd {
 
 // Tuning overrides (0 = automatic); set through llamd_hip_tune.
-extern int g_tune_batched_twin;  // grouped q6k_mv_batched: two chunks of one expert per wave
+extern int g_tune_batched_twin;
+extern int g_tune_fast_lds;  // LLAMD_HIP_REDUCTION LM head: the chunk's quants staged in LDS
+extern int g_tune_fast_ks;  // LLAMD_HIP_REDUCTION batched kernels: waves per item (K split), 0 = by shape  // grouped q6k_mv_batched: two chunks of one expert per wave
 extern int g_tune_mv_dot;  // 1: q6k_mv_b1's integer part on v_dot2 instead of MFMA (one matrix)
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
@@ -104,22 +106,40 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v = nullptr,
                           int *amax_i = nullptr, bool group_tables = false,
-                          const void *w2 = nullptr, float *y2 = nullptr);
+                          const void *w2 = nullptr, float *y2 = nullptr, bool fast = false);
 // Grouped (grp_expert set): sub_start holds 2 * (n_groups + 1) entries, the
 // chunk prefix sub_start[0..n_groups] and the twin prefix after it
 // (launch_moe_group's layout); group_tables: the GroupItem records follow
 // (written with the same max_chunks). act_q / act_d: the token-chunked
 // activations (q8k_wave.hpp). w2 / y2: a second matrix of the same shape on
-// the same activations, in the same launch.
+// the same activations, in the same launch. fast: the REDUCTION-tolerance
+// kernels (one float accumulator per output instead of the reference's eight
+// class sums; outputs within REDUCTION of dot_q6k_q8k, not bit-identical).
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
+// Per 16-row tile t of a tiled Q6_K matrix: mt[t] = the largest over its rows
+// of sum_b |f16(d_b)| * sum_e |sc(e) * (q_e - 32)| (an upper bound of the
+// row's sum of |dequantized weight| products' scale, for the arg-max
+// certificate below).
+int launch_q6k_tile_bound(const void *w, int rows, int blocks, float *mt, hipStream_t st);
+// The LM head's certified arg-max over REDUCTION-tolerance logits (the fast
+// batched kernel's per-(token, tile) candidates pv / pi, pi < 0 marking a tile
+// with a NaN logit): per token, every tile whose candidate can reach the
+// largest certified lower bound is recomputed exactly (dot_q6k_q8k's bits,
+// written back into logits), and ids = the reference's arg-max of the exact
+// logits. nq / nd: the tokens' Q8_K in the natural layout.
+int launch_lmhead_certify(const void *w, int rows, int blocks, int nseq, const int8_t *nq,
+                          const float *nd, const float *pv, const int *pi, const float *mt,
+                          float *logits, int32_t *ids, hipStream_t st);
 
 // q8k.hip
 int launch_q8k_quantize(const float *x, int8_t *qs, float *d, int16_t *bsums, int nblocks,
                         hipStream_t st);
 // rows of x to the token-chunked layout, each row to `fan` slots slot_of[r*fan+k]
 // (slot_of == nullptr: row r to slot r)
+// (nq, nd: optionally also the natural layout, row r at nq[r * blocks * 256], nd[r * blocks])
 int launch_q8k_quantize_chunks(const float *x, int rows, int blocks, const int32_t *slot_of,
-                               int fan, int8_t *cq, float *cd, hipStream_t st);
+                               int fan, int8_t *cq, float *cd, hipStream_t st,
+                               int8_t *nq = nullptr, float *nd = nullptr);
 int launch_swiglu_q8k(const float *gate, const float *up, float *act_out, int8_t *qs, float *d,
                       int16_t *bsums, int nblocks, hipStream_t st);
 int launch_swiglu_q8k_chunks(const float *gate, const float *up, int rows, int blocks,
@@ -316,6 +336,9 @@ struct LmHeadScratch {
     float *cd;
     float *pv;
     int *pi;
+    // non-null: REDUCTION-tolerance logits with a certified exact arg-max
+    // (nseq > 1; mt from launch_q6k_tile_bound)
+    const float *mt = nullptr;
 };
 size_t lmhead_chunk_q_bytes(int nseq, int blocks);
 size_t lmhead_chunk_d_bytes(int nseq, int blocks);

@@ -635,9 +635,9 @@ __device__ __forceinline__ void batched_tile(const BatchParams &p, int lane, int
         for (int u = 0; u < NC; ++u)
 #pragma unroll
             for (int v = 0; v < 4; ++v) dd[u][v] = d4[v] * r.adb[u];
+        const v4i zero = {0, 0, 0, 0};
         // software-pipelined by one class: the MFMAs of class c+1 are issued
         // before the epilogue of class c reads its results
-        const v4i zero = {0, 0, 0, 0};
         v4i dh[2][NC], dl[2][NC];
         {
             long a_lo, a_hi;
@@ -736,6 +736,7 @@ __global__ __launch_bounds__(256) void q6k_mv_batched(BatchParams pk) {
     const int lane = threadIdx.x & 63;
     BatchParams p;
     const int item = batch_item(pk, p);
+    if (item >= p.items_per_mat) return;  // the grid's rounding to whole workgroups
     const int t = item % p.tiles;
     const int sub = item / p.tiles;
     int st = sub, cnt, start = 0, expert = 0;
@@ -780,6 +781,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int lane = threadIdx.x & 63;
     BatchParams p;
     const int item = batch_item(pk, p);
+    if (item >= p.items_per_mat) return;  // the grid's rounding to whole workgroups
     const int t = item % p.tiles;
     const int tw = item / p.tiles;
     const int32_t *twin_start = p.sub_start + p.n_groups + 1;
@@ -814,11 +816,481 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         batched_tile<1>(p, lane, t, sub, st, cnt, start, expert);
 }
 
+// ---- REDUCTION-tolerance batched kernels (LLAMD_HIP_REDUCTION) ----------------
+//
+// The same operands, digits and MFMAs as batched_tile, but the MFMAs of all 8
+// classes of a block accumulate into one pair of digit accumulators: the
+// block's integer dot sum_c aux32[c] is exact in int32 (|.| < 2^27), and the
+// float epilogue is one convert and one fused multiply-add per (row, token,
+// block) instead of the reference's eight ordered class sums. Only the float
+// rounding differs from dot_q6k_q8k (nb products and additions per row
+// instead of 8 nb and the 8-term class sum), so outputs are within REDUCTION,
+// not bit-identical. Because the partial sums may now be added in any order,
+// K is split over KS waves of one workgroup (a shorter dependent chain of
+// block loads per wave, KS times the waves in flight), met in LDS.
+
+// The lane's partial sums (4 rows x NC chunks) over blocks [b0, b1) of tile t.
+// The dynamic LDS of the LDSA kernels below.
+extern __shared__ uint4 g_act_lds[];
+
+// LDSA: the chunk's quants are read from g_act_lds (same layout).
+template <int NC, bool LDSA = false>
+__device__ __forceinline__ void fast_tile_range(const BatchParams &p, int lane, int t, int sub0,
+                                                int expert, int b0, int b1, float acc[2][4]) {
+    const int n = lane & 15, s = lane >> 4;
+    const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
+    const size_t chunk_q = (size_t)p.blocks * CHUNK_BLOCK_BYTES, chunk_d = (size_t)p.blocks * CHUNK_TOKENS;
+    const int8_t *aq = (LDSA ? (const int8_t *)g_act_lds : p.act_q + (size_t)sub0 * chunk_q) + n * 32 + 8 * s;
+    const float *ad = p.act_d + (size_t)sub0 * chunk_d + n;
+    // class planes two classes ahead of their MFMAs, across blocks (past the
+    // range's last block the loads re-read it, unused)
+    constexpr int BQ = 2;
+    const int last = b1 - 1;
+    long act[BQ][NC];
+    auto aload = [&](int b, int c) {
+#pragma unroll
+        for (int u = 0; u < NC; ++u)
+            act[c % BQ][u] = *(const long *)(aq + u * chunk_q + (size_t)min(b, last) * CHUNK_BLOCK_BYTES + 512 * c);
+    };
+#pragma unroll
+    for (int c = 0; c < BQ; ++c) aload(b0, c);
+    struct W {
+        uint4 q0, q1, q2;
+        uint32_t scw;
+        uint2 dw;
+        float adb[NC];
+    };
+    auto wload = [&](W &r, int b) {
+        const uint8_t *sg = seg + (size_t)b * SEG_BYTES;
+        r.q0 = *(const uint4 *)(sg + 16 * lane);
+        r.q1 = *(const uint4 *)(sg + SEG_PART + 16 * lane);
+        r.q2 = *(const uint4 *)(sg + 2 * SEG_PART + 16 * lane);
+        r.scw = *(const uint32_t *)(sg + SEG_SC + 4 * lane);
+        r.dw = *(const uint2 *)(sg + SEG_D + 8 * s);  // f16 d of rows 4s..4s+3
+#pragma unroll
+        for (int u = 0; u < NC; ++u) r.adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
+    };
+    auto compute = [&](const W &r, int b) {
+        const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
+        const FoldScales fs = fold_scales(r.scw);
+        const v4i zero = {0, 0, 0, 0};
+        v4i ah[NC], al[NC];
+#pragma unroll
+        for (int u = 0; u < NC; ++u) ah[u] = al[u] = zero;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            long a_lo, a_hi;
+            fold_digits((uint64_t)unpack_codes(nib, hb, c), fs, a_lo, a_hi);
+#pragma unroll
+            for (int u = 0; u < NC; ++u) {
+                ah[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c % BQ][u], ah[u], 0, 0, 0);
+                al[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c % BQ][u], al[u], 0, 0, 0);
+            }
+            aload(c + BQ < 8 ? b : b + 1, (c + BQ) % 8);
+        }
+        const float d4[4] = {f16_bits_to_f32((uint16_t)(r.dw.x & 0xFFFF)), f16_bits_to_f32((uint16_t)(r.dw.x >> 16)),
+                             f16_bits_to_f32((uint16_t)(r.dw.y & 0xFFFF)), f16_bits_to_f32((uint16_t)(r.dw.y >> 16))};
+#pragma unroll
+        for (int u = 0; u < NC; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int aux = ah[u][v] * 256 + al[u][v];
+                acc[u][v] = __builtin_fmaf(d4[v] * r.adb[u], (float)aux, acc[u][v]);
+            }
+    };
+    if constexpr (LDSA) {
+        // the class planes come from LDS (lgkmcnt), so the next block's
+        // weights can be in flight a whole block ahead without a class-plane
+        // wait also waiting for them; the scheduling barriers keep the
+        // compiler from sinking those loads back to their first use
+        W ra, rb;
+        wload(ra, b0);
+        for (int b = b0; b < b1; b += 2) {
+            wload(rb, min(b + 1, last));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ra, b);
+            if (b + 1 >= b1) break;
+            wload(ra, min(b + 2, last));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(rb, b + 1);
+        }
+    } else {
+        for (int b = b0; b < b1; ++b) {
+            const uint8_t *sg = seg + (size_t)b * SEG_BYTES;
+            const uint4 q0 = *(const uint4 *)(sg + 16 * lane);
+            const uint4 q1 = *(const uint4 *)(sg + SEG_PART + 16 * lane);
+            const uint4 q2 = *(const uint4 *)(sg + 2 * SEG_PART + 16 * lane);
+            const uint32_t scw = *(const uint32_t *)(sg + SEG_SC + 4 * lane);
+            const uint2 dw = *(const uint2 *)(sg + SEG_D + 8 * s);
+            float adb[NC];
+#pragma unroll
+            for (int u = 0; u < NC; ++u) adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
+            const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
+            const FoldScales fs = fold_scales(scw);
+            const v4i zero = {0, 0, 0, 0};
+            v4i ah[NC], al[NC];
+#pragma unroll
+            for (int u = 0; u < NC; ++u) ah[u] = al[u] = zero;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                long a_lo, a_hi;
+                fold_digits((uint64_t)unpack_codes(nib, hb, c), fs, a_lo, a_hi);
+#pragma unroll
+                for (int u = 0; u < NC; ++u) {
+                    ah[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, act[c % BQ][u], ah[u], 0, 0, 0);
+                    al[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, act[c % BQ][u], al[u], 0, 0, 0);
+                }
+                aload(c + BQ < 8 ? b : b + 1, (c + BQ) % 8);
+            }
+            const float d4[4] = {f16_bits_to_f32((uint16_t)(dw.x & 0xFFFF)), f16_bits_to_f32((uint16_t)(dw.x >> 16)),
+                                 f16_bits_to_f32((uint16_t)(dw.y & 0xFFFF)), f16_bits_to_f32((uint16_t)(dw.y >> 16))};
+#pragma unroll
+            for (int u = 0; u < NC; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int aux = ah[u][v] * 256 + al[u][v];
+                    acc[u][v] = __builtin_fmaf(d4[v] * adb[u], (float)aux, acc[u][v]);
+                }
+        }
+    }
+}
+
+// KS waves per work item (4 / KS items per workgroup). TWIN: the items are
+// twins (moe_group's twin records), else 16-token chunks (chunk records, or
+// the single group of grp_expert == nullptr).
+// LDSA: one 16-token chunk for the whole grid (the LM head at batch <= 16):
+// each workgroup first copies the chunk's quants (blocks x 4 KiB, dynamic
+// LDS) once, so the class-plane loads of every block read LDS instead of
+// going through the vector memory path (they outnumber the weight loads).
+template <int KS, bool TWIN, bool LDSA = false>
+__global__ __launch_bounds__(256) void q6k_mv_batched_fast(BatchParams pk) {
+    constexpr int IPW = 4 / KS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kc = wave % KS;
+    const int n = lane & 15, s = lane >> 4;
+    int item = (int)blockIdx.x * IPW + wave / KS;
+    BatchParams p = pk;
+    if (p.w2 && item >= p.items_per_mat) {
+        item -= p.items_per_mat;
+        p.w = p.w2;
+        p.y = p.y2;
+    }
+    bool live = item < p.items_per_mat;  // the grid's rounding to whole workgroups
+    int t = 0, sub = 0, st = 0, cnt = 0, start = 0, expert = 0, nc = 1;
+    if (live) {
+        t = item % p.tiles;
+        const int unit = item / p.tiles;
+        if (p.grp_expert) {
+            const GroupItem it = TWIN ? p.twin_info[unit] : p.sub_info[unit];  // expert -1: spare
+            live = it.expert >= 0;
+            st = it.st;
+            sub = it.sub;
+            cnt = it.count;
+            start = it.start;
+            expert = it.expert;
+            nc = TWIN && it.twin2 ? 2 : 1;
+        } else {
+            cnt = p.single_count;
+            sub = st = unit;
+            live = unit < (cnt + 15) / 16;
+        }
+    }
+    const int bpc = (p.blocks + KS - 1) / KS;
+    const int b0 = kc * bpc, b1 = min(p.blocks, b0 + bpc);
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    if constexpr (LDSA) {
+        const int n16 = p.blocks * CHUNK_BLOCK_BYTES / 16;
+        const uint4 *src = (const uint4 *)p.act_q;
+        for (int i = threadIdx.x; i < n16; i += blockDim.x) g_act_lds[i] = src[i];
+        __syncthreads();
+        if (live && b0 < b1) fast_tile_range<1, true>(p, lane, t, 0, expert, b0, b1, acc);
+    } else if (live && b0 < b1) {
+        if (nc == 2) fast_tile_range<2>(p, lane, t, sub, expert, b0, b1, acc);
+        else fast_tile_range<1>(p, lane, t, sub, expert, b0, b1, acc);
+    }
+    if constexpr (KS > 1) {
+        // every wave reaches the barrier (no early return above)
+        __shared__ float part[4][2][4][WAVE];
+        if (kc != 0) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) part[wave][u][v][lane] = acc[u][v];
+        }
+        __syncthreads();
+        if (kc != 0) return;
+#pragma unroll
+        for (int k = 1; k < KS; ++k)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] += part[wave + k][u][v][lane];
+    }
+    if (!live) return;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        if (u >= nc) break;
+        const int tok = 16 * (st + u) + n;  // this lane's token
+        const bool tok_ok = tok < cnt;
+        float bv = -INFINITY;  // arg-max candidate of this lane's rows (lowest row on ties)
+        int bi = 0x7FFFFFFF;
+        int nan_row = 0;       // a NaN logit in the tile voids the tile's certificate
+        if (tok_ok) {
+            const int pos = start + tok;
+            const int orow = p.pair_out ? p.pair_out[pos] : pos;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = t * TILE_ROWS + 4 * s + v;
+                if (row < p.rows) {
+                    p.y[(size_t)orow * p.ldy + row] = acc[u][v];
+                    if (!isnan(acc[u][v])) argmax_step(bv, bi, acc[u][v], row);
+                    else nan_row = 1;
+                }
+            }
+        }
+        if (p.amax_v) {
+            // the 4 lanes (s = 0..3) of each token: lanes n, n+16, n+32, n+48
+            argmax_step(bv, bi, __shfl_xor(bv, 16, WAVE), __shfl_xor(bi, 16, WAVE));
+            argmax_step(bv, bi, __shfl_xor(bv, 32, WAVE), __shfl_xor(bi, 32, WAVE));
+            nan_row |= __shfl_xor(nan_row, 16, WAVE);
+            nan_row |= __shfl_xor(nan_row, 32, WAVE);
+            if (s == 0 && tok_ok) {
+                p.amax_v[(size_t)tok * p.tiles + t] = bv;
+                p.amax_i[(size_t)tok * p.tiles + t] = nan_row ? -1 : bi;
+            }
+        }
+    }
+}
+
+
+
+// ---- LM head: certified arg-max over REDUCTION-tolerance logits -------------
+//
+// The fast batched kernel's logit F_r of row r and the reference's E_r are two
+// roundings of the same real value T_r = sum_b dd_b * sum_c aux_b[c] (dd_b =
+// f16(d_b) * a.d_b, the same float in both; aux integers exact in both):
+//   |E_r - T_r| <= gamma_{nb+10} S_r  (8 class sums of nb rounded products,
+//                                     then the 8-term class sum)
+//   |F_r - T_r| <= gamma_{nb+1} S_r   (nb fused multiply-adds)
+// with S_r = sum_b |dd_b| sum_c |aux_b[c]| <= 127 (1 + u) sum_b |a.d_b|
+// |f16(d_b)| sum_e |sc(e)(q_e - 32)| <= 127 (1 + u) D_a M_r, since every Q8_K
+// quant is at most 127 in magnitude; D_a = max_b |a.d_b| of the token and M_r
+// the weights' own sum, bounded per tile by q6k_tile_bound. So
+// |F_r - E_r| <= delta_t = 2 (2 nb + 12) u 127 D_a M_t (+ 2^-20 |F|, covering
+// the bound's own float rounding) for every row r of tile t (u = 2^-24).
+// Every row whose E_r could be the maximum then lies in a tile with
+// F_t + delta_t >= L = max_t (F_t - delta_t), F_t the tile's largest F.
+
+// One wave per tile.
+__global__ __launch_bounds__(256) void q6k_tile_bound(const uint8_t *w, int tiles, int blocks,
+                                                      float *mt) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tiles) return;
+    const int n = lane & 15;
+    float m = 0.0f;
+    for (int b = 0; b < blocks; ++b) {
+        const uint8_t *sg = w + ((size_t)t * blocks + b) * SEG_BYTES;
+        const uint4 q0 = *(const uint4 *)(sg + 16 * lane);
+        const uint4 q1 = *(const uint4 *)(sg + SEG_PART + 16 * lane);
+        const uint4 q2 = *(const uint4 *)(sg + 2 * SEG_PART + 16 * lane);
+        const uint32_t scw = *(const uint32_t *)(sg + SEG_SC + 4 * lane);
+        const uint16_t dh = *(const uint16_t *)(sg + SEG_D + 2 * n);
+        const uint32_t nib[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hb[4] = {q2.x, q2.y, q2.z, q2.w};
+        // the lane's 64 weights of row n: class c, byte kk = weight 8 (8 s + kk) + c,
+        // scale group 4 s + kk / 2 (byte kk / 2 of scw)
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint64_t codes = (uint64_t)unpack_codes(nib, hb, c);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const int q = (int)((codes >> (8 * kk)) & 0xFF) - 32;
+                const int sc = __builtin_amdgcn_sbfe(scw, 8 * (kk >> 1), 8);
+                acc += abs(sc * q);
+            }
+        }
+        acc += __shfl_xor(acc, 16, WAVE);
+        acc += __shfl_xor(acc, 32, WAVE);
+        m += fabsf(f16_bits_to_f32(dh)) * (float)acc;  // acc <= 2^20: exact
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+    if (lane == 0) mt[t] = m;
+}
+
+struct CertifyParams {
+    const uint8_t *w;      // tiled Q6_K [rows x blocks]
+    const int8_t *nq;      // [nseq][blocks * 256] natural Q8_K
+    const float *nd;       // [nseq][blocks]
+    const float *pv;       // [nseq][tiles] the fast kernel's tile candidates
+    const int *pi;         //   (row, or -1: a NaN logit in the tile)
+    const float *mt;       // [tiles] q6k_tile_bound
+    float *logits;         // [nseq][rows]
+    int32_t *ids;          // [nseq]
+    int rows, tiles, blocks;
+};
+
+// One 1024-thread workgroup per token. Its tiles' candidates are read once
+// (CERT_PT per thread kept in registers), the candidate tiles gathered in LDS,
+// and their exact recomputation spread over the 16 waves by (tile, block):
+// each wave computes one block's eight class terms of one tile into LDS (a
+// single round trip to memory for up to 16 / blocks tiles), then one wave per
+// tile folds them in block order, as dot_q6k_q8k does (the q6k_mv_b1 split-K
+// fold).
+constexpr int CERT_PT = 16;     // tiles per thread held in registers (beyond: re-read)
+constexpr int CERT_CAP = 1024;  // candidate list; more (no certificate) -> every tile
+constexpr int CERT_MAXB = 32;   // blocks per row (k <= 8192)
+
+__global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
+    const int u = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, s = lane >> 4;
+    const float *F = p.pv + (size_t)u * p.tiles;
+    const int *FI = p.pi + (size_t)u * p.tiles;
+    const float *ad = p.nd + (size_t)u * p.blocks;
+    const int8_t *aq = p.nq + (size_t)u * p.blocks * QK_K;
+    __shared__ float s_lo[16];
+    __shared__ int s_bad[16];
+    __shared__ int s_cand[CERT_CAP];
+    __shared__ int s_ncand;
+    // per round: blocks <= 16: entry e = (tile e / blocks, block e % blocks);
+    // blocks > 16: one tile, entry b = block b
+    __shared__ float s_terms[CERT_MAXB][TILE_ROWS][8];
+    if (tid == 0) s_ncand = 0;
+    // 1. the certified lower bound L of the largest exact logit
+    float fv[CERT_PT], dv[CERT_PT];
+    float lo = -INFINITY;
+    int bad = 0;
+    float da, cst;
+    {
+        // all of the thread's loads in flight at once: unconditional, at a
+        // clamped index, the out-of-range ones discarded afterwards
+        int fi[CERT_PT];
+        float mv[CERT_PT];
+#pragma unroll
+        for (int i = 0; i < CERT_PT; ++i) {
+            const int t = min(tid + i * (int)blockDim.x, p.tiles - 1);
+            fv[i] = F[t];
+            mv[i] = p.mt[t];
+            fi[i] = FI[t];
+        }
+        // D_a = max_b |a.d_b|: one load per lane (blocks <= 32), a wave max
+        da = lane < p.blocks ? fabsf(ad[lane]) : 0.0f;
+#pragma unroll
+        for (int o = 1; o < WAVE; o <<= 1) da = fmaxf(da, __shfl_xor(da, o, WAVE));
+        cst = 2.0f * (float)(2 * p.blocks + 12) * 0x1p-24f * 127.0f * da;
+#pragma unroll
+        for (int i = 0; i < CERT_PT; ++i) {
+            if (tid + i * (int)blockDim.x >= p.tiles) continue;
+            dv[i] = cst * mv[i] + 0x1p-20f * fabsf(fv[i]);
+            if (!isfinite(fv[i]) || !isfinite(dv[i]) || fi[i] < 0) bad = 1;
+            else lo = fmaxf(lo, fv[i] - dv[i]);
+        }
+    }
+    for (int t = tid + CERT_PT * (int)blockDim.x; t < p.tiles; t += blockDim.x) {
+        const float f = F[t], d = cst * p.mt[t] + 0x1p-20f * fabsf(f);
+        if (!isfinite(f) || !isfinite(d) || FI[t] < 0) bad = 1;
+        else lo = fmaxf(lo, f - d);
+    }
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        lo = fmaxf(lo, __shfl_xor(lo, o, WAVE));
+        bad |= __shfl_xor(bad, o, WAVE);
+    }
+    if (lane == 0) { s_lo[wave] = lo; s_bad[wave] = bad; }
+    __syncthreads();
+    for (int w = 0; w < 16; ++w) { lo = fmaxf(lo, s_lo[w]); bad |= s_bad[w]; }
+    // 2. the candidate tiles (tile 0 always: the reference's incumbent is row 0)
+    if (!bad) {
+        auto keep = [&](int t, float f, float d) {
+            if (t == 0 || f + d >= lo) {
+                const int at = atomicAdd(&s_ncand, 1);
+                if (at < CERT_CAP) s_cand[at] = t;
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < CERT_PT; ++i) {
+            const int t = tid + i * (int)blockDim.x;
+            if (t < p.tiles) keep(t, fv[i], dv[i]);
+        }
+        for (int t = tid + CERT_PT * (int)blockDim.x; t < p.tiles; t += blockDim.x)
+            keep(t, F[t], cst * p.mt[t] + 0x1p-20f * fabsf(F[t]));
+    }
+    __syncthreads();
+    const bool all = bad || s_ncand > CERT_CAP;
+    const int total = all ? p.tiles : s_ncand;
+    // 3. exact recomputation, (tile, block) pairs over the waves
+    const int per = p.blocks <= 16 ? 16 / p.blocks : 1;  // tiles per round
+    const int pairs = per * p.blocks;
+    const MaskSel msel = mask_selectors(n, (n >> 2) == s);
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    int nan0 = 0;
+    for (int r0 = 0; r0 < total; r0 += per) {
+        float se = 0.0f, so = 0.0f;
+        for (int e = wave; e < pairs; e += 16) {
+            const int ci = r0 + e / p.blocks, b = e % p.blocks;
+            if (ci >= total) break;
+            const int tt = all ? ci : s_cand[ci];
+            BlockRegs r;
+            load_block(r, p.w + ((size_t)tt * p.blocks + b) * SEG_BYTES, aq, ad, b, lane, n);
+            float te, to;
+            block_terms(r, msel, te, to);
+            const int slot = p.blocks <= 16 ? e : b;
+            s_terms[slot][n][2 * s] = te;
+            s_terms[slot][n][2 * s + 1] = to;
+        }
+        __syncthreads();
+        if (wave < per && r0 + wave < total) {
+            const int tt = all ? r0 + wave : s_cand[r0 + wave];
+            const int base = p.blocks <= 16 ? wave * p.blocks : 0;
+            for (int b = 0; b < p.blocks; ++b) {
+                se = se + s_terms[base + b][n][2 * s];
+                so = so + s_terms[base + b][n][2 * s + 1];
+            }
+            float cls[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
+                cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
+            }
+            float tot = -0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) tot = tot + cls[c];
+            const int row = tt * TILE_ROWS + n;
+            if (s == 0 && row < p.rows) {
+                p.logits[(size_t)u * p.rows + row] = tot;
+                if (!isnan(tot)) argmax_step(bv, bi, tot, row);
+                if (row == 0 && isnan(tot)) nan0 = 1;
+            }
+        }
+        __syncthreads();
+    }
+    wave_argmax(bv, bi, -INFINITY);
+    nan0 = __ballot(nan0 != 0) != 0 ? 1 : 0;
+    __shared__ float s_bv[16];
+    __shared__ int s_bi[16], s_nan[16];
+    if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; s_nan[wave] = nan0; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) {
+            argmax_step(bv, bi, s_bv[w], s_bi[w]);
+            nan0 |= s_nan[w];
+        }
+        p.ids[u] = (nan0 || bi == 0x7FFFFFFF) ? 0 : bi;
+    }
+}
+
 }  // namespace
 
 int g_tune_mv_ks = 0;
 int g_tune_mv_dot = 0;
 int g_tune_batched_twin = 1;
+int g_tune_fast_ks = 0;
+int g_tune_fast_lds = 1;
 
 namespace {
 
@@ -985,7 +1457,7 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
                           const int32_t *sub_start, const int32_t *pair_out, const int8_t *act_q,
                           const float *act_d, float *y, int ldy, int rows, int blocks,
                           int n_groups, int max_chunks, hipStream_t st, float *amax_v,
-                          int *amax_i, bool group_tables, const void *w2, float *y2) {
+                          int *amax_i, bool group_tables, const void *w2, float *y2, bool fast) {
     if (amax_v && grp_expert) return -1;
     // every item of the grids below indexes a record below max_chunks when
     // max_chunks >= n_groups (twins: ceil((max_chunks + n_groups) / 2) items)
@@ -1014,6 +1486,31 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
     p.blocks = blocks;
     p.n_groups = n_groups;
+    if (fast) {
+        // K split over ks waves (tune key fast_ks): one measured best on
+        // MI355X for both the prefill and the LM head shapes
+        const int ks = g_tune_fast_ks ? g_tune_fast_ks : 1;
+        const bool twin = grp_expert && g_tune_batched_twin;
+        if (grp_expert && !group_tables) return -1;
+        const long units = twin ? (max_chunks + n_groups + 1) / 2 : max_chunks;
+        const long items = (long)p.tiles * units;
+        if (items <= 0) return 0;
+        p.items_per_mat = (int)items;
+        const long all = w2 ? 2 * items : items;
+        const unsigned grid = (unsigned)((all * ks + 3) / 4);
+        const size_t lds = (size_t)blocks * CHUNK_BLOCK_BYTES;
+        if (!grp_expert && n_groups <= CHUNK_TOKENS && lds <= 65536 && g_tune_fast_lds) {
+            if (ks == 4) hipLaunchKernelGGL((q6k_mv_batched_fast<4, false, true>), dim3(grid), dim3(256), lds, st, p);
+            else if (ks == 2) hipLaunchKernelGGL((q6k_mv_batched_fast<2, false, true>), dim3(grid), dim3(256), lds, st, p);
+            else hipLaunchKernelGGL((q6k_mv_batched_fast<1, false, true>), dim3(grid), dim3(256), lds, st, p);
+        } else if (ks == 4 && twin) hipLaunchKernelGGL((q6k_mv_batched_fast<4, true>), dim3(grid), dim3(256), 0, st, p);
+        else if (ks == 4) hipLaunchKernelGGL((q6k_mv_batched_fast<4, false>), dim3(grid), dim3(256), 0, st, p);
+        else if (ks == 2 && twin) hipLaunchKernelGGL((q6k_mv_batched_fast<2, true>), dim3(grid), dim3(256), 0, st, p);
+        else if (ks == 2) hipLaunchKernelGGL((q6k_mv_batched_fast<2, false>), dim3(grid), dim3(256), 0, st, p);
+        else if (twin) hipLaunchKernelGGL((q6k_mv_batched_fast<1, true>), dim3(grid), dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((q6k_mv_batched_fast<1, false>), dim3(grid), dim3(256), 0, st, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (grp_expert && g_tune_batched_twin) {
         // twins: sum of ceil(ch/2) <= (sum of ch + n_groups) / 2
         const long items = (long)p.tiles * ((max_chunks + n_groups + 1) / 2);
@@ -1063,6 +1560,28 @@ int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStrea
     const int items = tiles * blocks;
     hipLaunchKernelGGL(q6k_dequant_tiled, dim3((items + 3) / 4), dim3(256), 0, st,
                        (const uint8_t *)w, rows, tiles, blocks, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace llamd
+
+namespace llamd {
+
+int launch_q6k_tile_bound(const void *w, int rows, int blocks, float *mt, hipStream_t st) {
+    const int tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
+    if (tiles <= 0 || blocks <= 0) return -1;
+    hipLaunchKernelGGL(q6k_tile_bound, dim3((tiles + 3) / 4), dim3(256), 0, st, (const uint8_t *)w,
+                       tiles, blocks, mt);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_lmhead_certify(const void *w, int rows, int blocks, int nseq, const int8_t *nq,
+                          const float *nd, const float *pv, const int *pi, const float *mt,
+                          float *logits, int32_t *ids, hipStream_t st) {
+    if (rows <= 0 || blocks <= 0 || blocks > CERT_MAXB || nseq <= 0) return -1;
+    CertifyParams p{(const uint8_t *)w, nq, nd, pv, pi, mt, logits, ids, rows,
+                    (rows + TILE_ROWS - 1) / TILE_ROWS, blocks};
+    hipLaunchKernelGGL(lmhead_certify, dim3(nseq), dim3(1024), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

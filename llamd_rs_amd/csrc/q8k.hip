@@ -36,7 +36,8 @@ __global__ __launch_bounds__(256) void q8k_quantize(const float *x, int8_t *qs, 
 // of its `fan` slots: slot_of[r * fan + k], or slot r when slot_of is null.
 __global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int rows, int blocks,
                                                            const int32_t *slot_of, int fan,
-                                                           int8_t *cq, float *cd) {
+                                                           int8_t *cq, float *cd, int8_t *nq,
+                                                           float *nd) {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= rows * blocks) return;
@@ -49,6 +50,8 @@ __global__ __launch_bounds__(256) void q8k_quantize_chunks(const float *x, int r
     int q[4];
     float dv;
     quantize_wave_q(v, lane, q, dv);
+    // optionally the reference's natural layout too, row r at nq[r][blocks*256]
+    if (nq) store_q8k(q, dv, lane, nq + (size_t)item * QK_K, nd + item, nullptr);
     const uint32_t dw = chunk_dword(q, lane);
     for (int k = 0; k < fan; ++k)
         store_chunk(dw, dv, lane, cq, cd, slot_of ? __builtin_amdgcn_readlane(my_slot, k) : r, b, blocks);
@@ -154,11 +157,12 @@ int launch_q8k_quantize(const float *x, int8_t *qs, float *d, int16_t *bsums, in
 }
 
 int launch_q8k_quantize_chunks(const float *x, int rows, int blocks, const int32_t *slot_of,
-                               int fan, int8_t *cq, float *cd, hipStream_t st) {
+                               int fan, int8_t *cq, float *cd, hipStream_t st, int8_t *nq,
+                               float *nd) {
     if (rows <= 0 || blocks <= 0) return 0;
-    if (fan < 1 || fan > WAVE) return -1;
+    if (fan < 1 || fan > WAVE || (!nq) != (!nd)) return -1;
     hipLaunchKernelGGL(q8k_quantize_chunks, dim3((rows * blocks + 3) / 4), dim3(256), 0, st, x,
-                       rows, blocks, slot_of, fan, cq, cd);
+                       rows, blocks, slot_of, fan, cq, cd, nq, nd);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

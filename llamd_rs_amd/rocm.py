@@ -372,15 +372,17 @@ class MoeLayer:
                                                      _ptr(w), _ptr(lg), nseq), "moe_forward_batch")
         return out, ids, w, lg
 
-    def prefill(self, x, ids, weights) -> np.ndarray:
-        """moe_ffn for n_tok tokens with the given routing [n_tok, n_used]."""
+    def prefill(self, x, ids, weights, reduction: bool = False) -> np.ndarray:
+        """moe_ffn for n_tok tokens with the given routing [n_tok, n_used].
+        reduction=True: the REDUCTION-tolerance GEMMs (LLAMD_HIP_REDUCTION);
+        otherwise bit-identical to the CPU path."""
         x = _f32(x).reshape(-1, self.n_embd)
         n_tok = x.shape[0]
         ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(n_tok, self.n_used)
         w = _f32(weights).reshape(n_tok, self.n_used)
         out = np.empty((n_tok, self.n_embd), np.float32)
-        check(lib().llamd_hip_moe_prefill_host(self._h, _ptr(x), _ptr(ids), _ptr(w), _ptr(out), n_tok),
-              "moe_prefill")
+        check(lib().llamd_hip_moe_prefill_host_ex(self._h, _ptr(x), _ptr(ids), _ptr(w), _ptr(out), n_tok,
+                                                  1 if reduction else 0), "moe_prefill")
         return out
 
     def stats(self) -> tuple[int, int]:
@@ -463,14 +465,17 @@ class LmHead:
     def handle(self):
         return self._h
 
-    def forward(self, x) -> tuple[np.ndarray, np.ndarray]:
+    def forward(self, x, reduction: bool = False) -> tuple[np.ndarray, np.ndarray]:
+        """logits [nseq, rows] and arg-max ids [nseq]. reduction=True
+        (LLAMD_HIP_REDUCTION, nseq > 1): logits within REDUCTION, ids still
+        the exact logits' arg-max."""
         x = np.atleast_2d(_f32(x))
         nseq = x.shape[0]
         if x.shape[1] != self.blocks * QK_K or nseq > self.max_seq:
             raise ValueError("x must be [nseq <= max_seq, k]")
         self._x.upload(x)
-        check(lib().llamd_hip_lmhead_forward(self._h, self._x.ptr, nseq, self._logits.ptr, self._ids.ptr),
-              "lmhead_forward")
+        check(lib().llamd_hip_lmhead_forward_ex(self._h, self._x.ptr, nseq, self._logits.ptr, self._ids.ptr,
+                                                1 if reduction else 0), "lmhead_forward")
         logits = self._logits.download(np.empty((nseq, self.rows), np.float32))
         ids = self._ids.download(np.empty(nseq, np.int32))
         return logits, ids

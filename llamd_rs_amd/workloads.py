@@ -13,8 +13,11 @@ rocprofv3 (--kernel-trace, --pmc) so a profile covers exactly one workload:
                  rotating
     lm_head_b1   the LM head call (151936x2048), batch 1 and 16
     lm_head_b16
+    lm_head_b16_reduction  the b=16 call with LLAMD_HIP_REDUCTION (tolerance
+                 logits, certified exact arg-max)
     moe_decode   one MoE decode layer per call, 4 layers rotating
     prefill      the expert-grouped FFN of 512 tokens, top-8 of 128, Zipf 1.1
+    prefill_reduction  the same with LLAMD_HIP_REDUCTION (tolerance GEMMs)
     decode       whole-token decode of a Qwen3-30B-A3B-shaped model cut to 4
                  layers (plain launches, no graph), positions 3..3+N
 """
@@ -70,7 +73,7 @@ def configs1_grouped(L, iters):
             c.close()
 
 
-def lm_head(L, iters, nseq):
+def lm_head(L, iters, nseq, flags=0):
     rows, k = 151936, 2048
     w = synth.q6k_matrix(4242, 0.02, rows, k)
     heads = []
@@ -80,7 +83,7 @@ def lm_head(L, iters, nseq):
     xb = rocm.DeviceBuffer.from_array(synth.normal(31, 1.0, 16 * k))
     lg, ids = rocm.DeviceBuffer(16 * rows * 4), rocm.DeviceBuffer(64)
     for i in range(iters):
-        if L.llamd_hip_lmhead_forward(heads[i % 2][1].handle, xb.ptr, nseq, lg.ptr, ids.ptr):
+        if L.llamd_hip_lmhead_forward_ex(heads[i % 2][1].handle, xb.ptr, nseq, lg.ptr, ids.ptr, flags):
             raise RuntimeError("lmhead")
     _sync(L)
 
@@ -104,7 +107,7 @@ def moe_decode(L, iters):
     _sync(L)
 
 
-def prefill(L, iters):
+def prefill(L, iters, flags=0):
     layers = _moe_layers(2)
     n_tok = 512
     xs = rocm.DeviceBuffer.from_array(synth.normal(700, 1.0, n_tok * 2048))
@@ -112,7 +115,7 @@ def prefill(L, iters):
     di, dw = rocm.DeviceBuffer.from_array(ids.astype(np.int32)), rocm.DeviceBuffer.from_array(w)
     out = rocm.DeviceBuffer(n_tok * 2048 * 4)
     for i in range(iters):
-        if L.llamd_hip_moe_prefill(layers[i % 2].handle, xs.ptr, di.ptr, dw.ptr, out.ptr, n_tok):
+        if L.llamd_hip_moe_prefill_ex(layers[i % 2].handle, xs.ptr, di.ptr, dw.ptr, out.ptr, n_tok, flags):
             raise RuntimeError("prefill")
     _sync(L)
 
@@ -144,8 +147,10 @@ WORKLOADS = {
     "configs1_grouped": configs1_grouped,
     "lm_head_b1": lambda L, n: lm_head(L, n, 1),
     "lm_head_b16": lambda L, n: lm_head(L, n, 16),
+    "lm_head_b16_reduction": lambda L, n: lm_head(L, n, 16, 1),
     "moe_decode": moe_decode,
     "prefill": prefill,
+    "prefill_reduction": lambda L, n: prefill(L, n, 1),
     "decode": decode,
 }
 
