@@ -1066,6 +1066,148 @@ __global__ __launch_bounds__(256) void q6k_mv_batched_fast(BatchParams pk) {
 
 
 
+// The grouped kernel with the activations staged in LDS. A workgroup's 4
+// waves are 4 tiles of one unit (tiles % 4 == 0), so they read the same
+// chunks: per block, the unit's NC x 4 KiB of class planes are copied once
+// into LDS by direct global-to-LDS loads (1 KiB per wave instruction, no
+// registers), double-buffered, and every wave reads its planes from LDS. The
+// next block's planes and weights are in flight while the current block is
+// computed; one barrier per block hands the buffer over.
+using lds_ptr = __attribute__((address_space(3))) void *;
+
+template <int NC>
+__device__ __forceinline__ void fast_tile_staged(const BatchParams &p, int lane, int wave, int t,
+                                                 int sub0, int expert, float acc[2][4]) {
+    const int n = lane & 15, s = lane >> 4;
+    const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
+    const size_t chunk_q = (size_t)p.blocks * CHUNK_BLOCK_BYTES, chunk_d = (size_t)p.blocks * CHUNK_TOKENS;
+    const int8_t *gq = p.act_q + (size_t)sub0 * chunk_q;
+    const float *ad = p.act_d + (size_t)sub0 * chunk_d + n;
+    int8_t *lds = (int8_t *)g_act_lds;  // [2][NC][4096]
+    constexpr int BUF = NC * CHUNK_BLOCK_BYTES;
+    // this wave's share of a block's planes: NC KiB, one 16-byte piece per lane
+    auto stage = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int off = (wave * NC + i) * 1024;  // within the NC x 4 KiB
+            const int u = off / CHUNK_BLOCK_BYTES, o = off % CHUNK_BLOCK_BYTES;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(gq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + o + 16 * lane),
+                (lds_ptr)(lds + (b & 1) * BUF + off), 16, 0, 0);
+        }
+    };
+    struct W {
+        uint4 q0, q1, q2;
+        uint32_t scw;
+        uint2 dw;
+        float adb[NC];
+    };
+    auto wload = [&](W &r, int b) {
+        const uint8_t *sg = seg + (size_t)b * SEG_BYTES;
+        r.q0 = *(const uint4 *)(sg + 16 * lane);
+        r.q1 = *(const uint4 *)(sg + SEG_PART + 16 * lane);
+        r.q2 = *(const uint4 *)(sg + 2 * SEG_PART + 16 * lane);
+        r.scw = *(const uint32_t *)(sg + SEG_SC + 4 * lane);
+        r.dw = *(const uint2 *)(sg + SEG_D + 8 * s);
+#pragma unroll
+        for (int u = 0; u < NC; ++u) r.adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
+    };
+    auto compute = [&](const W &r, int b) {
+        const int8_t *aq = lds + (b & 1) * BUF + n * 32 + 8 * s;
+        const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
+        const FoldScales fs = fold_scales(r.scw);
+        const v4i zero = {0, 0, 0, 0};
+        v4i ah[NC], al[NC];
+#pragma unroll
+        for (int u = 0; u < NC; ++u) ah[u] = al[u] = zero;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            long a_lo, a_hi;
+            fold_digits((uint64_t)unpack_codes(nib, hb, c), fs, a_lo, a_hi);
+#pragma unroll
+            for (int u = 0; u < NC; ++u) {
+                const long av = *(const long *)(aq + u * CHUNK_BLOCK_BYTES + 512 * c);
+                ah[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, av, ah[u], 0, 0, 0);
+                al[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, av, al[u], 0, 0, 0);
+            }
+        }
+        const float d4[4] = {f16_bits_to_f32((uint16_t)(r.dw.x & 0xFFFF)), f16_bits_to_f32((uint16_t)(r.dw.x >> 16)),
+                             f16_bits_to_f32((uint16_t)(r.dw.y & 0xFFFF)), f16_bits_to_f32((uint16_t)(r.dw.y >> 16))};
+#pragma unroll
+        for (int u = 0; u < NC; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int aux = ah[u][v] * 256 + al[u][v];
+                acc[u][v] = __builtin_fmaf(d4[v] * r.adb[u], (float)aux, acc[u][v]);
+            }
+    };
+    // the block's planes must be in LDS (this wave's pieces landed, every
+    // wave past the barrier) before any wave reads them; the barrier also
+    // keeps a buffer from being refilled while a wave still reads it
+    auto handover = [&]() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+    const int last = p.blocks - 1;
+    W ra, rb;
+    stage(0);
+    wload(ra, 0);
+    handover();
+    for (int b = 0; b < p.blocks; b += 2) {
+        if (b + 1 <= last) stage(b + 1);
+        wload(rb, min(b + 1, last));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ra, b);
+        handover();
+        if (b + 1 > last) break;
+        if (b + 2 <= last) stage(b + 2);
+        wload(ra, min(b + 2, last));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(rb, b + 1);
+        handover();
+    }
+}
+
+// One wave per (unit, tile), 4 tiles of one unit per workgroup; TWIN as in
+// q6k_mv_batched_fast. Dynamic LDS: 2 x (TWIN ? 2 : 1) x 4 KiB.
+template <bool TWIN>
+__global__ __launch_bounds__(256) void q6k_mv_batched_fast_staged(BatchParams pk) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, s = lane >> 4;
+    int item = (int)blockIdx.x * 4 + wave;
+    BatchParams p = pk;
+    if (p.w2 && item >= p.items_per_mat) {
+        item -= p.items_per_mat;
+        p.w = p.w2;
+        p.y = p.y2;
+    }
+    // the workgroup's 4 items share their unit (tiles % 4 == 0), so these
+    // exits are uniform over the workgroup and no barrier below is skipped
+    // by some waves only
+    if (item >= p.items_per_mat) return;
+    const int t = item % p.tiles;
+    const GroupItem it = TWIN ? p.twin_info[item / p.tiles] : p.sub_info[item / p.tiles];
+    if (it.expert < 0) return;
+    const int nc = TWIN && it.twin2 ? 2 : 1;
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    if (nc == 2) fast_tile_staged<2>(p, lane, wave, t, it.sub, it.expert, acc);
+    else fast_tile_staged<1>(p, lane, wave, t, it.sub, it.expert, acc);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        if (u >= nc) break;
+        const int tok = 16 * (it.st + u) + n;
+        if (tok >= it.count) continue;
+        const int pos = it.start + tok;
+        const int orow = p.pair_out ? p.pair_out[pos] : pos;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = t * TILE_ROWS + 4 * s + v;
+            if (row < p.rows) p.y[(size_t)orow * p.ldy + row] = acc[u][v];
+        }
+    }
+}
+
 // ---- LM head: certified arg-max over REDUCTION-tolerance logits -------------
 //
 // The fast batched kernel's logit F_r of row r and the reference's E_r are two
@@ -1499,7 +1641,11 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
         const long all = w2 ? 2 * items : items;
         const unsigned grid = (unsigned)((all * ks + 3) / 4);
         const size_t lds = (size_t)blocks * CHUNK_BLOCK_BYTES;
-        if (!grp_expert && n_groups <= CHUNK_TOKENS && lds <= 65536 && g_tune_fast_lds) {
+        if (grp_expert && ks == 1 && p.tiles % 4 == 0 && g_tune_fast_lds) {
+            const size_t slds = (size_t)2 * (twin ? 2 : 1) * CHUNK_BLOCK_BYTES;
+            if (twin) hipLaunchKernelGGL(q6k_mv_batched_fast_staged<true>, dim3(grid), dim3(256), slds, st, p);
+            else hipLaunchKernelGGL(q6k_mv_batched_fast_staged<false>, dim3(grid), dim3(256), slds, st, p);
+        } else if (!grp_expert && n_groups <= CHUNK_TOKENS && lds <= 65536 && g_tune_fast_lds) {
             if (ks == 4) hipLaunchKernelGGL((q6k_mv_batched_fast<4, false, true>), dim3(grid), dim3(256), lds, st, p);
             else if (ks == 2) hipLaunchKernelGGL((q6k_mv_batched_fast<2, false, true>), dim3(grid), dim3(256), lds, st, p);
             else hipLaunchKernelGGL((q6k_mv_batched_fast<1, false, true>), dim3(grid), dim3(256), lds, st, p);
