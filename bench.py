@@ -74,6 +74,54 @@ class Timer:
             self.L.llamd_hip_event_destroy(e)
 
 
+KERNEL_CLOCK_HZ = 100e6  # s_memrealtime on gfx950
+
+
+def clocked_region(L, rocm, many, names, steps, warmup):
+    """The headline's timed region once more with the in-kernel clock on
+    (llamd_hip_kernel_clock): each q6k_mv_b1 launch records its earliest
+    workgroup start and latest wave end, inside the same back-to-back
+    enqueue. Returns per-shape mean kernel durations, their sum per step, the
+    mean gap between one launch's end and the next one's start, and the
+    region's HIP-event time (the clock's frequency is checked against it)."""
+    n = len(names) * steps
+    rec = 2048  # words per launch record: 1024 wave starts, then 1024 wave ends
+    buf = rocm.DeviceBuffer.from_array(np.zeros(rec * n, np.uint64))
+    warm, timed = many(names, 0, warmup), many(names, warmup, steps)
+    if warm():
+        raise RuntimeError("matvec_many failed")
+    sync(L)
+    if L.llamd_hip_kernel_clock(buf.ptr, n):
+        raise RuntimeError("kernel clock")
+    try:
+        t = Timer(L)
+        t.rec(0)
+        if timed():
+            raise RuntimeError("matvec_many failed")
+        t.rec(1)
+        sync(L)
+        ms_ = t.ms(0, 1)
+        t.close()
+    finally:
+        L.llamd_hip_kernel_clock(None, 0)
+    got = buf.download(np.empty(rec * n, np.uint64)).reshape(n, 2, rec // 2)
+    buf.close()
+    starts = np.where(got[:, 0] > 0, got[:, 0], np.iinfo(np.uint64).max)
+    st, en = starts.min(axis=1).astype(np.float64), got[:, 1].max(axis=1).astype(np.float64)
+    dur = (en - st) / KERNEL_CLOCK_HZ * 1e6
+    gaps = (st[1:] - en[:-1]) / KERNEL_CLOCK_HZ * 1e6
+    span = (en[-1] - st[0]) / KERNEL_CLOCK_HZ * 1e3
+    per = dur.reshape(steps, len(names))
+    return {"us_per_launch": {nm: round(float(per[:, j].mean()), 3) for j, nm in enumerate(names)},
+            "p10_p90_us": [round(float(np.percentile(dur, 10)), 3), round(float(np.percentile(dur, 90)), 3)],
+            "kernel_us_per_step": round(float(per.sum(axis=1).mean()), 3),
+            "gap_us": round(float(gaps.mean()), 3),
+            "event_us_per_step": round(ms_ / steps * 1e3, 3),
+            "clock_span_over_event": round(float(span / ms_), 4),
+            "how": "llamd_hip_kernel_clock: s_memrealtime at every wave's start and end (plain vector "
+                   "stores, one word per wave), the same K steps enqueued back to back once more"}
+
+
 def sync(L):
     if L.llamd_fwd_sync() or L.llamd_fwd_last_error():
         from llamd_rs_amd._lib import last_error
@@ -138,6 +186,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="skip the large extra configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the in-kernel clock region (counter runs: its records add writes)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--eager", action="store_true",
                     help="plain launches everywhere, no graph replay: for rocprofv3 kernel traces, "
@@ -237,6 +287,7 @@ def main():
     # same command reproduces the figure. The graph-replay figure (launch
     # overhead hidden further) follows in extra.
     ms = time_many([sh[0] for sh in shapes], K, W)
+    in_situ = None if args.no_clock else clocked_region(L, rocm, many, [sh[0] for sh in shapes], K, W)
     bytes_step = sum(per_shape_bytes.values())
     value = bytes_step * K / (ms * 1e-3) / 1e9
     log(f"configs[1] step: {ms / K * 1e3:.2f} us, {value:.1f} GB/s")
@@ -300,7 +351,8 @@ def main():
                 "kernel": "q6k_mv_b1", "bytes_per_launch": bytes_launch,
                 "avg_launch_us": round(avg_us, 3), "launches": launches,
                 "profile": "profiles/q6k_mv_b1.configs1.kernel_trace.txt",
-                "traffic_source": "profiles/q6k_mv_b1.configs1.hbm_traffic.txt"}
+                "traffic_source": "profiles/q6k_mv_b1.configs1.hbm_traffic.txt",
+                "in_situ": in_situ}
     for lst in copies.values():
         for c in lst:
             c.close()

@@ -513,6 +513,18 @@ int llamd_hip_lmhead_forward_noalloc(const void *d_w, int rows, int blocks, cons
 size_t llamd_hip_lmhead_noalloc_scratch_bytes(void);
 
 /* ---- timing on the library stream ---------------------------------------- */
+/* Diagnostics, not in the reference. While d_slots is set, every Q6_K
+ * batch-1 matvec launch (q6k_mv_b1: llamd_fwd_matvec, _grouped, _x3, the LM
+ * head at batch 1, ...) records into the next of n_slots device records, in
+ * turn: record r is 2048 uint64 words at d_slots + 2048 r; wave w of the grid
+ * (w < 1024) stores its start at word w and its end at word 1024 + w, in
+ * s_memrealtime ticks (100 MHz on gfx950). The launch's duration inside the
+ * caller's back-to-back enqueue (not a tracer's isolated dispatch) is then
+ * max(ends) - min(starts) over the words written; the caller zeroes the
+ * records first. NULL turns it off. Not for captured graphs (the record is
+ * chosen at launch). */
+int llamd_hip_kernel_clock(unsigned long long *d_slots, int n_slots);
+
 /* Not in the reference (its llamd_rocm_matvec_bench, llamd.hip:1101-1148,
  * times one kernel; these let the caller bracket any queued sequence). */
 void *llamd_hip_event_create(void);

@@ -123,6 +123,7 @@ SIGNATURES = {
     "llamd_hip_lmhead_destroy": (None, [vp]),
     "llamd_hip_lmhead_forward": (i32, [vp, vp, i32, vp, vp]),
     "llamd_hip_lmhead_forward_ex": (i32, [vp, vp, i32, vp, vp, i32]),
+    "llamd_hip_kernel_clock": (i32, [vp, i32]),
     "llamd_hip_lmhead_forward_noalloc": (i32, [vp, i32, i32, vp, i32, vp, vp]),
     "llamd_hip_lmhead_noalloc_scratch_bytes": (sz, []),
     "llamd_hip_event_create": (vp, []),

@@ -71,7 +71,27 @@ struct MvParams {
     // optional per-tile arg-max candidates (one segment): [n_slots][tiles]
     float *amax_v;
     int *amax_i;
+    // optional in-kernel clock (llamd_hip_kernel_clock): the launch's record
+    unsigned long long *clk;
 };
+
+// In-kernel clock: wave w (flat index over the grid) stores its start at
+// clk[w] and its end at clk[CLOCK_WAVES + w], s_memrealtime ticks, with plain
+// vector stores (one writer per word: no contention, no atomics). The end is
+// stored on every exit of the kernel.
+constexpr int CLOCK_WAVES = 1024;
+struct ClockEnd {
+    unsigned long long *clk;  // this wave's start word, or null
+    __device__ ~ClockEnd() {
+        if (clk && (threadIdx.x & 63) == 0) clk[CLOCK_WAVES] = __builtin_amdgcn_s_memrealtime();
+    }
+};
+__device__ __forceinline__ unsigned long long *clock_start(unsigned long long *rec) {
+    const int w = (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    if (!rec || w >= CLOCK_WAVES) return nullptr;
+    if ((threadIdx.x & 63) == 0) rec[w] = __builtin_amdgcn_s_memrealtime();
+    return rec + w;
+}
 
 // One (slot, 16-row tile) item per KS waves of a 4-wave (KS = 8: 8-wave) workgroup; wave kc of
 // the item takes blocks [kc*bpc, (kc+1)*bpc) with the next block's loads in
@@ -90,6 +110,7 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
     asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.y), "s"(p.seg0.rows), "s"(p.seg0.tiles),
                  "s"(p.aq), "s"(p.ad), "s"(p.ids), "s"(p.expert_stride), "s"(p.items),
                  "s"(p.blocks), "s"(p.act_per_slot));
+    const ClockEnd clock_end{clock_start(p.clk)};
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int kc = wave % KS;
     const int local = wave / KS;
@@ -1483,7 +1504,16 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
     }
 }
 
-int launch_b1(const MvParams &p, hipStream_t st) {
+// llamd_hip_kernel_clock: slots [n][2] for the q6k_mv_b1 launches, in turn
+unsigned long long *g_clk_slots = nullptr;
+int g_clk_n = 0, g_clk_next = 0;
+
+int launch_b1(const MvParams &pin, hipStream_t st) {
+    MvParams p = pin;
+    if (g_clk_slots) {
+        p.clk = g_clk_slots + 2 * (size_t)CLOCK_WAVES * g_clk_next;
+        g_clk_next = (g_clk_next + 1) % g_clk_n;
+    }
     if (p.amax_v && g_tune_mv_dot) launch_b1_n<1, true, true>(p, st);
     else if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
     else if (p.n_seg == 1 && g_tune_mv_dot) launch_b1_n<1, false, true>(p, st);  // VALU dot products
@@ -1732,3 +1762,11 @@ int launch_lmhead_certify(const void *w, int rows, int blocks, int nseq, const i
 }
 
 }  // namespace llamd
+
+extern "C" int llamd_hip_kernel_clock(unsigned long long *d_slots, int n_slots) {
+    if (d_slots && n_slots <= 0) return -1;
+    llamd::g_clk_slots = d_slots;
+    llamd::g_clk_n = d_slots ? n_slots : 0;
+    llamd::g_clk_next = 0;
+    return 0;
+}
