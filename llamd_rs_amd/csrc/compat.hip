@@ -163,7 +163,13 @@ __global__ __launch_bounds__(256) void bias_sums(const int8_t *qs, uint8_t *qb, 
 // layer.rs:62-79). Then NeoX rotation with the table row of pos
 // (a*cos - b*sin, a*sin + b*cos), in place; with kc, the rotated head and the
 // matching v head are also stored at row pos of the sequence's cache slice.
-// A position outside the table writes NaN and stores nothing.
+// The table (host libm: cosf / sinf of pos / powf(base, 2i/hd), the CPU
+// path's own calls) covers positions below cs_rows; a position past it is
+// rotated with theta = pos / den[i] (the table's denominators, so theta is
+// the CPU's bit for bit) and the device's sincosf, within a few ulp of the
+// CPU's cos / sin (no table, so any position a cache holds works). A
+// negative position (device meta) writes NaN and stores nothing; a position
+// at or past cache_rows is rotated but not stored.
 __global__ __launch_bounds__(64) void head_norm_rope(HeadRopeArgs a) {
     __shared__ __align__(16) float sq[256];
     __shared__ float buf[256];
@@ -181,17 +187,24 @@ __global__ __launch_bounds__(64) void head_norm_rope(HeadRopeArgs a) {
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const bool ok = pos >= 0 && pos < a.cs_rows;
-    const float2 *row = a.cs + (size_t)(ok ? pos : 0) * half;
+    const bool ok = pos >= 0;
+    const bool in_table = ok && pos < a.cs_rows;
+    const float2 *row = a.cs + (size_t)(in_table ? pos : 0) * half;
     float *kc = nullptr, *vc = nullptr;
-    if (a.kc && ok) {
+    if (a.kc && ok && pos < a.cache_rows) {
         const size_t o = (size_t)s * a.cache_seq_stride + (size_t)pos * a.kv_dim + (size_t)hh * hd;
         kc = a.kc + o;
         vc = a.vc + o;
     }
     for (int i = lane; i < half; i += WAVE) {
         const float p = buf[i], q = buf[i + half];
-        const float2 c = row[i];
+        float2 c;
+        if (in_table) {
+            c = row[i];
+        } else {
+            const float theta = (float)pos / a.den[i];
+            sincosf(theta, &c.y, &c.x);
+        }
         float lo = p * c.x - q * c.y;
         float hi = p * c.y + q * c.x;
         if (!ok) lo = hi = __builtin_nanf("");

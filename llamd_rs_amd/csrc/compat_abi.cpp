@@ -71,10 +71,13 @@ struct RopeTab {
     int hd;
     uint32_t base_bits;
     int rows;
-    float2 *d;
+    float2 *d;  // [rows][hd / 2], then den [hd / 2] floats
 };
 std::vector<RopeTab> g_rope;
-std::vector<void *> g_retired;  // superseded buffers a captured graph may still read
+// Superseded scratch buffers a captured graph may still read, kept until the
+// process ends. Scratch only grows by at least doubling, so together they
+// never exceed the live scratch's size.
+std::vector<void *> g_retired;
 
 void *g_scr = nullptr;
 size_t g_scr_cap = 0;
@@ -125,20 +128,22 @@ void *scratch(size_t bytes) {
 
 // cos / sin of theta = pos / powf(base, 2i / hd) for pos in [0, rows) and
 // i < hd / 2, with the host libm -- the calls the reference CPU path makes
-// (crates/llamd-cpu/src/lib.rs:183-205, freq_scale 1).
-const float2 *rope_table(int hd, float base, int need, int *rows_out) {
+// (crates/llamd-cpu/src/lib.rs:183-205, freq_scale 1) -- followed by the
+// denominators powf(base, 2i / hd), with which head_norm_rope rotates the
+// positions past the table on the device. One table of ROPE_DEFAULT_ROWS
+// rows per (head_dim, base), made once: no position rebuilds it.
+const float2 *rope_table(int hd, float base, int *rows_out, const float **den_out) {
     std::lock_guard<std::mutex> lk(g_cmu);
     uint32_t bits;
     memcpy(&bits, &base, 4);
-    RopeTab *t = nullptr;
-    for (auto &r : g_rope)
-        if (r.hd == hd && r.base_bits == bits) t = &r;
-    if (t && t->rows >= need) {
-        *rows_out = t->rows;
-        return t->d;
-    }
-    const int rows = std::max({need, ROPE_DEFAULT_ROWS, t ? 2 * t->rows : 0});
     const int half = hd / 2;
+    for (auto &r : g_rope)
+        if (r.hd == hd && r.base_bits == bits) {
+            *rows_out = r.rows;
+            *den_out = (const float *)(r.d + (size_t)r.rows * half);
+            return r.d;
+        }
+    const int rows = ROPE_DEFAULT_ROWS;
     std::vector<float> den(half);
     for (int i = 0; i < half; ++i) den[i] = powf(base, 2.0f * (float)i / (float)hd);
     std::vector<float2> cs((size_t)rows * half);
@@ -151,21 +156,18 @@ const float2 *rope_table(int hd, float base, int need, int *rows_out) {
     }
     float2 *d = nullptr;
     hipStream_t sd = side();
-    if (!sd || hipMalloc(&d, cs.size() * sizeof(float2)) != hipSuccess ||
-        hipMemcpyAsync(d, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice, sd) !=
-            hipSuccess ||
+    const size_t tab_bytes = cs.size() * sizeof(float2);
+    if (!sd || hipMalloc(&d, tab_bytes + half * sizeof(float)) != hipSuccess ||
+        hipMemcpyAsync(d, cs.data(), tab_bytes, hipMemcpyHostToDevice, sd) != hipSuccess ||
+        hipMemcpyAsync((char *)d + tab_bytes, den.data(), half * sizeof(float), hipMemcpyHostToDevice,
+                       sd) != hipSuccess ||
         hipStreamSynchronize(sd) != hipSuccess) {
         set_error("rope table: device copy failed");
         return nullptr;
     }
-    if (t) {
-        g_retired.push_back(t->d);
-        t->d = d;
-        t->rows = rows;
-    } else {
-        g_rope.push_back(RopeTab{hd, bits, rows, d});
-    }
+    g_rope.push_back(RopeTab{hd, bits, rows, d});
     *rows_out = rows;
+    *den_out = (const float *)((char *)d + tab_bytes);
     return d;
 }
 
@@ -393,13 +395,14 @@ int bench_matvec(const void *w, const size_t *off, const int8_t *qs, const float
 
 void head_rope(float *x, const float *w, const float *v, float *kc, float *vc, int n_heads, int hd,
                int kv_dim, size_t cache_stride, const int32_t *pos_p, int pos_stride, int pos_fixed,
-               int table_rows, int nseq, float base, float eps) {
+               int cache_rows, int nseq, float base, float eps) {
     REFUSE_IF(!x || n_heads <= 0 || hd <= 0 || hd % 2 || hd > 256 || nseq <= 0,
               "rope: n_head %d, head_dim %d (even, at most 256), nseq %d", n_heads, hd, nseq);
     REFUSE_IF(kc && (!vc || !v || kv_dim != n_heads * hd),
               "k_norm_rope_store: kv_dim %d must be n_head_kv * head_dim = %d", kv_dim, n_heads * hd);
     int rows = 0;
-    const float2 *cs = rope_table(hd, base, table_rows, &rows);
+    const float *den = nullptr;
+    const float2 *cs = rope_table(hd, base, &rows, &den);
     if (!cs) return fwd_refused();
     HeadRopeArgs a{};
     a.x = x;
@@ -407,6 +410,17 @@ void head_rope(float *x, const float *w, const float *v, float *kc, float *vc, i
     a.eps = eps;
     a.cs = cs;
     a.cs_rows = rows;
+    a.den = den;
+    // the cache slice's rows: max_kv (batched), else the rows left in kc's
+    // allocation when the library made it, else the default table's length
+    a.cache_rows = ROPE_DEFAULT_ROWS;
+    if (kc) {
+        uintptr_t a0, a1;
+        std::lock_guard<std::mutex> lk(g_cmu);
+        if (alloc_range((uintptr_t)kc, &a0, &a1))
+            a.cache_rows = (int)std::min<size_t>((a1 - (uintptr_t)kc) / ((size_t)kv_dim * sizeof(float)), INT_MAX);
+    }
+    if (cache_rows > 0) a.cache_rows = cache_rows;
     a.pos_p = pos_p;
     a.pos_stride = pos_stride;
     a.pos_fixed = pos_fixed;
@@ -582,8 +596,8 @@ void llamd_fwd_embed_meta(const void *table, const int32_t *meta, float *out, in
 
 void llamd_fwd_rope(float *x, int pos, int n_head, int hd, float freq_base) {
     REFUSE_IF(pos < 0, "rope: position %d", pos);
-    head_rope(x, nullptr, nullptr, nullptr, nullptr, n_head, hd, 0, 0, nullptr, 0, pos, pos + 1, 1,
-              freq_base, 0.0f);
+    head_rope(x, nullptr, nullptr, nullptr, nullptr, n_head, hd, 0, 0, nullptr, 0, pos, 0, 1, freq_base,
+              0.0f);
 }
 
 void llamd_fwd_norm_rope(float *x, const float *w, int n_head, int hd, const int32_t *meta,

@@ -277,11 +277,14 @@ struct HeadRopeArgs {
     float eps;
     const float2 *cs;         // [cs_rows][hd / 2] (cos, sin)
     int cs_rows;
+    const float *den;         // [hd / 2] base^(2i/hd) (the table's): positions
+                              // at or past cs_rows are rotated on the device
     const int32_t *pos_p;     // pos of sequence s at pos_p[s * pos_stride]
     int pos_stride;
     int pos_fixed;            // without pos_p: this position (< 0: pos = s)
     int n_heads, hd;
     float *kc, *vc;           // null: no store
+    int cache_rows;           // positions the cache slice holds (no store at or past it)
     const float *v;           // [nseq][n_heads][hd] with kc
     int kv_dim;               // n_heads * hd
     size_t cache_seq_stride;  // floats between sequences' cache slices

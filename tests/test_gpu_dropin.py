@@ -599,6 +599,60 @@ def test_rope_norm_and_cache_store_exact(gpu):
         assert bits_equal(vc2[s, p], v2[s * kv_dim:(s + 1) * kv_dim])
 
 
+def test_rope_past_the_table(gpu):
+    """Positions at and past the 32768-row cos / sin table (Qwen3-30B-A3B
+    allows 40960): the reference kernel computes theta for any position
+    (llamd_forward.hip:419-440). Below the table the rotation is the CPU's bit
+    for bit; past it theta = pos / powf(base, 2i/hd) is still the CPU's and
+    only the device sincosf differs, so every value is within REDUCTION of
+    CpuBackend::rope under close. The K store lands at its row when the cache
+    holds it and is skipped (no write outside the cache) when it does not."""
+    n_head, n_head_kv, hd, base, eps = 4, 2, 128, 1.0e6, 1e-6
+    kv_dim = n_head_kv * hd
+    q = (H.sample(n_head * hd, 41) * 2).astype(np.float32)
+    Qd = dev(gpu, q)
+
+    def near(got, want):
+        rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.maximum(np.abs(got), np.abs(want)), 1.0)
+        return rel.max() <= O.REDUCTION
+    for pos in (32767, 32768, 40959, 1_000_000):
+        Qd.upload(q)
+        L().llamd_fwd_rope(Qd.ptr, pos, n_head, hd, C.c_float(base))
+        sync()
+        got, want = down(Qd, q.size), O.rope(q, n_head, hd, pos, base)
+        assert near(got, want), pos
+        if pos < 32768:
+            assert bits_equal(got, want)
+    qw = (1 + 0.1 * H.sample(hd, 42)).astype(np.float32)
+    QW = dev(gpu, qw)
+    meta = dev(gpu, np.array([1, 40000], np.int32))
+    Qd.upload(q)
+    L().llamd_fwd_norm_rope(Qd.ptr, QW.ptr, n_head, hd, meta.ptr, C.c_float(base), C.c_float(eps))
+    sync()
+    assert near(down(Qd, q.size), O.rope(_qk(q, qw, n_head, hd, eps), n_head, hd, 40000, base))
+    # K store: a cache of 40001 rows holds position 40000; one of 39000 does not
+    k = (H.sample(kv_dim, 43) * 2).astype(np.float32)
+    v = H.sample(kv_dim, 44)
+    kw = (1 + 0.1 * H.sample(hd, 45)).astype(np.float32)
+    KW, Vd = dev(gpu, kw), dev(gpu, v)
+    kr = O.rope(_qk(k, kw, n_head_kv, hd, eps), n_head_kv, hd, 40000, base)
+    for rows in (40001, 39000):
+        Kd = dev(gpu, k)
+        KC, VC = gpu.DeviceBuffer(rows * kv_dim * 4), gpu.DeviceBuffer(rows * kv_dim * 4)
+        KC.upload(np.zeros(rows * kv_dim, np.float32))
+        VC.upload(np.zeros(rows * kv_dim, np.float32))
+        L().llamd_fwd_k_norm_rope_store(Kd.ptr, KW.ptr, Vd.ptr, KC.ptr, VC.ptr, n_head_kv, hd, kv_dim,
+                                        meta.ptr, C.c_float(base), C.c_float(eps))
+        sync()
+        assert near(down(Kd, kv_dim), kr)
+        kc = down(KC, rows * kv_dim).reshape(rows, kv_dim)
+        vc = down(VC, rows * kv_dim).reshape(rows, kv_dim)
+        if rows > 40000:
+            assert near(kc[40000], kr) and bits_equal(vc[40000], v)
+        else:
+            assert not kc.any() and not vc.any()
+
+
 def test_attention_exact(gpu):
     n_head, n_head_kv, hd, n_kv, max_kv = 32, 4, 128, 211, 512
     kv_dim = n_head_kv * hd
