@@ -227,7 +227,10 @@ void llamd_fwd_moe_combine_add(const float *down, const float *weights, const fl
 /* llamd_forward.hip:819-825; scratch_v/scratch_i hold nblocks partials. */
 void llamd_fwd_argmax(const float *x, int n, float *scratch_v, int32_t *scratch_i, int32_t *out,
                       int nblocks);
-/* llamd_forward.hip:792-796 (FMA accumulation; REDUCTION vs the reference). */
+/* llamd_forward.hip:792-796. Each row is the CPU path's sequential f32 fold
+ * (model.rs:253-262: rounded products added in order), bit for bit, when k is
+ * a multiple of 256 up to 2048 (the MoE router's shape); other k use FMA
+ * accumulation (REDUCTION). */
 void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int rows);
 /* Not in the reference (its Q8_0 path is CPU-only, model.rs:253-262): Q8_0
  * weight from llamd_hip_upload_q8_0 times an f32 activation. */
@@ -347,7 +350,8 @@ void llamd_b_attention(const float *q, const float *kc, const float *vc, float *
 /* llamd_batch.hip:954-960 */
 void llamd_b_add(const float *a, const float *b, float *o, int n);
 void llamd_b_silu_mul(const float *g, const float *u, float *o, int n);
-/* llamd_batch.hip:962-966 (FMA accumulation, as llamd_fwd_matvec_f32) */
+/* llamd_batch.hip:962-966: as llamd_fwd_matvec_f32 for every sequence, in
+ * one launch (rows x nseq workgroups) when the fold applies */
 void llamd_b_matvec_f32(const float *w, const float *x, float *out, int k, int rows, int nseq);
 /* llamd_batch.hip:968-972 (n_expert <= 256) */
 void llamd_b_router(const float *logits, int n_expert, int n_used, int32_t *ids, float *weights,

@@ -783,12 +783,13 @@ void llamd_fwd_moe_combine_add(const float *d, const float *weights, const float
 
 void llamd_fwd_argmax(const float *x, int n, float *scratch_v, int32_t *scratch_i, int32_t *out,
                       int nblocks) {
-    (void)nblocks;  // partial count is chosen from n (argmax_parts); scratch must hold it
-    checked(launch_argmax(x, n, n, 1, scratch_v, (int *)scratch_i, out, stream()), "argmax");
+    // partials: one per 4096 values, at most nblocks (the caller's scratch size)
+    checked(nblocks <= 0 ? -1 : launch_argmax(x, n, n, 1, scratch_v, (int *)scratch_i, out, stream(), nblocks),
+            "argmax");
 }
 
 void llamd_fwd_matvec_f32(const float *w, const float *x, float *out, int k, int rows) {
-    checked(launch_f32_mv(w, x, out, rows, k, stream()), "matvec_f32");
+    checked(launch_matvec_f32_exact(w, x, out, rows, k, 1, stream()), "matvec_f32");
 }
 
 void llamd_hip_fwd_matvec_q8_0(const void *d_w, const float *d_x, float *d_out, int rows, int k) {

@@ -787,9 +787,7 @@ void llamd_b_silu_mul(const float *g, const float *u, float *o, int n) {
 
 void llamd_b_matvec_f32(const float *w, const float *x, float *out, int k, int rows, int nseq) {
     REFUSE_IF(!w || !x || !out || k <= 0 || rows <= 0 || nseq <= 0, "b_matvec_f32: bad arguments");
-    for (int s = 0; s < nseq; ++s)
-        if (launch_f32_mv(w, x + (size_t)s * k, out + (size_t)s * rows, rows, k, S()))
-            REFUSE("b_matvec_f32: launch");
+    if (launch_matvec_f32_exact(w, x, out, rows, k, nseq, S())) REFUSE("b_matvec_f32: launch");
 }
 
 void llamd_b_router(const float *logits, int n_expert, int n_used, int32_t *ids, float *weights,

@@ -224,6 +224,13 @@ struct RouterLaunch {
     int nseq = 1;  // x [nseq][k] -> logits [nseq][n_expert]; xblocks only with nseq = 1
 };
 int launch_router(const RouterLaunch &l, hipStream_t st);
+// y [nseq][rows] = w [rows][k] . x [nseq][k], each row's sum the reference's
+// sequential f32 fold (model.rs:253-262: products rounded, added in order
+// from -0.0) in one launch for every sequence; k outside the fold kernel's
+// range (a multiple of 256 up to 2048) falls back to the FMA matvec
+// (REDUCTION), one launch per sequence.
+int launch_matvec_f32_exact(const float *w, const float *x, float *y, int rows, int k, int nseq,
+                            hipStream_t st);
 // nseq sequences: logits [nseq][n_expert] -> ids, weights [nseq][n_used];
 // probs (optional): the softmax over every expert, [nseq][n_expert]
 int launch_route_logits(const float *logits, int n_expert, int n_used, int32_t *ids,

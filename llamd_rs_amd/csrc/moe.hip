@@ -361,6 +361,27 @@ int launch_q8_0_dequant(const void *planar, int rows, int k, float *out, hipStre
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+int launch_matvec_f32_exact(const float *w, const float *x, float *y, int rows, int k, int nseq,
+                            hipStream_t st) {
+    if (rows <= 0 || k <= 0 || nseq <= 0) return -1;
+    if (k % QK_K == 0 && k <= 2048) {
+        RouterLaunch l;
+        l.w = w;
+        l.x = x;
+        l.n_expert = rows;
+        l.k = k;
+        l.logits = y;
+        l.xq = nullptr;
+        l.xd = nullptr;
+        l.xblocks = 0;
+        l.nseq = nseq;
+        return launch_router(l, st);
+    }
+    for (int s = 0; s < nseq; ++s)
+        if (launch_f32_mv(w, x + (size_t)s * k, y + (size_t)s * rows, rows, k, st)) return -1;
+    return 0;
+}
+
 int launch_f32_mv(const float *w, const float *x, float *y, int rows, int k, hipStream_t st) {
     hipLaunchKernelGGL(f32_mv, dim3((rows + 3) / 4), dim3(256), 0, st, w, x, y, rows, k);
     return hipGetLastError() == hipSuccess ? 0 : -1;

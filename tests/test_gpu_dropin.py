@@ -407,14 +407,30 @@ def test_batched_f32_pieces_exact(gpu):
     sync()
     assert list(down(am, nseq, np.int32)) == [O.argmax(v[s]) for s in range(nseq)] == \
         [O.argmax(v[0]), 1000, 0]
-    # the router's F32 matvec, per sequence (REDUCTION)
+    # the router's F32 matvec: every sequence in one launch, each row the CPU
+    # path's sequential fold bit for bit (model.rs:253-262)
     rw = H.sample(n_expert * n, 33).reshape(n_expert, n).astype(np.float32)
     RW = dev(gpu, rw)
     L().llamd_b_matvec_f32(RW.ptr, X.ptr, LG.ptr, n, n_expert, nseq)
     sync()
     got = down(LG, nseq * n_expert).reshape(nseq, n_expert)
     for s in range(nseq):
-        assert O.max_deviation(got[s], O.matvec_f32(rw, n_expert, n, x[s]))[1] <= 1e-4
+        assert bits_equal(got[s], O.matvec_f32(rw, n_expert, n, x[s])), s
+    L().llamd_fwd_matvec_f32(RW.ptr, X.ptr, LG.ptr, n, n_expert)
+    sync()
+    assert bits_equal(down(LG, n_expert), O.matvec_f32(rw, n_expert, n, x[0]))
+    # k outside the fold kernel's range (not a multiple of 256): FMA, within
+    # REDUCTION x the rms of the outputs (grouped_expert.rs:147-175)
+    k2 = 300
+    X2 = dev(gpu, x.reshape(-1)[: nseq * k2])
+    L().llamd_b_matvec_f32(RW.ptr, X2.ptr, LG.ptr, k2, n_expert, nseq)
+    sync()
+    got = down(LG, nseq * n_expert).reshape(nseq, n_expert)
+    rw2 = rw.reshape(-1)[: n_expert * k2].reshape(n_expert, k2)
+    for s in range(nseq):
+        want = O.matvec_f32(rw2, n_expert, k2, x.reshape(-1)[s * k2:(s + 1) * k2])
+        rms = float(np.sqrt((want.astype(np.float64) ** 2).mean()))
+        assert np.abs(got[s].astype(np.float64) - want).max() <= O.REDUCTION * rms, s
 
 
 # ---- the unsigned-activation form (llamd_udot.hip) ---------------------------------
