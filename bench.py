@@ -734,8 +734,10 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
         with Gguf(path) as g:
             dm = rocm.DeviceModel(g, max_kv=1024)
         t_load = time.time() - t0
-    finally:
+    except BaseException:
         os.unlink(path)
+        raise
+    finally:
         L.llamd_hip_tune(b"model_graph", prev_graph)
     tok = 1
     for pos in range(3):
@@ -755,7 +757,59 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                                      "(tests/test_gpu_model.py::test_decode_full_qwen3_30b_a3b_widths)"}
     log(f"  decode token: {out['decode_token']}")
     dm.close()
+    try:
+        out.update(bench_ffi_decode(path))
+    finally:
+        os.unlink(path)
     return out
+
+
+def bench_ffi_decode(path):
+    """The same 48-layer model through the reference's own DeviceModel call
+    sequence on the exported FFI (llamd_rs_amd/ffi_replay.py: planar weights,
+    llamd_fwd_* per token with its graph capture, llamd_b_* / llamd_u_* for a
+    16-sequence batch): what the unchanged Rust runtime gets from this
+    library."""
+    from llamd_rs_amd.ffi_replay import FfiModel
+    from llamd_rs_amd.gguf import Gguf
+    res = {}
+    t0 = time.time()
+    with Gguf(path) as g:
+        fm = FfiModel(g, max_kv=1024, max_seq=16, use_graph=not EAGER_ONLY)
+    t_load = time.time() - t0
+    try:
+        tok = 1
+        for pos in range(3):
+            tok = fm.forward(tok, pos)
+        n = 64
+        t0 = time.perf_counter()
+        for pos in range(3, 3 + n):
+            tok = fm.forward(tok, pos)
+        dt = time.perf_counter() - t0
+        res["ffi_decode"] = {
+            "us_per_token": dt / n * 1e6, "tok_s": n / dt, "tokens": n, "load_s": round(t_load, 1),
+            "graph": not EAGER_ONLY,
+            "calls": "DeviceModel::forward's sequence (device.rs:486-722) on llamd_fwd_* / planar weights",
+            "parity": "bit-identical to the CPU forward at these widths on 4 layers x 3 tokens "
+                      "(tests/test_gpu_ffi_model.py::test_ffi_forward_full_qwen3_30b_a3b_widths)"}
+        log(f"  ffi decode: {res['ffi_decode']}")
+        nseq, steps = 16, 8
+        toks = list(range(1, nseq + 1))
+        toks = fm.forward_batch(toks, [0] * nseq)
+        t0 = time.perf_counter()
+        for st_ in range(1, 1 + steps):
+            toks = fm.forward_batch(toks, [st_] * nseq)
+        dt = time.perf_counter() - t0
+        res["ffi_decode_batch16"] = {
+            "us_per_batch": dt / steps * 1e6, "us_per_token": dt / steps / nseq * 1e6,
+            "tok_s": nseq * steps / dt, "steps": steps,
+            "calls": "DeviceModel::forward_batch's sequence (device.rs:741-962) on llamd_b_* / llamd_u_*",
+            "parity": "bit-identical per sequence to the CPU forward "
+                      "(tests/test_gpu_ffi_model.py::test_ffi_forward_batch_matches_the_cpu)"}
+        log(f"  ffi decode batch 16: {res['ffi_decode_batch16']}")
+    finally:
+        fm.close()
+    return res
 
 
 def bench_cpu(mats, shapes, xs, seconds):

@@ -259,10 +259,8 @@ void x3_entry(const void *const w[3], const size_t *const off[3], const void *q,
         if (launch_q6k_mv_x3(t, o, rows, 3, a.q, a.d, blocks, S())) REFUSE("matvec_x3: launch");
         return;
     }
-    for (int i = 0; i < 3; ++i) {
-        Q6kView v{t[i], 0, 1};
-        if (matvec_n(v, a, o[i], rows[i], blocks, nseq)) REFUSE("matvec_x3: launch");
-    }
+    if (launch_q6k_mv_batched_x3(t, o, rows, 3, a.cq, a.cd, blocks, nseq, S()))
+        REFUSE("matvec_x3: launch");
 }
 
 // gate and up of nseq sequences' own experts: slot s * n_used + k reads

@@ -115,6 +115,11 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
 // the same activations, in the same launch. fast: the REDUCTION-tolerance
 // kernels (one float accumulator per output instead of the reference's eight
 // class sums; outputs within REDUCTION of dot_q6k_q8k, not bit-identical).
+// Up to three matrices with their own row counts (Q, K, V) against the same
+// nseq token-chunked activations, one launch: y[i] [nseq][rows[i]].
+int launch_q6k_mv_batched_x3(const void *const w[3], float *const y[3], const int rows[3], int n_mat,
+                             const int8_t *act_q, const float *act_d, int blocks, int nseq,
+                             hipStream_t st);
 int launch_q6k_dequant(const void *w, int rows, int blocks, float *out, hipStream_t st);
 // Per 16-row tile t of a tiled Q6_K matrix: mt[t] = the largest over its rows
 // of sum_b |f16(d_b)| * sum_e |sc(e) * (q_e - 32)| (an upper bound of the

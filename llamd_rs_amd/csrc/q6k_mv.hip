@@ -526,6 +526,15 @@ struct BatchParams {
     const uint8_t *w2;
     float *y2;
     int items_per_mat;
+    // n_segs > 0 (single group only): up to three matrices of their own row
+    // counts on the same activations in one launch (Q, K and V of a batch);
+    // segment i's items start at item segs[i].first
+    int n_segs;
+    struct Seg {
+        const uint8_t *w;
+        float *y;
+        int rows, tiles, first, items;
+    } segs[3];
 };
 
 // The work item of this wave and the parameters it runs with: the second
@@ -533,6 +542,18 @@ struct BatchParams {
 __device__ __forceinline__ int batch_item(const BatchParams &p, BatchParams &q) {
     int item = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
     q = p;
+    if (p.n_segs > 0) {
+        // the item's segment, chosen with scalar selects
+        BatchParams::Seg sg = p.segs[0];
+        if (p.n_segs > 1 && item >= p.segs[1].first) sg = p.segs[1];
+        if (p.n_segs > 2 && item >= p.segs[2].first) sg = p.segs[2];
+        q.w = sg.w;
+        q.y = sg.y;
+        q.rows = q.ldy = sg.rows;
+        q.tiles = sg.tiles;
+        q.items_per_mat = sg.items;
+        return item - sg.first;
+    }
     if (p.w2 && item >= p.items_per_mat) {
         item -= p.items_per_mat;
         q.w = p.w2;
@@ -1635,6 +1656,7 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     // max_chunks >= n_groups (twins: ceil((max_chunks + n_groups) / 2) items)
     if (group_tables && (!grp_expert || max_chunks < n_groups || max_chunks <= 0)) return -1;
     BatchParams p;
+    p.n_segs = 0;
     if (w2 && (!y2 || amax_v)) return -1;
     p.w2 = (const uint8_t *)w2;
     p.y2 = y2;
@@ -1701,6 +1723,37 @@ int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *gr
     p.items_per_mat = (int)items;
     const long all = w2 ? 2 * items : items;
     hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((all + 3) / 4)), dim3(256), 0, st, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_q6k_mv_batched_x3(const void *const w[3], float *const y[3], const int rows[3], int n_mat,
+                             const int8_t *act_q, const float *act_d, int blocks, int nseq,
+                             hipStream_t st) {
+    if (n_mat < 1 || n_mat > 3 || nseq <= 0 || blocks <= 0) return -1;
+    BatchParams p = {};
+    const int chunks = (nseq + CHUNK_TOKENS - 1) / CHUNK_TOKENS;
+    int first = 0;
+    p.n_segs = n_mat;
+    for (int i = 0; i < n_mat; ++i) {
+        auto &sg = p.segs[i];
+        sg.w = (const uint8_t *)w[i];
+        sg.y = y[i];
+        sg.rows = rows[i];
+        sg.tiles = (rows[i] + TILE_ROWS - 1) / TILE_ROWS;
+        sg.first = first;
+        sg.items = sg.tiles * chunks;
+        first += sg.items;
+    }
+    p.w = p.segs[0].w;
+    p.y = p.segs[0].y;
+    p.rows = p.ldy = rows[0];
+    p.tiles = p.segs[0].tiles;
+    p.items_per_mat = p.segs[0].items;
+    p.act_q = act_q;
+    p.act_d = act_d;
+    p.blocks = blocks;
+    p.single_count = nseq;  // one group (expert 0) of nseq tokens
+    hipLaunchKernelGGL(q6k_mv_batched, dim3((unsigned)((first + 3) / 4)), dim3(256), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

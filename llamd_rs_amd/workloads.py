@@ -20,6 +20,9 @@ rocprofv3 (--kernel-trace, --pmc) so a profile covers exactly one workload:
     prefill_reduction  the same with LLAMD_HIP_REDUCTION (tolerance GEMMs)
     decode       whole-token decode of a Qwen3-30B-A3B-shaped model cut to 4
                  layers (plain launches, no graph), positions 3..3+N
+    ffi_decode   the same model through the reference's own DeviceModel call
+                 sequence on the exported FFI (ffi_replay.py), plain launches
+    ffi_decode_batch16  its forward_batch at 16 sequences
 """
 from __future__ import annotations
 
@@ -142,6 +145,35 @@ def decode(L, iters):
     dm.close()
 
 
+def ffi_decode(L, iters, nseq=1):
+    """The reference's DeviceModel call sequence on the exported FFI
+    (ffi_replay.py), the 4-layer cut of the Qwen3-30B-A3B shapes; plain
+    launches (no graph) so a kernel trace sees every launch."""
+    import os
+    import tempfile
+    from . import synth_model
+    from .ffi_replay import FfiModel
+    from .gguf import Gguf
+    hp = dict(synth_model.QWEN3_30B_A3B, n_layer=4)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        synth_model.write_model(path, hp)
+        with Gguf(path) as g:
+            fm = FfiModel(g, max_kv=1024, max_seq=max(nseq, 1), use_graph=False)
+    finally:
+        os.unlink(path)
+    if nseq == 1:
+        tok = 1
+        for pos in range(3 + iters):
+            tok = fm.forward(tok, pos)
+    else:
+        toks = list(range(1, nseq + 1))
+        for pos in range(iters):
+            toks = fm.forward_batch(toks, [pos] * nseq)
+    fm.close()
+
+
 WORKLOADS = {
     "configs1": configs1,
     "configs1_grouped": configs1_grouped,
@@ -152,6 +184,8 @@ WORKLOADS = {
     "prefill": prefill,
     "prefill_reduction": lambda L, n: prefill(L, n, 1),
     "decode": decode,
+    "ffi_decode": ffi_decode,
+    "ffi_decode_batch16": lambda L, n: ffi_decode(L, n, 16),
 }
 
 
