@@ -44,7 +44,7 @@ GIB = 1 << 30
 # scaled by the same counters on a copy of known size (x2.0 fetch, x1.0
 # write); the commands and per-kernel values are in
 # profiles/q6k_mv_b1.configs1.hbm_traffic.txt. Algorithmic: 1,301,504 B.
-TRAFFIC_Q6K_MV_CONFIGS1 = 1386959
+TRAFFIC_Q6K_MV_CONFIGS1 = 1398190
 
 
 def log(*a):
