@@ -1340,8 +1340,7 @@ __global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
     __shared__ int s_bad[16];
     __shared__ int s_cand[CERT_CAP];
     __shared__ int s_ncand;
-    // per round: blocks <= 16: entry e = (tile e / blocks, block e % blocks);
-    // blocks > 16: one tile, entry b = block b
+    // per round: entry e = (tile e / blocks, block e % blocks), CERT_MAXB / blocks tiles
     __shared__ float s_terms[CERT_MAXB][TILE_ROWS][8];
     if (tid == 0) s_ncand = 0;
     // 1. the certified lower bound L of the largest exact logit
@@ -1406,8 +1405,11 @@ __global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
     __syncthreads();
     const bool all = bad || s_ncand > CERT_CAP;
     const int total = all ? p.tiles : s_ncand;
-    // 3. exact recomputation, (tile, block) pairs over the waves
-    const int per = p.blocks <= 16 ? 16 / p.blocks : 1;  // tiles per round
+    // 3. exact recomputation, (tile, block) pairs over the waves: up to
+    // CERT_MAXB pairs per round, two per wave with both pairs' loads in
+    // flight together (a round is one memory round trip)
+    // tiles per round: a wave folds each (blocks <= CERT_MAXB, checked at launch)
+    const int per = min(16, CERT_MAXB / p.blocks);
     const int pairs = per * p.blocks;
     const MaskSel msel = mask_selectors(n, (n >> 2) == s);
     float bv = -INFINITY;
@@ -1415,22 +1417,34 @@ __global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
     int nan0 = 0;
     for (int r0 = 0; r0 < total; r0 += per) {
         float se = 0.0f, so = 0.0f;
-        for (int e = wave; e < pairs; e += 16) {
-            const int ci = r0 + e / p.blocks, b = e % p.blocks;
-            if (ci >= total) break;
-            const int tt = all ? ci : s_cand[ci];
-            BlockRegs r;
-            load_block(r, p.w + ((size_t)tt * p.blocks + b) * SEG_BYTES, aq, ad, b, lane, n);
-            float te, to;
-            block_terms(r, msel, te, to);
-            const int slot = p.blocks <= 16 ? e : b;
-            s_terms[slot][n][2 * s] = te;
-            s_terms[slot][n][2 * s + 1] = to;
+        for (int e0 = wave; e0 < pairs; e0 += 32) {
+            BlockRegs r[2];
+            bool ok[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int e = e0 + 16 * h;
+                const int ci = r0 + e / p.blocks, b = e % p.blocks;
+                ok[h] = e < pairs && ci < total;
+                if (ok[h]) {
+                    const int tt = all ? ci : s_cand[ci];
+                    load_block(r[h], p.w + ((size_t)tt * p.blocks + b) * SEG_BYTES, aq, ad, b, lane, n);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (!ok[h]) continue;
+                const int e = e0 + 16 * h;
+                float te, to;
+                block_terms(r[h], msel, te, to);
+                const int slot = e;
+                s_terms[slot][n][2 * s] = te;
+                s_terms[slot][n][2 * s + 1] = to;
+            }
         }
         __syncthreads();
         if (wave < per && r0 + wave < total) {
             const int tt = all ? r0 + wave : s_cand[r0 + wave];
-            const int base = p.blocks <= 16 ? wave * p.blocks : 0;
+            const int base = wave * p.blocks;
             for (int b = 0; b < p.blocks; ++b) {
                 se = se + s_terms[base + b][n][2 * s];
                 so = so + s_terms[base + b][n][2 * s + 1];
