@@ -875,6 +875,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // The dynamic LDS of the LDSA kernels below.
 extern __shared__ uint4 g_act_lds[];
 
+// Activation planes in LDS are stored with a swizzle: in each 512-byte plane
+// (16 tokens x 32 bytes), the two 16-byte halves of token n's row are swapped
+// when bit 2 of n is set. The MFMA lane (token n, quarter s) reads 8 bytes at
+// 32 n + 8 s; without the swap, tokens n and n + 4 hit the same banks and a
+// plane read has 4-way bank conflicts, with it 2-way at most (the 16-byte
+// unit of the global-to-LDS copies allows no finer move).
+__device__ __forceinline__ int act_lds_byte(int n, int s) {
+    return 32 * n + 16 * ((s >> 1) ^ ((n >> 2) & 1)) + 8 * (s & 1);
+}
+// The global 16-byte unit (offset within the chunk's block) that LDS unit
+// `slot` of the same block holds: the swap is its own inverse.
+__device__ __forceinline__ int act_lds_src(int slot) {
+    const int n = (slot >> 1) & 15;
+    return 16 * (slot ^ ((n >> 2) & 1));
+}
+
 // LDSA: the chunk's quants are read from g_act_lds (same layout).
 template <int NC, bool LDSA = false>
 __device__ __forceinline__ void fast_tile_range(const BatchParams &p, int lane, int t, int sub0,
@@ -882,7 +898,8 @@ __device__ __forceinline__ void fast_tile_range(const BatchParams &p, int lane, 
     const int n = lane & 15, s = lane >> 4;
     const uint8_t *seg = p.w + (size_t)expert * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
     const size_t chunk_q = (size_t)p.blocks * CHUNK_BLOCK_BYTES, chunk_d = (size_t)p.blocks * CHUNK_TOKENS;
-    const int8_t *aq = (LDSA ? (const int8_t *)g_act_lds : p.act_q + (size_t)sub0 * chunk_q) + n * 32 + 8 * s;
+    const int8_t *aq = LDSA ? (const int8_t *)g_act_lds + act_lds_byte(n, s)
+                            : p.act_q + (size_t)sub0 * chunk_q + n * 32 + 8 * s;
     const float *ad = p.act_d + (size_t)sub0 * chunk_d + n;
     // class planes two classes ahead of their MFMAs, across blocks (past the
     // range's last block the loads re-read it, unused)
@@ -1045,7 +1062,7 @@ __global__ __launch_bounds__(256) void q6k_mv_batched_fast(BatchParams pk) {
     if constexpr (LDSA) {
         const int n16 = p.blocks * CHUNK_BLOCK_BYTES / 16;
         const uint4 *src = (const uint4 *)p.act_q;
-        for (int i = threadIdx.x; i < n16; i += blockDim.x) g_act_lds[i] = src[i];
+        for (int i = threadIdx.x; i < n16; i += blockDim.x) g_act_lds[i] = src[act_lds_src(i) / 16];
         __syncthreads();
         if (live && b0 < b1) fast_tile_range<1, true>(p, lane, t, 0, expert, b0, b1, acc);
     } else if (live && b0 < b1) {
@@ -1134,7 +1151,7 @@ __device__ __forceinline__ void fast_tile_staged(const BatchParams &p, int lane,
             const int off = (wave * NC + i) * 1024;  // within the NC x 4 KiB
             const int u = off / CHUNK_BLOCK_BYTES, o = off % CHUNK_BLOCK_BYTES;
             __builtin_amdgcn_global_load_lds(
-                (const void *)(gq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + o + 16 * lane),
+                (const void *)(gq + u * chunk_q + (size_t)b * CHUNK_BLOCK_BYTES + act_lds_src(o / 16 + lane)),
                 (lds_ptr)(lds + (b & 1) * BUF + off), 16, 0, 0);
         }
     };
@@ -1155,7 +1172,7 @@ __device__ __forceinline__ void fast_tile_staged(const BatchParams &p, int lane,
         for (int u = 0; u < NC; ++u) r.adb[u] = ad[u * chunk_d + (size_t)b * CHUNK_TOKENS];
     };
     auto compute = [&](const W &r, int b) {
-        const int8_t *aq = lds + (b & 1) * BUF + n * 32 + 8 * s;
+        const int8_t *aq = lds + (b & 1) * BUF + act_lds_byte(n, s);
         const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
         const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
         const FoldScales fs = fold_scales(r.scw);
