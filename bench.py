@@ -193,7 +193,7 @@ def main():
                     help="plain launches everywhere, no graph replay: for rocprofv3 kernel traces, "
                          "which space graph-replayed kernels tens of microseconds apart")
     ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
-                    help="set a kernel tune key (llamd_hip_tune) before measuring, e.g. mv_dot=1")
+                    help="set a kernel tune key (llamd_hip_tune) before measuring, e.g. mv_ks=4")
     args = ap.parse_args()
     global EAGER_ONLY
     EAGER_ONLY = args.eager
@@ -681,10 +681,26 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
         t0 = time.perf_counter()
         O.moe_ffn_tokens(xh[:ns], n_embd, n_ff, n_expert, gate, up, down, ids_h[:ns], w_h[:ns])
         dt = time.perf_counter() - t0
+        # and one full 512-token pass on the host's threads: 16-token slices
+        # of the same call in a thread pool (the C oracle releases the GIL)
+        from concurrent.futures import ThreadPoolExecutor
+        nt = min(16, host_threads())
+        slices = [(s0, min(n_tok, s0 + 16)) for s0 in range(0, n_tok, 16)]
+        with ThreadPoolExecutor(max_workers=nt) as ex:
+            t0 = time.perf_counter()
+            parts = list(ex.map(lambda ab: O.moe_ffn_tokens(
+                xh[ab[0]:ab[1]], n_embd, n_ff, n_expert, gate, up, down, ids_h[ab[0]:ab[1]],
+                w_h[ab[0]:ab[1]]), slices))
+            dt_n = time.perf_counter() - t0
+        assert sum(len(q) for q in parts) == n_tok
         out["prefill_grouped"].update({
             "cpu_1t_ms_per_pass_est": dt / ns * n_tok * 1e3,
             "cpu_sample": f"{ns} tokens of moe_ffn in {dt:.2f}s on 1 host thread, scaled to {n_tok}",
-            "vs_cpu_1t": (dt / ns * n_tok) / (ms / steps * 1e-3)})
+            "vs_cpu_1t": (dt / ns * n_tok) / (ms / steps * 1e-3),
+            "cpu_nt_ms_per_pass": dt_n * 1e3, "cpu_threads": nt,
+            "cpu_nt_sample": f"one full {n_tok}-token pass of moe_ffn, {len(slices)} slices of 16 tokens "
+                             f"over {nt} host threads",
+            "vs_cpu_nt": dt_n / (ms / steps * 1e-3)})
     log(f"  prefill: {out['prefill_grouped']}")
     for ly in layers:
         ly.close()

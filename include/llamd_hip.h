@@ -63,14 +63,9 @@ const char *llamd_hip_last_error(void);
  * the previous value, -1 for an unknown key or value.
  *   "mv_ks": waves per 16-row tile of the Q6_K matvec, 1, 4 or 8 (0: by
  *     shape, the default; all three are chosen by shape somewhere);
- *   "mv_dot": 1 runs the batch-1 Q6_K matvec's integer part on v_dot2
- *     instead of the matrix cores (0, default; slower, kept as the measured
- *     alternative);
  *   "batched_twin": the grouped prefill GEMM's waves take two 16-token
  *     chunks of one expert (1, default) or one (0, the kernel ungrouped
  *     batches always use);
- *   "moe_fused": the MoE decode schedule, 2 (default) or the fallbacks that
- *     shapes outside the two-launch kernel's limits take, 1 and 0;
  *   "moe_polls": loads a wait inside the MoE decode kernel makes before the
  *     waiting wave computes the awaited router logit itself (default 2^18;
  *     0 = at once);

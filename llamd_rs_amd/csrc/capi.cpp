@@ -35,7 +35,6 @@ std::mutex g_mu;             // serialises host-in/host-out calls and the regist
 hipStream_t g_stream = nullptr;
 // MoE decode schedule: 2 router fold beside gate/up, then down (moe_decode.hip);
 // 1 router, gate/up + SwiGLU, down + combine; 0 unfused (separate SwiGLU).
-int g_tune_moe_fused = 2;
 // batched decode: up to this many sequences through the decode kernels, more
 // through the expert-grouped (prefill) kernels. Measured on MI355X (configs[2]
 // layer, us per token, decode / grouped): 12 sequences 9.06 / 9.31, 16
@@ -227,11 +226,6 @@ const char *llamd_hip_last_error(void) { return g_err; }
 
 int llamd_hip_tune(const char *key, int value) {
     if (!key) return fail("tune: null key");
-    if (!strcmp(key, "moe_fused")) {
-        const int prev = g_tune_moe_fused;
-        g_tune_moe_fused = value < 0 ? 0 : value > 2 ? 2 : value;
-        return prev;
-    }
     if (!strcmp(key, "model_fused_norm")) {
         const int prev = g_tune_model_fused_norm;
         g_tune_model_fused_norm = value ? 1 : 0;
@@ -272,11 +266,6 @@ int llamd_hip_tune(const char *key, int value) {
             return fail("tune: fast_ks takes 0 (by shape), 1, 2 or 4");
         const int prev = g_tune_fast_ks;
         g_tune_fast_ks = value;
-        return prev;
-    }
-    if (!strcmp(key, "mv_dot")) {
-        const int prev = g_tune_mv_dot;
-        g_tune_mv_dot = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "mv_ks")) {
@@ -853,7 +842,7 @@ MoeDecodeLaunch decode_launch(MoeLayer *m, const float *d_x, const float *d_res,
 
 bool llamd::moe_normed_applies(void *h) {
     const MoeLayer *m = (const MoeLayer *)h;
-    return m && m->decode_fits() && g_tune_moe_fused == 2;
+    return m && m->decode_fits();
 }
 
 int llamd::moe_forward_normed(void *h, const float *x, const float *o, const float *w, float eps,
@@ -970,41 +959,29 @@ int llamd_hip_moe_forward(void *h, const float *d_x, const float *d_res, float *
     rl.xq = m->xq.as<int8_t>();
     rl.xd = m->xd.as<float>();
     rl.xblocks = m->be;
-    if (g_tune_moe_fused == 2 && m->decode_fits()) {
+    if (m->decode_fits()) {
         // router and gate/up overlapped, then down + combine (moe_decode.hip)
         MoeDecodeLaunch dl = decode_launch(m, d_x, d_res, d_out);
         rc |= launch_moe_decode(dl, st);
         return rc ? fail("moe_forward: launch failed") : 0;
     }
+    // n_ff beyond the decode kernel's LDS (more than 8 blocks): one launch
+    // per step of the reference's chain
     rc |= launch_router(rl, st);
-    if (g_tune_moe_fused && m->bf <= 8) {
-        // 2. route (prologue) + gate and up of each routed expert's tile in
-        //    one workgroup + act = silu(gate) * up
-        rc |= launch_q6k_gateup_silu(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
-                                     m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
-                                     m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
-                                     m->g.as<float>(), m->n_ff, m->be, st);
-        // 3. Q8_K of act in the prologue, down projection, weighted combine,
-        //    residual
-        rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), nullptr, nullptr,
-                                      m->g.as<float>(), m->weights.as<float>(), d_res, d_out,
-                                      m->n_embd, m->bf, m->n_used, st);
-    } else {
-        // 2. route (prologue) + gate and up of the routed experts in one
-        //    launch: g holds [gate | up] x n_used x n_ff
-        rc |= launch_q6k_mv_routed(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
-                                   m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
-                                   m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
-                                   m->g.as<float>(), m->n_ff, m->be, st);
-        // 3. SwiGLU + Q8_K of the activations
-        rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
-                                nullptr, m->aq.as<int8_t>(), m->ad.as<float>(), nullptr,
-                                m->n_used * m->bf, st);
-        // 4. down projection of the routed experts + weighted combine + residual
-        rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
-                                      m->ad.as<float>(), nullptr, m->weights.as<float>(), d_res,
-                                      d_out, m->n_embd, m->bf, m->n_used, st);
-    }
+    // 2. route (prologue) + gate and up of the routed experts in one
+    //    launch: g holds [gate | up] x n_used x n_ff
+    rc |= launch_q6k_mv_routed(m->gate, m->upw, m->sgu, m->logits.as<float>(), m->n_expert,
+                               m->n_used, m->ids.as<int32_t>(), m->weights.as<float>(),
+                               m->stats.as<int>(), m->xq.as<int8_t>(), m->xd.as<float>(),
+                               m->g.as<float>(), m->n_ff, m->be, st);
+    // 3. SwiGLU + Q8_K of the activations
+    rc |= launch_swiglu_q8k(m->g.as<float>(), m->g.as<float>() + (size_t)m->n_used * m->n_ff,
+                            nullptr, m->aq.as<int8_t>(), m->ad.as<float>(), nullptr,
+                            m->n_used * m->bf, st);
+    // 4. down projection of the routed experts + weighted combine + residual
+    rc |= launch_q6k_down_combine(m->downw, m->sd, m->ids.as<int32_t>(), m->aq.as<int8_t>(),
+                                  m->ad.as<float>(), m->weights.as<float>(), d_res, d_out,
+                                  m->n_embd, m->bf, m->n_used, st);
     return rc ? fail("moe_forward: launch failed") : 0;
 }
 

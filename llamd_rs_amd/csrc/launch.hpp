@@ -14,7 +14,6 @@ namespace llamd {
 extern int g_tune_batched_twin;
 extern int g_tune_fast_lds;  // LLAMD_HIP_REDUCTION LM head: the chunk's quants staged in LDS
 extern int g_tune_fast_ks;  // LLAMD_HIP_REDUCTION batched kernels: waves per item (K split), 0 = by shape  // grouped q6k_mv_batched: two chunks of one expert per wave
-extern int g_tune_mv_dot;  // 1: q6k_mv_b1's integer part on v_dot2 instead of MFMA (one matrix)
 extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0: automatic)
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
@@ -46,18 +45,12 @@ int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
                         const float *logits, int n_expert, int n_used, int32_t *ids_out,
                         float *w_out, int *stats, const int8_t *aq, const float *ad, float *y,
                         int rows, int blocks, hipStream_t st);
-// act non-null: f32 activations [n_slots][blocks*256] quantized to Q8_K in the
-// prologue (aq, ad unused; blocks <= 8).
+// Down projection of the routed experts' Q8_K activations [n_slots] + the
+// weighted combine in routing order + residual.
 int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
-                            const int8_t *aq, const float *ad, const float *act,
-                            const float *weights, const float *res, float *out, int rows,
-                            int blocks, int n_slots, hipStream_t st);
-// Routing prologue + gate and up of the routed experts + act = silu(g) * up
-// ([n_used][rows] f32) in one launch.
-int launch_q6k_gateup_silu(const void *w_gate, const void *w_up, size_t expert_stride,
-                           const float *logits, int n_expert, int n_used, int32_t *ids_out,
-                           float *w_out, int *stats, const int8_t *aq, const float *ad, float *act,
-                           int rows, int blocks, hipStream_t st);
+                            const int8_t *aq, const float *ad, const float *weights,
+                            const float *res, float *out, int rows, int blocks, int n_slots,
+                            hipStream_t st);
 // Expert-grouped batched matvec (see q6k_mv.hip). Activations are in the
 // token-chunked layout (q8k_wave.hpp): chunk k holds the 16 tokens of
 // sub-tile k. sub_start has 2 * (n_groups + 1) entries: the prefix of

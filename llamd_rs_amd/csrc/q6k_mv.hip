@@ -99,12 +99,11 @@ __device__ __forceinline__ unsigned long long *clock_start(unsigned long long *r
 // meet in LDS and are folded in block order -- the same additions in the same
 // order as a single wave walking every block, so splitting K changes the
 // latency, never the bits.
-template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false, bool DOT = false>
+template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false>
 __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) {
     constexpr int IPW = KS >= 4 ? 1 : 4 / KS;   // items per workgroup
     constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
     __shared__ float terms[KS > 1 ? IPW : 1][KS > 1 ? MAXB : 1][TILE_ROWS][8];
-    __shared__ __align__(16) int16_t a16s[DOT ? IPW * KS : 1][DOT ? QK_K : 1];  // DOT: per wave
     const int lane = threadIdx.x & 63;
     // every kernarg field the common path reads, fetched in one batch up front
     asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.y), "s"(p.seg0.rows), "s"(p.seg0.tiles),
@@ -171,12 +170,10 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
         // flight while the current block is computed, with no copies
         BlockRegs ra, rb;
         auto load = [&](BlockRegs &r, int bb) {
-            if constexpr (DOT) load_block_dot(r, seg0 + (size_t)bb * SEG_BYTES, aq, ad, bb, lane, n);
-            else load_block(r, seg0 + (size_t)bb * SEG_BYTES, aq, ad, bb, lane, n);
+            load_block(r, seg0 + (size_t)bb * SEG_BYTES, aq, ad, bb, lane, n);
         };
         auto terms_of = [&](const BlockRegs &r, float &te, float &to) {
-            if constexpr (DOT) block_terms_dot(r, a16s[DOT ? wave : 0], lane, n, s, te, to);
-            else block_terms(r, msel, te, to);
+            block_terms(r, msel, te, to);
         };
         load(ra, b0);
         for (int b = b0; b < b1; b += 2) {
@@ -241,24 +238,16 @@ struct DownParams {
     const int32_t *ids;
     const int8_t *aq;     // [n_slots][blocks*256]  (act == nullptr)
     const float *ad;      // [n_slots][blocks]
-    const float *act;     // [n_slots][blocks*256] f32 activations to quantize here, or nullptr
     const float *weights; // [n_slots] routing weights
     const float *res;     // [rows] or nullptr
     float *out;           // [rows]
     int rows, tiles, blocks, n_slots;
 };
 
-// QACT: the activations arrive as f32 (act = silu(gate) * up from
-// q6k_gateup_silu); wave e quantizes its slot's blocks to Q8_K in LDS --
-// quantize_q8_k exactly, the same bits as a separate quantize pass -- while
-// its first weight blocks are already in flight.
-template <bool QACT>
 __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
-    asm volatile("" ::"s"(p.w), "s"(p.expert_stride), "s"(p.ids), "s"(p.act), "s"(p.aq), "s"(p.ad),
+    asm volatile("" ::"s"(p.w), "s"(p.expert_stride), "s"(p.ids), "s"(p.aq), "s"(p.ad),
                  "s"(p.weights), "s"(p.res), "s"(p.out), "s"(p.rows), "s"(p.blocks), "s"(p.n_slots));
     __shared__ float ys[16][TILE_ROWS];
-    __shared__ __align__(16) int8_t lq[QACT ? 16 : 1][QACT ? DOWN_ACT_BLOCKS * QK_K : 1];
-    __shared__ float ld[QACT ? 16 : 1][QACT ? DOWN_ACT_BLOCKS : 1];
     const int lane = threadIdx.x & 63;
     const int e = threadIdx.x >> 6;
     const int t = blockIdx.x;
@@ -266,54 +255,7 @@ __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
     const MaskSel msel = mask_selectors(n, (n >> 2) == s);
     float se = 0.0f, so = 0.0f;
     BlockRegs ra, rb;
-    if constexpr (QACT) {
-        // the activations do not depend on the routed ids: their loads go
-        // out first, then the ids, then the weights
-        const float *a = p.act + (size_t)e * p.blocks * QK_K;
-        float4 av[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (j < p.blocks) av[j] = *(const float4 *)(a + (size_t)j * QK_K + 4 * lane);
-        const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
-        load_weights(ra, seg0, lane, n);
-        if (p.blocks > 1) load_weights(rb, seg0 + SEG_BYTES, lane, n);
-        for (int c0 = 0; c0 < p.blocks; c0 += 4) {
-            if (c0 > 0) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (c0 + j < p.blocks) av[j] = *(const float4 *)(a + (size_t)(c0 + j) * QK_K + 4 * lane);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (c0 + j < p.blocks) {
-                    const float v[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
-                    quantize_wave(v, lane, &lq[e][(c0 + j) * QK_K], &ld[e][c0 + j], nullptr);
-                }
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        auto fetch = [&](BlockRegs &r, int b) {
-            r.g = *(const uint4 *)(&lq[e][b * QK_K + 16 * n]);
-            r.ad = ld[e][b];
-        };
-        fetch(ra, 0);
-        for (int b = 0; b < p.blocks; b += 2) {
-            if (b + 1 < p.blocks) fetch(rb, b + 1);
-            float te, to;
-            block_terms(ra, msel, te, to);
-            se = se + te;
-            so = so + to;
-            if (b + 1 >= p.blocks) break;
-            if (b + 2 < p.blocks) {
-                load_weights(ra, seg0 + (size_t)(b + 2) * SEG_BYTES, lane, n);
-                fetch(ra, b + 2);
-            }
-            block_terms(rb, msel, te, to);
-            se = se + te;
-            so = so + to;
-            if (b + 3 < p.blocks) load_weights(rb, seg0 + (size_t)(b + 3) * SEG_BYTES, lane, n);
-        }
-    } else {
+    {
         const uint8_t *seg0 = p.w + (size_t)p.ids[e] * p.expert_stride + (size_t)t * p.blocks * SEG_BYTES;
         const int8_t *aq = p.aq + (size_t)e * p.blocks * QK_K;
         const float *ad = p.ad + (size_t)e * p.blocks;
@@ -354,99 +296,6 @@ __global__ __launch_bounds__(1024) void q6k_down_combine(DownParams p) {
             }
             p.out[row] = p.res ? p.res[row] + acc : acc;
         }
-    }
-}
-
-// Gate and up of one (routed slot, 16-row tile) in one workgroup of 8 waves,
-// with the routing in the prologue (wave 0, as q6k_mv_b1<4, true>): waves
-// 0-3 split the gate row's blocks four ways and waves 4-7 the up row's; the
-// per-block terms meet in LDS and are folded in block order (bit-identical
-// to one wave walking the row), and wave 0 writes act = silu(gate) * up for
-// the tile's 16 rows (CpuBackend::silu and mul, llamd-cpu/src/lib.rs:103-113).
-__global__ __launch_bounds__(512) void q6k_gateup_silu(MvParams p, const uint8_t *w_up,
-                                                       float *act) {
-    asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.rows), "s"(p.seg0.tiles), "s"(p.aq), "s"(p.ad),
-                 "s"(p.expert_stride), "s"(p.blocks), "s"(p.route_l), "s"(p.n_expert),
-                 "s"(p.n_used), "s"(w_up), "s"(act));
-    constexpr int MAXB = 16;
-    __shared__ float terms[2][MAXB][TILE_ROWS][8];
-    __shared__ float gu[2][TILE_ROWS];
-    __shared__ RouteLds rsh;
-    __shared__ uint64_t tab[32];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int half = wave >> 2;  // 0: gate, 1: up
-    const int kc = wave & 3;
-    const int tiles = p.seg0.tiles, rows = p.seg0.rows;
-    const int slot = (int)blockIdx.x / tiles;
-    const int t = (int)blockIdx.x - slot * tiles;
-    const int n = lane & 15, s = lane >> 4;
-    const MaskSel msel = mask_selectors(n, (n >> 2) == s);
-    if (wave == 0) {
-        float l[RW];
-#pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            const int i = lane + WAVE * j;
-            l[j] = i < p.n_expert ? p.route_l[i] : 0.0f;
-        }
-        const bool writer = blockIdx.x == 0;
-        route_finish(l, p.n_expert, p.n_used, true, rsh, writer ? p.ids_out : nullptr,
-                     writer ? p.w_out : nullptr, nullptr);
-        if (writer && lane == 0 && p.stats) {
-            p.stats[0] += 1;
-            p.stats[1] += 1;
-        }
-        expf_ref_tab_fill(tab);
-    }
-    __syncthreads();
-    const int expert = rsh.sorted[slot];
-    const uint8_t *seg0 = (half ? w_up : p.seg0.w) + (size_t)expert * p.expert_stride +
-                          (size_t)t * p.blocks * SEG_BYTES;
-    const int bpc = (p.blocks + 3) / 4;
-    const int b0 = kc * bpc;
-    const int b1 = min(p.blocks, b0 + bpc);
-    float se = 0.0f, so = 0.0f;
-    if (b0 < b1) {
-        BlockRegs ra, rb;
-        load_block(ra, seg0 + (size_t)b0 * SEG_BYTES, p.aq, p.ad, b0, lane, n);
-        for (int b = b0; b < b1; b += 2) {
-            if (b + 1 < b1) load_block(rb, seg0 + (size_t)(b + 1) * SEG_BYTES, p.aq, p.ad, b + 1, lane, n);
-            float te, to;
-            block_terms(ra, msel, te, to);
-            consume_terms<4>(b, te, to, se, so, terms[half], n, s);
-            if (b + 1 >= b1) break;
-            if (b + 2 < b1) load_block(ra, seg0 + (size_t)(b + 2) * SEG_BYTES, p.aq, p.ad, b + 2, lane, n);
-            block_terms(rb, msel, te, to);
-            consume_terms<4>(b + 1, te, to, se, so, terms[half], n, s);
-        }
-    }
-    __syncthreads();
-    if (kc == 0) {
-        // fold in block order, classes 2s and 2s+1 on lane (n, s), then the
-        // eight class sums in class order (dot.rs:195)
-        se = 0.0f;
-        so = 0.0f;
-        for (int b = 0; b < p.blocks; ++b) {
-            se = se + terms[half][b][n][2 * s];
-            so = so + terms[half][b][n][2 * s + 1];
-        }
-        float cls[8];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
-            cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
-        }
-        if (s == 0) {
-            float tot = -0.0f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) tot = tot + cls[c];
-            gu[half][n] = tot;
-        }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < TILE_ROWS) {
-        const int row = t * TILE_ROWS + lane;
-        if (row < rows) act[(size_t)slot * rows + row] = silu_ref(gu[0][lane], tab) * gu[1][lane];
     }
 }
 
@@ -1502,7 +1351,6 @@ __global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
 }  // namespace
 
 int g_tune_mv_ks = 0;
-int g_tune_mv_dot = 0;
 int g_tune_batched_twin = 1;
 int g_tune_fast_ks = 0;
 int g_tune_fast_lds = 1;
@@ -1528,7 +1376,7 @@ void set_segments(MvParams &p, int n, const void *const *w, float *const *y, con
     p.n_slots = n_slots;
 }
 
-template <int NSEG, bool AMAX = false, bool DOT = false>
+template <int NSEG, bool AMAX = false>
 void launch_b1_n(const MvParams &p, hipStream_t st) {
     const int items = p.items;
     // Measured on MI355X: eight waves per tile (one block each at k = 2048)
@@ -1544,15 +1392,15 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
                                 : (p.blocks > 4 && items <= 384 ? 8 : (p.blocks <= 4 && items >= 1024 ? 1 : 0));
     if (p.blocks <= 16 && (ks == 4 || ks == 8 || ks == 0)) {
         if (ks == 8)
-            hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX, DOT>), dim3(items), dim3(512), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX>), dim3(items), dim3(512), 0, st, p);
         else
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
             // tile -- more loads in flight per tile and shorter per-wave
             // chains -- except for short rows in large grids (above).
-            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX, DOT>), dim3(items), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX>), dim3(items), dim3(256), 0, st, p);
     } else {
-        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX, DOT>), dim3((items + 3) / 4), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX>), dim3((items + 3) / 4), dim3(256), 0, st, p);
     }
 }
 
@@ -1566,9 +1414,7 @@ int launch_b1(const MvParams &pin, hipStream_t st) {
         p.clk = g_clk_slots + 2 * (size_t)CLOCK_WAVES * g_clk_next;
         g_clk_next = (g_clk_next + 1) % g_clk_n;
     }
-    if (p.amax_v && g_tune_mv_dot) launch_b1_n<1, true, true>(p, st);
-    else if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
-    else if (p.n_seg == 1 && g_tune_mv_dot) launch_b1_n<1, false, true>(p, st);  // VALU dot products
+    if (p.amax_v) launch_b1_n<1, true>(p, st);  // LM head: one segment, one slot
     else if (p.n_seg == 1) launch_b1_n<1>(p, st);
     else if (p.n_seg == 2) launch_b1_n<2>(p, st);
     else launch_b1_n<3>(p, st);
@@ -1625,31 +1471,6 @@ int launch_q6k_mv_grouped_x2(const void *wa, const void *wb, size_t expert_strid
     p.blocks = blocks;
     p.act_per_slot = act_per_slot;
     return launch_b1(p, st);
-}
-
-int launch_q6k_gateup_silu(const void *w_gate, const void *w_up, size_t expert_stride,
-                           const float *logits, int n_expert, int n_used, int32_t *ids_out,
-                           float *w_out, int *stats, const int8_t *aq, const float *ad, float *act,
-                           int rows, int blocks, hipStream_t st) {
-    if (blocks > 16 || n_expert > ROUTE_MAX_EXPERTS || n_used > ROUTE_MAX_USED) return -1;
-    MvParams p = {};
-    const void *ws[1] = {w_gate};
-    float *ys[1] = {act};
-    const int rs[1] = {rows};
-    set_segments(p, 1, ws, ys, rs, n_used);
-    p.expert_stride = expert_stride;
-    p.aq = aq;
-    p.ad = ad;
-    p.blocks = blocks;
-    p.route_l = logits;
-    p.n_expert = n_expert;
-    p.n_used = n_used;
-    p.ids_out = ids_out;
-    p.w_out = w_out;
-    p.stats = stats;
-    hipLaunchKernelGGL(q6k_gateup_silu, dim3(p.items), dim3(512), 0, st, p, (const uint8_t *)w_up,
-                       act);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
@@ -1789,18 +1610,16 @@ int launch_q6k_mv_batched_x3(const void *const w[3], float *const y[3], const in
 }
 
 int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *ids,
-                            const int8_t *aq, const float *ad, const float *act,
-                            const float *weights, const float *res, float *out, int rows,
-                            int blocks, int n_slots, hipStream_t st) {
+                            const int8_t *aq, const float *ad, const float *weights,
+                            const float *res, float *out, int rows, int blocks, int n_slots,
+                            hipStream_t st) {
     if (n_slots <= 0 || n_slots > 16) return -1;
-    if (act && blocks > DOWN_ACT_BLOCKS) return -1;
     DownParams p;
     p.w = (const uint8_t *)w;
     p.expert_stride = expert_stride;
     p.ids = ids;
     p.aq = aq;
     p.ad = ad;
-    p.act = act;
     p.weights = weights;
     p.res = res;
     p.out = out;
@@ -1808,10 +1627,7 @@ int launch_q6k_down_combine(const void *w, size_t expert_stride, const int32_t *
     p.tiles = (rows + TILE_ROWS - 1) / TILE_ROWS;
     p.blocks = blocks;
     p.n_slots = n_slots;
-    if (act)
-        hipLaunchKernelGGL(q6k_down_combine<true>, dim3(p.tiles), dim3(64 * n_slots), 0, st, p);
-    else
-        hipLaunchKernelGGL(q6k_down_combine<false>, dim3(p.tiles), dim3(64 * n_slots), 0, st, p);
+    hipLaunchKernelGGL(q6k_down_combine, dim3(p.tiles), dim3(64 * n_slots), 0, st, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -135,71 +135,6 @@ __device__ __forceinline__ void block_terms(const BlockRegs &r, const MaskSel &m
     t_odd = dd * (float)ao;
 }
 
-// The same per-block terms with the integer part on the VALU instead of the
-// matrix cores. The wave first stages its block's activation in LDS
-// class-major as int16 (a16[c][m] = a[8m + c]); then per class c the lane's
-// 8 weights (m = 8s .. 8s+7, two per scale group) meet their activations in
-// four v_dot2_i32_i16 (one per group pair), and the group scales are applied
-// with 24-bit multiplies. The integer aux32 is the MFMA path's exactly, and
-// reduce_classes and the float terms are shared, so the bits are the same.
-typedef short s16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ void load_block_dot(BlockRegs &r, const uint8_t *seg, const int8_t *aq,
-                                               const float *ad, int b, int lane, int n) {
-    r.q0 = *(const uint4 *)(seg + 16 * lane);
-    r.q1 = *(const uint4 *)(seg + SEG_PART + 16 * lane);
-    r.q2 = *(const uint4 *)(seg + 2 * SEG_PART + 16 * lane);
-    r.scw = *(const uint32_t *)(seg + SEG_SC + 4 * lane);
-    r.dh = *(const uint16_t *)(seg + SEG_D + 2 * n);
-    r.g.x = *(const uint32_t *)(aq + (size_t)b * QK_K + 4 * lane);  // quants 4 lane .. 4 lane + 3
-    r.ad = ad[b];
-}
-
-__device__ __forceinline__ s16x2_t minus32_pair(uint32_t word, uint32_t sel) {
-    const uint32_t v = __builtin_amdgcn_perm(0u, word, sel);  // two codes in 16-bit lanes
-    return __builtin_bit_cast(s16x2_t, v) - s16x2_t{32, 32};
-}
-
-__device__ __forceinline__ void block_terms_dot(const BlockRegs &r, int16_t *a16, int lane, int n,
-                                                int s, float &t_even, float &t_odd) {
-    {
-        const uint32_t qw = r.g.x;
-        const int m = lane >> 1, c0 = 4 * (lane & 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a16[(c0 + i) * 32 + m] = (int16_t)(int8_t)(qw >> (8 * i));
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const uint32_t nib[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    const uint32_t hb[4] = {r.q2.x, r.q2.y, r.q2.z, r.q2.w};
-    const int sc0 = __builtin_amdgcn_sbfe(r.scw, 0, 8), sc1 = __builtin_amdgcn_sbfe(r.scw, 8, 8);
-    const int sc2 = __builtin_amdgcn_sbfe(r.scw, 16, 8), sc3 = __builtin_amdgcn_sbfe(r.scw, 24, 8);
-    int acc[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const uint4 av = *(const uint4 *)(a16 + c * 32 + 8 * s);  // (m 8s, 8s+1), (8s+2, 8s+3), ...
-        const uint64_t codes = (uint64_t)unpack_codes(nib, hb, c);
-        const uint32_t lo = (uint32_t)codes, hi = (uint32_t)(codes >> 32);
-        const int t0 = __builtin_amdgcn_sdot2(minus32_pair(lo, 0x0C010C00u),
-                                              __builtin_bit_cast(s16x2_t, av.x), 0, false);
-        const int t1 = __builtin_amdgcn_sdot2(minus32_pair(lo, 0x0C030C02u),
-                                              __builtin_bit_cast(s16x2_t, av.y), 0, false);
-        const int t2 = __builtin_amdgcn_sdot2(minus32_pair(hi, 0x0C010C00u),
-                                              __builtin_bit_cast(s16x2_t, av.z), 0, false);
-        const int t3 = __builtin_amdgcn_sdot2(minus32_pair(hi, 0x0C030C02u),
-                                              __builtin_bit_cast(s16x2_t, av.w), 0, false);
-        int v = __mul24(sc0, t0);
-        v = __mul24(sc1, t1) + v;
-        v = __mul24(sc2, t2) + v;
-        acc[c] = __mul24(sc3, t3) + v;
-    }
-    int ae, ao;
-    reduce_classes(acc, ae, ao);
-    const float dd = f16_bits_to_f32(r.dh) * r.ad;
-    t_even = dd * (float)ae;
-    t_odd = dd * (float)ao;
-}
-
 template <int KS>
 __device__ __forceinline__ void consume_terms(int b, float te, float to, float &se, float &so,
                                               float (*terms)[TILE_ROWS][8], int n, int s) {

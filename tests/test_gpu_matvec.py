@@ -199,25 +199,3 @@ def test_every_k_split_is_bit_identical(gpu, rows, blocks):
     finally:
         L.llamd_hip_tune(b"mv_ks", 0)
         dw.close()
-
-
-@pytest.mark.parametrize("rows,blocks", [(48, 8), (40, 5), (33, 3), (2048, 8), (768, 16), (1, 1)])
-def test_valu_dot_variant_is_bit_identical(gpu, rows, blocks):
-    """The batch-1 kernel with its integer part on v_dot2 (tune key mv_dot)
-    instead of the matrix cores gives the same bits at every K split."""
-    from llamd_rs_amd._lib import lib
-    w = H.weights(rows, blocks, 90 + blocks)
-    x = H.sample(blocks * QK_K, 91 + rows)
-    act = gpu.quantize_q8k_on_device(x)
-    want = cpu_rows(w, rows, blocks, act)
-    dw = gpu.DeviceWeights.upload(w, rows, blocks)
-    L = lib()
-    try:
-        assert L.llamd_hip_tune(b"mv_dot", 1) == 0
-        for ks in (1, 4, 8, 0):
-            L.llamd_hip_tune(b"mv_ks", ks)
-            assert bits_equal(dw.matvec(act), want), ks
-    finally:
-        L.llamd_hip_tune(b"mv_dot", 0)
-        L.llamd_hip_tune(b"mv_ks", 0)
-        dw.close()
