@@ -803,3 +803,72 @@ def test_host_calls_from_several_threads(gpu):
     finally:
         for p in ptrs:
             L().llamd_rocm_release(p)
+
+
+def _fold_rows(k, rng):
+    """Router rows that stress the in-order fold: random products, exact
+    cancellation, zeros of both signs, a wide exponent range, values on a
+    coarse grid (ties of round-to-nearest), subnormals, non-finite terms and
+    a sum that overflows; with x = 1 each row's products are its values."""
+    f32 = np.float32
+    rows = []
+    for t in range(6):
+        rows.append((rng.normal(0, 0.02, k) * rng.normal(0, 1, k)).astype(f32))
+    v = rng.normal(0, 1, k // 2).astype(f32)
+    rows.append(np.concatenate([v, -v[::-1]]))
+    v = rng.normal(0, 1, k).astype(f32)
+    v[1::2] = -v[::2]
+    rows.append(v)
+    rows.append(np.zeros(k, f32))
+    rows.append(-np.zeros(k, f32))
+    v = -np.zeros(k, f32)
+    v[k // 3] = 0.0
+    rows.append(v)
+    rows.append((rng.normal(0, 1, k) * 2.0 ** rng.integers(-60, 60, k)).astype(f32))
+    rows.append((rng.integers(-1000, 1000, k) * 2.0 ** -10).astype(f32))
+    v = np.full(k, f32(1.0))
+    v[::3] = f32(2.0 ** -24)
+    rows.append(v)
+    rows.append((rng.normal(0, 1, k) * 1e-39).astype(f32))
+    v = rng.normal(0, 1, k).astype(f32)
+    v[:2] = f32(3e38)
+    rows.append(v)
+    v = rng.normal(0, 1, k).astype(f32)
+    v[5] = np.nan
+    rows.append(v)
+    v = rng.normal(0, 1, k).astype(f32)
+    v[k - 1] = np.inf
+    rows.append(v)
+    rows.append(rng.normal(1, 0.1, k).astype(f32))
+    v = (rng.normal(0, 1, k) * 2.0 ** -20).astype(f32)
+    v[0] = f32(1.0)
+    v[k // 2] = f32(-1.0)
+    rows.append(v)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("k", [256, 768, 2048])
+def test_router_fold_adversarial_rows(gpu, k):
+    """The F32 router matvec's in-order fold (model.rs:253-262) on rows built
+    to break a shortcut: every logit bit-identical to the CPU's sequential
+    sum from -0.0, NaN and inf where the CPU has them."""
+    rng = np.random.default_rng(k)
+    rw = _fold_rows(k, rng)
+    n_expert = rw.shape[0]
+    x = np.ones(k, np.float32)
+    RW, X, LG = dev(gpu, rw), dev(gpu, x), gpu.DeviceBuffer(n_expert * 4)
+    L().llamd_fwd_matvec_f32(RW.ptr, X.ptr, LG.ptr, k, n_expert)
+    sync()
+    got = down(LG, n_expert)
+    want = O.matvec_f32(rw, n_expert, k, x)
+    bad = [i for i in range(n_expert)
+           if not (np.isnan(want[i]) and np.isnan(got[i]))
+           and got[i:i + 1].view(np.uint32)[0] != want[i:i + 1].view(np.uint32)[0]]
+    assert not bad, [(i, got[i], want[i]) for i in bad]
+    # and a real router on a normal activation, every row
+    rw2 = (rng.normal(0, 0.02, (128, k))).astype(np.float32)
+    x2 = rng.normal(0, 1, k).astype(np.float32)
+    RW2, X2, LG2 = dev(gpu, rw2), dev(gpu, x2), gpu.DeviceBuffer(128 * 4)
+    L().llamd_fwd_matvec_f32(RW2.ptr, X2.ptr, LG2.ptr, k, 128)
+    sync()
+    assert bits_equal(down(LG2, 128), O.matvec_f32(rw2, 128, k, x2))
