@@ -38,6 +38,10 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results in VGPRs: no accumulator-register reads after every MFMA
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # leading scalar kernel arguments arrive preloaded in SGPRs (gfx950's
+    # kernarg preload): a latency-bound launch starts its first loads without
+    # waiting for the kernarg segment
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     f"-I{ROOT / 'include'}",

@@ -80,22 +80,24 @@ __device__ __forceinline__ double read_lane(double v, int l) {
 }
 
 // The run of terms a thread holds: thread t of the workgroup owns terms
-// [t m, t m + m) of the row, m = ceil(n / blockDim.x) <= XSUM_M, in registers.
+// [t m, t m + m) of the row, m = ceil(n / threads) <= XSUM_M, in registers.
 constexpr int XSUM_M = 8;
 
-__device__ __forceinline__ int xsum_run(int n) { return (n + (int)blockDim.x - 1) / (int)blockDim.x; }
+// (nt: the workgroup's thread count, a constant where the caller knows it, so
+// that the kernel needs no implicit kernel arguments)
+__device__ __forceinline__ int xsum_run(int n, int nt) { return (n + nt - 1) / nt; }
 
 // All threads of the workgroup call this (it synchronises the workgroup);
-// blockDim.x is a multiple of 64, at most 64 * XSUM_MAX_WAVES, and at least
-// n / XSUM_M. v[0..cnt) are this thread's terms j0 .. j0 + cnt - 1 (j0 =
-// threadIdx.x * xsum_run(n); cnt = what remains of the row, at most the run),
+// nt (the thread count) is a multiple of 64, at most 64 * XSUM_MAX_WAVES, and
+// at least n / XSUM_M. v[0..cnt) are this thread's terms j0 .. j0 + cnt - 1 (j0 =
+// threadIdx.x * xsum_run(n, nt); cnt = what remains of the row, at most the run),
 // non-negative or NaN. term(j) recomputes term j for the serial fallback.
 // Returns the reference's sum on every thread.
 template <class Term>
-__device__ float exact_sum_nonneg(const float (&vin)[XSUM_M], int n, ExactSumLds &L, Term term) {
+__device__ float exact_sum_nonneg(const float (&vin)[XSUM_M], int n, int nt, ExactSumLds &L, Term term) {
     constexpr int M = XSUM_M;
-    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
-    const int m = xsum_run(n);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    const int m = xsum_run(n, nt);
     const int j0 = min(tid * m, n), cnt_here = min(m, n - j0);
     float v[M];
 #pragma unroll

@@ -272,7 +272,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // wrow (or null): a router row this wave stages into wdst (LDS) meanwhile.
 __device__ void norm_prologue(const DecodeParams &p, float *xs, ExactSumLds &xl, bool write_sum,
                               const float *wrow, float4 *wdst) {
-    const int m = xsum_run(p.k), j0 = min((int)threadIdx.x * m, p.k - 1), lane = threadIdx.x & 63;
+    const int m = xsum_run(p.k, 512), j0 = min((int)threadIdx.x * m, p.k - 1), lane = threadIdx.x & 63;
     float a[XSUM_M], b[XSUM_M], v[XSUM_M], sq[XSUM_M];
 #pragma unroll
     for (int j = 0; j < XSUM_M; ++j) {
@@ -297,7 +297,7 @@ __device__ void norm_prologue(const DecodeParams &p, float *xs, ExactSumLds &xl,
             if (64 * j < p.k / 4) *(f4v *)&wdst[64 * j + lane] = wr[j];
     }
     const float *na = p.norm_a, *nb = p.norm_b;
-    const float sum = exact_sum_nonneg(sq, p.k, xl, [na, nb](int i) {
+    const float sum = exact_sum_nonneg(sq, p.k, 512, xl, [na, nb](int i) {
         const float t = na[i] + nb[i];
         return t * t;
     });

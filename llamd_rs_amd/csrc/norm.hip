@@ -30,8 +30,8 @@ constexpr int NORM_MAX = 8192;  // longest row (the exact sum's bound holds to 8
 // This thread's run of a row (xsum_run(n) contiguous elements starting at
 // threadIdx.x * run) into registers; lanes past the row's end read its last
 // element (unconditional loads) and are ignored by the callers.
-__device__ __forceinline__ void load_run(const float *src, int n, float (&v)[XSUM_M]) {
-    const int m = xsum_run(n), j0 = min((int)threadIdx.x * m, n - 1);
+__device__ __forceinline__ void load_run(const float *src, int n, int nt, float (&v)[XSUM_M]) {
+    const int m = xsum_run(n, nt), j0 = min((int)threadIdx.x * m, n - 1);
     if ((m & 3) == 0 && m <= XSUM_M && j0 + m <= n && ((uintptr_t)(src + j0) & 15) == 0) {
 #pragma unroll
         for (int k = 0; k < XSUM_M; k += 4) {
@@ -51,12 +51,12 @@ __device__ __forceinline__ void load_run(const float *src, int n, float (&v)[XSU
 // vals (load_run), the sum in the reference's order, by the whole workgroup
 // (every thread calls it; every thread gets the scale). src is the row in
 // global memory, read only by the serial fallback.
-__device__ float row_scale_block(const float *src, const float (&vals)[XSUM_M], int n, float eps,
-                                 ExactSumLds &L) {
+__device__ float row_scale_block(const float *src, const float (&vals)[XSUM_M], int n, int nt,
+                                 float eps, ExactSumLds &L) {
     float sq[XSUM_M];
 #pragma unroll
     for (int k = 0; k < XSUM_M; ++k) sq[k] = vals[k] * vals[k];
-    const float sum = exact_sum_nonneg(sq, n, L, [src](int i) {
+    const float sum = exact_sum_nonneg(sq, n, nt, L, [src](int i) {
         const float v = src[i];
         return v * v;
     });
@@ -72,16 +72,20 @@ inline int row_threads(int n) {
 
 // out[r][i] = (x[r][i] * scale_r) * w[i % w_len], one workgroup per row
 // (rows = heads for the per-head QK norm). w may be null (no multiply).
-__global__ __launch_bounds__(1024) void rms_norm_mul(const float *x, const float *w, float *out,
+// NT: the thread count when the launch fixes it (no implicit kernel
+// arguments then), 0 for any other (blockDim).
+template <int NT>
+__global__ __launch_bounds__(NT ? NT : 1024) void rms_norm_mul(const float *x, const float *w, float *out,
                                                      int n, int w_len, float eps) {
+    const int nt = NT ? NT : (int)blockDim.x;
     __shared__ ExactSumLds xs;
     const int r = blockIdx.x;
     const float *src = x + (size_t)r * n;
     float v[XSUM_M];
-    load_run(src, n, v);
-    const float scale = row_scale_block(src, v, n, eps, xs);
+    load_run(src, n, nt, v);
+    const float scale = row_scale_block(src, v, n, nt, eps, xs);
     float *dst = out + (size_t)r * n;
-    const int m = xsum_run(n), j0 = (int)threadIdx.x * m;
+    const int m = xsum_run(n, nt), j0 = (int)threadIdx.x * m;
     if (m <= XSUM_M) {
 #pragma unroll
         for (int k = 0; k < XSUM_M; ++k) {
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(1024) void rms_norm_mul(const float *x, const float
             }
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        for (int i = threadIdx.x; i < n; i += nt) {
             const float y = src[i] * scale;
             dst[i] = w ? y * w[w_len == n ? i : i % w_len] : y;
         }
@@ -102,9 +106,11 @@ __global__ __launch_bounds__(1024) void rms_norm_mul(const float *x, const float
 // One row of n = 256 * blocks per workgroup (row blockIdx.x of x, out, qs,
 // d, inv_out): the workgroup finds the scale, then wave k forms block k (and
 // k + waves, ...) of (x * scale) * w and quantizes it.
-__global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const float *w, float *out,
+template <int NT>
+__global__ __launch_bounds__(NT ? NT : 1024) void rms_norm_quant(const float *x, const float *w, float *out,
                                                        int8_t *qs, float *d, float *inv_out,
                                                        int n, float eps) {
+    const int nt = NT ? NT : (int)blockDim.x;
     __shared__ ExactSumLds xs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t r = blockIdx.x;
@@ -114,10 +120,10 @@ __global__ __launch_bounds__(1024) void rms_norm_quant(const float *x, const flo
     d += r * (n / QK_K);
     if (inv_out) inv_out += r;
     float v0[XSUM_M];
-    load_run(x, n, v0);
-    const float scale = row_scale_block(x, v0, n, eps, xs);
+    load_run(x, n, nt, v0);
+    const float scale = row_scale_block(x, v0, n, nt, eps, xs);
     if (inv_out && threadIdx.x == 0) *inv_out = scale;
-    const int blocks = n / QK_K, waves = blockDim.x >> 6;
+    const int blocks = n / QK_K, waves = nt >> 6;
     for (int b = wave; b < blocks; b += waves) {
         const size_t o = (size_t)b * QK_K + 4 * lane;
         const float4 xv = *(const float4 *)(x + o);
@@ -171,30 +177,32 @@ __global__ __launch_bounds__(64) void qk_norm_rope_store(float *q, const float *
 
 // ffn_inp = x + o (the attention residual, layer.rs:170), then
 // out = rms_norm(ffn_inp) * w: one row, one workgroup.
-__global__ __launch_bounds__(1024) void add_rms_norm_mul(const float *x, const float *o,
+template <int NT>
+__global__ __launch_bounds__(NT ? NT : 1024) void add_rms_norm_mul(const float *x, const float *o,
                                                          const float *w, float *sum_out,
                                                          float *out, int n, float eps) {
+    const int nt = NT ? NT : (int)blockDim.x;
     __shared__ ExactSumLds xs;
-    const int m = xsum_run(n), j0 = (int)threadIdx.x * m;
+    const int m = xsum_run(n, nt), j0 = (int)threadIdx.x * m;
     float v[XSUM_M], ov[XSUM_M];
-    load_run(x, n, v);
-    load_run(o, n, ov);
+    load_run(x, n, nt, v);
+    load_run(o, n, nt, ov);
 #pragma unroll
     for (int k = 0; k < XSUM_M; ++k) {
         v[k] = v[k] + ov[k];
         if (k < m && j0 + k < n) sum_out[j0 + k] = v[k];
     }
     if (m > XSUM_M)
-        for (int i = threadIdx.x; i < n; i += blockDim.x) sum_out[i] = x[i] + o[i];
+        for (int i = threadIdx.x; i < n; i += nt) sum_out[i] = x[i] + o[i];
     // the serial fallback reads sum_out back; exact_sum_nonneg's barriers
     // order these stores before it
-    const float scale = row_scale_block(sum_out, v, n, eps, xs);
+    const float scale = row_scale_block(sum_out, v, n, nt, eps, xs);
     if (m <= XSUM_M) {
 #pragma unroll
         for (int k = 0; k < XSUM_M; ++k)
             if (k < m && j0 + k < n) out[j0 + k] = (v[k] * scale) * w[j0 + k];
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (sum_out[i] * scale) * w[i];
+        for (int i = threadIdx.x; i < n; i += nt) out[i] = (sum_out[i] * scale) * w[i];
     }
 }
 
@@ -213,14 +221,22 @@ int launch_qk_norm_rope_store(float *q, const float *k, const float *v, const fl
 int launch_add_rms_norm_mul(const float *x, const float *o, const float *w, float *sum_out,
                             float *out, int n, float eps, hipStream_t st) {
     if (n <= 0 || n > NORM_MAX || !w) return -1;
-    hipLaunchKernelGGL(add_rms_norm_mul, dim3(1), dim3(row_threads(n)), 0, st, x, o, w, sum_out, out, n, eps);
+    const int nt = row_threads(n);
+    if (nt == 512)
+        hipLaunchKernelGGL(add_rms_norm_mul<512>, dim3(1), dim3(nt), 0, st, x, o, w, sum_out, out, n, eps);
+    else
+        hipLaunchKernelGGL(add_rms_norm_mul<0>, dim3(1), dim3(nt), 0, st, x, o, w, sum_out, out, n, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, int n, int w_len,
                         float eps, hipStream_t st) {
     if (rows <= 0 || n <= 0 || n > NORM_MAX || (w && w_len <= 0)) return -1;
-    hipLaunchKernelGGL(rms_norm_mul, dim3(rows), dim3(row_threads(n)), 0, st, x, w, out, n, w_len, eps);
+    const int nt = row_threads(n);
+    if (nt == 512)
+        hipLaunchKernelGGL(rms_norm_mul<512>, dim3(rows), dim3(nt), 0, st, x, w, out, n, w_len, eps);
+    else
+        hipLaunchKernelGGL(rms_norm_mul<0>, dim3(rows), dim3(nt), 0, st, x, w, out, n, w_len, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -228,8 +244,12 @@ int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs
                           float *inv_out, int n, float eps, hipStream_t st, int rows) {
     if (n <= 0 || n % QK_K || n > NORM_MAX || !w || rows <= 0) return -1;
     const int waves = n / QK_K < 16 ? n / QK_K : 16;
-    hipLaunchKernelGGL(rms_norm_quant, dim3(rows), dim3(64 * waves), 0, st, x, w, out, qs, d, inv_out,
-                       n, eps);
+    if (waves == 8)
+        hipLaunchKernelGGL(rms_norm_quant<512>, dim3(rows), dim3(512), 0, st, x, w, out, qs, d, inv_out,
+                           n, eps);
+    else
+        hipLaunchKernelGGL(rms_norm_quant<0>, dim3(rows), dim3(64 * waves), 0, st, x, w, out, qs, d,
+                           inv_out, n, eps);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

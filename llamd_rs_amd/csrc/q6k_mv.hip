@@ -77,21 +77,22 @@ struct MvParams {
 
 // In-kernel clock: wave w (flat index over the grid) stores its start at
 // clk[w] and its end at clk[CLOCK_WAVES + w], s_memrealtime ticks, with plain
-// vector stores (one writer per word: no contention, no atomics). The end is
-// stored on every exit of the kernel.
+// vector stores (one writer per word: no contention, no atomics). The start
+// is read first thing and both are stored on every exit of the kernel, so
+// the record's pointer is not needed before the kernel's first loads.
 constexpr int CLOCK_WAVES = 1024;
+template <int WAVES_PER_WG>
 struct ClockEnd {
-    unsigned long long *clk;  // this wave's start word, or null
+    unsigned long long *r;  // the launch's record (null: no clock)
+    unsigned long long t0;
     __device__ ~ClockEnd() {
-        if (clk && (threadIdx.x & 63) == 0) clk[CLOCK_WAVES] = __builtin_amdgcn_s_memrealtime();
+        const int w = (int)(blockIdx.x * WAVES_PER_WG + (threadIdx.x >> 6));
+        if (r && w < CLOCK_WAVES && (threadIdx.x & 63) == 0) {
+            r[w] = t0;
+            r[CLOCK_WAVES + w] = __builtin_amdgcn_s_memrealtime();
+        }
     }
 };
-__device__ __forceinline__ unsigned long long *clock_start(unsigned long long *rec) {
-    const int w = (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
-    if (!rec || w >= CLOCK_WAVES) return nullptr;
-    if ((threadIdx.x & 63) == 0) rec[w] = __builtin_amdgcn_s_memrealtime();
-    return rec + w;
-}
 
 // One (slot, 16-row tile) item per KS waves of a 4-wave (KS = 8: 8-wave) workgroup; wave kc of
 // the item takes blocks [kc*bpc, (kc+1)*bpc) with the next block's loads in
@@ -99,29 +100,77 @@ __device__ __forceinline__ unsigned long long *clock_start(unsigned long long *r
 // meet in LDS and are folded in block order -- the same additions in the same
 // order as a single wave walking every block, so splitting K changes the
 // latency, never the bits.
-template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false>
-__global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) {
+//
+// The fields the first loads depend on come as leading scalar arguments,
+// which gfx950 preloads into SGPRs at dispatch (kernarg preload): the first
+// weight and activation loads issue without waiting for the kernarg segment.
+//
+// PX is MvParams, or MvLite for the plain matvec (one segment, no routing
+// prologue, no arg-max): a 40-byte block instead of 216 bytes, since the
+// size of the kernarg segment shows in the launch cost of a small matvec.
+struct MvLite {
+    float *y;
+    size_t expert_stride;
+    unsigned long long *clk;
+    int rows, n_slots;
+};
+__device__ __forceinline__ MvParams expand_params(const MvParams &p) { return p; }
+__device__ __forceinline__ MvParams expand_params(const MvLite &l) {
+    MvParams p = {};
+    p.seg0.y = l.y;
+    p.seg0.rows = l.rows;
+    p.expert_stride = l.expert_stride;
+    p.clk = l.clk;
+    p.n_slots = l.n_slots;
+    p.n_seg = 1;
+    return p;
+}
+
+template <int KS, bool ROUTE = false, int NSEG = 1, bool AMAX = false, class PX = MvParams>
+__global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(
+    const uint8_t *w0, const int8_t *aq0, const float *ad0, const int32_t *ids0, int blocks0,
+    int tiles0, int items0, int act_per_slot0, PX px) {
+    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+    MvParams p = expand_params(px);
+    p.seg0.w = w0;
+    p.aq = aq0;
+    p.ad = ad0;
+    p.ids = ids0;
+    p.blocks = blocks0;
+    p.seg0.tiles = tiles0;
+    p.items = items0;
+    p.act_per_slot = act_per_slot0;
     constexpr int IPW = KS >= 4 ? 1 : 4 / KS;   // items per workgroup
     constexpr int MAXB = 16;                    // blocks per row held in LDS (KS > 1)
     __shared__ float terms[KS > 1 ? IPW : 1][KS > 1 ? MAXB : 1][TILE_ROWS][8];
     const int lane = threadIdx.x & 63;
-    // every kernarg field the common path reads, fetched in one batch up front
-    asm volatile("" ::"s"(p.seg0.w), "s"(p.seg0.y), "s"(p.seg0.rows), "s"(p.seg0.tiles),
-                 "s"(p.aq), "s"(p.ad), "s"(p.ids), "s"(p.expert_stride), "s"(p.items),
-                 "s"(p.blocks), "s"(p.act_per_slot));
-    const ClockEnd clock_end{clock_start(p.clk)};
+    // the parameter block's fields that the item's segment and the weight
+    // address need, fetched in one batch up front (not one dependent scalar
+    // load after another)
+    if constexpr (NSEG > 1)
+        asm volatile("" ::"s"(p.seg1.w), "s"(p.seg1.first), "s"(p.seg1.tiles), "s"(p.seg2.w),
+                     "s"(p.seg2.first), "s"(p.seg2.tiles), "s"(p.expert_stride), "s"(p.seg0.y),
+                     "s"(p.seg0.rows));
+    else
+        asm volatile("" ::"s"(p.expert_stride), "s"(p.seg0.y), "s"(p.seg0.rows));
+    const ClockEnd<(KS > 4 ? KS : 4)> clock_end{p.clk, t_start};
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int kc = wave % KS;
     const int local = wave / KS;
     const int item = blockIdx.x * IPW + local;
     const bool live = item < p.items;
     // the item's segment, chosen with scalar selects (no indexed kernarg load)
+    // field by field (a whole-struct select becomes an indexed stack copy)
     MvSeg sgm = p.seg0;
+    sgm.first = 0;  // segment 0 always starts the item numbering
     if constexpr (NSEG > 1) {
-        if (item >= p.seg1.first) sgm = p.seg1;
-    }
-    if constexpr (NSEG > 2) {
-        if (item >= p.seg2.first) sgm = p.seg2;
+        const bool in1 = item >= px.seg1.first;
+        const bool in2 = NSEG > 2 && item >= px.seg2.first;
+        sgm.w = in2 ? px.seg2.w : in1 ? px.seg1.w : sgm.w;
+        sgm.y = in2 ? px.seg2.y : in1 ? px.seg1.y : sgm.y;
+        sgm.rows = in2 ? px.seg2.rows : in1 ? px.seg1.rows : sgm.rows;
+        sgm.tiles = in2 ? px.seg2.tiles : in1 ? px.seg1.tiles : sgm.tiles;
+        sgm.first = in2 ? px.seg2.first : in1 ? px.seg1.first : 0;
     }
     const int pos = item - sgm.first;
     const int slot = live ? pos / sgm.tiles : 0;
@@ -157,8 +206,9 @@ __global__ __launch_bounds__(KS > 4 ? 64 * KS : 256) void q6k_mv_b1(MvParams p) 
     const int act = p.act_per_slot ? slot / p.act_per_slot : 0;
     const int8_t *aq = p.aq + (size_t)act * p.blocks * QK_K;
     const float *ad = p.ad + (size_t)act * p.blocks;
-    const uint8_t *seg0 = sgm.w + (size_t)expert * p.expert_stride +
-                          (size_t)t * p.blocks * SEG_BYTES;
+    // (without ids, expert 0: no kernarg-segment field on the way to the first load)
+    const uint8_t *wexp = (ROUTE || p.ids) ? sgm.w + (size_t)expert * p.expert_stride : sgm.w;
+    const uint8_t *seg0 = wexp + (size_t)t * p.blocks * SEG_BYTES;
 
     const int bpc = (p.blocks + KS - 1) / KS;
     const int b0 = kc * bpc;
@@ -1376,6 +1426,13 @@ void set_segments(MvParams &p, int n, const void *const *w, float *const *y, con
     p.n_slots = n_slots;
 }
 
+// q6k_mv_b1's preloaded leading arguments, then the whole parameter block
+#define B1_ARGS(p) (p).seg0.w, (p).aq, (p).ad, (p).ids, (p).blocks, (p).seg0.tiles, (p).items, \
+                   (p).act_per_slot, (p)
+// ... or, for the plain matvec, the compact one
+#define B1_LITE(p) (p).seg0.w, (p).aq, (p).ad, (p).ids, (p).blocks, (p).seg0.tiles, (p).items, \
+                   (p).act_per_slot, MvLite{(p).seg0.y, (p).expert_stride, (p).clk, (p).seg0.rows, (p).n_slots}
+
 template <int NSEG, bool AMAX = false>
 void launch_b1_n(const MvParams &p, hipStream_t st) {
     const int items = p.items;
@@ -1390,17 +1447,28 @@ void launch_b1_n(const MvParams &p, hipStream_t st) {
     // tiles four waves stay ahead (512 tiles: 2.98 vs 3.12 us).
     const int ks = g_tune_mv_ks ? g_tune_mv_ks
                                 : (p.blocks > 4 && items <= 384 ? 8 : (p.blocks <= 4 && items >= 1024 ? 1 : 0));
+    constexpr bool LITE = NSEG == 1 && !AMAX;
     if (p.blocks <= 16 && (ks == 4 || ks == 8 || ks == 0)) {
-        if (ks == 8)
-            hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX>), dim3(items), dim3(512), 0, st, p);
-        else
+        if (ks == 8) {
+            if constexpr (LITE)
+                hipLaunchKernelGGL((q6k_mv_b1<8, false, 1, false, MvLite>), dim3(items), dim3(512), 0, st, B1_LITE(p));
+            else
+                hipLaunchKernelGGL((q6k_mv_b1<8, false, NSEG, AMAX>), dim3(items), dim3(512), 0, st, B1_ARGS(p));
+        } else {
             // Measured on MI355X (gate/up/down/q_proj/LM-head shapes): four
             // waves per tile, each on a quarter of the row, beat one wave per
             // tile -- more loads in flight per tile and shorter per-wave
             // chains -- except for short rows in large grids (above).
-            hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX>), dim3(items), dim3(256), 0, st, p);
+            if constexpr (LITE)
+                hipLaunchKernelGGL((q6k_mv_b1<4, false, 1, false, MvLite>), dim3(items), dim3(256), 0, st, B1_LITE(p));
+            else
+                hipLaunchKernelGGL((q6k_mv_b1<4, false, NSEG, AMAX>), dim3(items), dim3(256), 0, st, B1_ARGS(p));
+        }
     } else {
-        hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX>), dim3((items + 3) / 4), dim3(256), 0, st, p);
+        if constexpr (LITE)
+            hipLaunchKernelGGL((q6k_mv_b1<1, false, 1, false, MvLite>), dim3((items + 3) / 4), dim3(256), 0, st, B1_LITE(p));
+        else
+            hipLaunchKernelGGL((q6k_mv_b1<1, false, NSEG, AMAX>), dim3((items + 3) / 4), dim3(256), 0, st, B1_ARGS(p));
     }
 }
 
@@ -1493,7 +1561,7 @@ int launch_q6k_mv_routed(const void *w, const void *w_b, size_t expert_stride,
     p.ids_out = ids_out;
     p.w_out = w_out;
     p.stats = stats;
-    hipLaunchKernelGGL((q6k_mv_b1<4, true, 2>), dim3(p.items), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((q6k_mv_b1<4, true, 2>), dim3(p.items), dim3(256), 0, st, B1_ARGS(p));
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
