@@ -97,9 +97,11 @@ __global__ __launch_bounds__(256) void q6k_retile(Q6kSource s, int rows, int blo
 }
 
 // ---- memset without a memset node (graph-capture safe) -----------------------
+// (the grid-stride kernels below take their grid width as an argument: no
+// implicit kernel arguments, a smaller kernarg segment per launch)
 __global__ __launch_bounds__(256) void fill_bytes(uint8_t *p, uint8_t v, size_t head, size_t n16,
-                                                  size_t tail) {
-    const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, step = (size_t)gridDim.x * 256;
+                                                  size_t tail, unsigned nblk) {
+    const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, step = (size_t)nblk * 256;
     const uint32_t w = 0x01010101u * v;
     const uint4 q = make_uint4(w, w, w, w);
     for (size_t i = tid; i < head; i += step) p[i] = v;
@@ -113,8 +115,8 @@ __global__ __launch_bounds__(256) void fill_bytes(uint8_t *p, uint8_t v, size_t 
 // Natural-layout Q8_K quants (signed, or biased with `flip` = 0x80808080)
 // [n_act][blocks * 256] -> signed natural copy.
 __global__ __launch_bounds__(256) void act_unbias(const uint32_t *q, uint32_t flip, uint32_t *out,
-                                                  size_t n_dw) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_dw; i += (size_t)gridDim.x * 256)
+                                                  size_t n_dw, unsigned nblk) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_dw; i += (size_t)nblk * 256)
         out[i] = q[i] ^ flip;
 }
 
@@ -124,9 +126,9 @@ __global__ __launch_bounds__(256) void act_unbias(const uint32_t *q, uint32_t fl
 // chunk at n * 32, byte e / 8. Token slots past n_act are zero.
 __global__ __launch_bounds__(256) void act_to_chunks(const uint8_t *q, const float *d, uint8_t flip,
                                                      int n_act, int blocks, uint8_t *cq, float *cd,
-                                                     size_t n_bytes) {
+                                                     size_t n_bytes, unsigned nblk) {
     for (size_t D = (size_t)blockIdx.x * 256 + threadIdx.x; D < n_bytes;
-         D += (size_t)gridDim.x * 256) {
+         D += (size_t)nblk * 256) {
         const size_t kb = D >> 12;  // chunk * blocks + block
         const int w = (int)(D & 4095);
         const int k = (int)(kb / blocks), b = (int)(kb - (size_t)k * blocks);
@@ -232,21 +234,22 @@ __global__ __launch_bounds__(256) void kv_store(float *kc, float *vc, const floa
 
 // ---- elementwise (CpuBackend::add / mul / scale / silu, lib.rs:103-118) -----
 __global__ __launch_bounds__(256) void ew_binary(const float *a, const float *b, float *o, size_t n,
-                                                 int op) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+                                                 int op, unsigned nblk) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)nblk * 256)
         o[i] = op == 0 ? a[i] + b[i] : a[i] * b[i];
 }
 
-__global__ __launch_bounds__(256) void ew_scale(const float *x, float by, float *o, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+__global__ __launch_bounds__(256) void ew_scale(const float *x, float by, float *o, size_t n,
+                                                unsigned nblk) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)nblk * 256)
         o[i] = x[i] * by;
 }
 
-__global__ __launch_bounds__(256) void ew_silu(const float *x, float *o, size_t n) {
+__global__ __launch_bounds__(256) void ew_silu(const float *x, float *o, size_t n, unsigned nblk) {
     __shared__ uint64_t tab[32];
     if (threadIdx.x < 64) expf_ref_tab_fill(tab);
     __syncthreads();
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)nblk * 256)
         o[i] = silu_ref(x[i], tab);
 }
 
@@ -319,8 +322,9 @@ int launch_fill(void *p, int value, size_t bytes, hipStream_t st) {
     const size_t n16 = (bytes - head) / 16, tail = bytes - head - n16 * 16;
     const size_t work = std::max(std::max(head, tail), n16);
     const size_t grid = std::min<size_t>((work + 255) / 256, 8192);
-    hipLaunchKernelGGL(fill_bytes, dim3((unsigned)std::max<size_t>(grid, 1)), dim3(256), 0, st,
-                       (uint8_t *)p, (uint8_t)value, head, n16, tail);
+    const unsigned nblk = (unsigned)std::max<size_t>(grid, 1);
+    hipLaunchKernelGGL(fill_bytes, dim3(nblk), dim3(256), 0, st, (uint8_t *)p, (uint8_t)value, head,
+                       n16, tail, nblk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -328,8 +332,9 @@ int launch_act_unbias(const void *q, bool biased, int n_act, int blocks, int8_t 
                       hipStream_t st) {
     const size_t n_dw = (size_t)n_act * blocks * QK_K / 4;
     const size_t grid = std::min<size_t>((n_dw + 255) / 256, 4096);
-    hipLaunchKernelGGL(act_unbias, dim3((unsigned)std::max<size_t>(grid, 1)), dim3(256), 0, st,
-                       (const uint32_t *)q, biased ? 0x80808080u : 0u, (uint32_t *)out, n_dw);
+    const unsigned nblk = (unsigned)std::max<size_t>(grid, 1);
+    hipLaunchKernelGGL(act_unbias, dim3(nblk), dim3(256), 0, st, (const uint32_t *)q,
+                       biased ? 0x80808080u : 0u, (uint32_t *)out, n_dw, nblk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -339,7 +344,8 @@ int launch_act_to_chunks(const void *q, const float *d, bool biased, int n_act, 
     const size_t n_bytes = chunks * blocks * 4096;
     const size_t grid = std::min<size_t>((n_bytes + 255) / 256, 8192);
     hipLaunchKernelGGL(act_to_chunks, dim3((unsigned)grid), dim3(256), 0, st, (const uint8_t *)q, d,
-                       (uint8_t)(biased ? 0x80 : 0), n_act, blocks, (uint8_t *)cq, cd, n_bytes);
+                       (uint8_t)(biased ? 0x80 : 0), n_act, blocks, (uint8_t *)cq, cd, n_bytes,
+                       (unsigned)grid);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -372,11 +378,11 @@ int launch_ew(int op, const float *a, const float *b, float by, float *o, size_t
     if (!n) return 0;
     if (op == EW_ADD || op == EW_MUL)
         hipLaunchKernelGGL(ew_binary, dim3(ew_grid(n)), dim3(256), 0, st, a, b, o, n,
-                           op == EW_ADD ? 0 : 1);
+                           op == EW_ADD ? 0 : 1, ew_grid(n));
     else if (op == EW_SCALE)
-        hipLaunchKernelGGL(ew_scale, dim3(ew_grid(n)), dim3(256), 0, st, a, by, o, n);
+        hipLaunchKernelGGL(ew_scale, dim3(ew_grid(n)), dim3(256), 0, st, a, by, o, n, ew_grid(n));
     else if (op == EW_SILU)
-        hipLaunchKernelGGL(ew_silu, dim3(ew_grid(n)), dim3(256), 0, st, a, o, n);
+        hipLaunchKernelGGL(ew_silu, dim3(ew_grid(n)), dim3(256), 0, st, a, o, n, ew_grid(n));
     else
         return -1;
     return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -74,15 +74,15 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     kc += (size_t)sq * cache_seq_stride;
     vc += (size_t)sq * cache_seq_stride;
     if (n_kv < 1 || n_kv > ATT_MAX_KV) {
-        for (int d = tid; d < hd; d += blockDim.x) out[h * hd + d] = __builtin_nanf("");
+        for (int d = tid; d < hd; d += 256) out[h * hd + d] = __builtin_nanf("");
         return;
     }
     const int kv_dim = n_head_kv * hd, kvh = h / (n_head / n_head_kv);
     if (wave == 0) expf_ref_tab_fill(tab);
-    for (int d = tid; d < hd; d += blockDim.x) qs[d] = q[h * hd + d];
+    for (int d = tid; d < hd; d += 256) qs[d] = q[h * hd + d];
     __syncthreads();
     float mx = -INFINITY;
-    for (int t = tid; t < n_kv; t += blockDim.x) {
+    for (int t = tid; t < n_kv; t += 256) {
         const float *kr = kc + (size_t)t * kv_dim + kvh * hd;
         float dot = 0.0f;
         for (int d = 0; d < hd; d += 4) {
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t < n_kv; t += blockDim.x) lg[t] = expf_ref_tab(lg[t] - mx, tab);
+    for (int t = tid; t < n_kv; t += 256) lg[t] = expf_ref_tab(lg[t] - mx, tab);
     __syncthreads();
     if (tid == 0) {
         float sum = 0.0f;
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void attend_decode(const float *q, const float
     }
     __syncthreads();
     const float inv = red[0];
-    for (int d = tid; d < hd; d += blockDim.x) {
+    for (int d = tid; d < hd; d += 256) {
         const float *vr = vc + (size_t)kvh * hd + d;
         float acc = 0.0f;
         int t = 0;

@@ -105,11 +105,12 @@ __global__ __launch_bounds__(64) void route_logits(const float *logits, int n_ex
 // blockIdx.y = token (prefill); down is [n_tok][n_used][n_embd].
 // skip (optional): pair slots of the grouped prefill; a pair with slot < 0
 // had an out-of-range expert id and adds no term.
+// (256 threads per workgroup: a constant, so no implicit kernel arguments)
 template <int V>
-__global__ void moe_combine(const float *down, const float *weights, const float *res, float *out,
+__global__ __launch_bounds__(256) void moe_combine(const float *down, const float *weights, const float *res, float *out,
                             int n_used, int n_embd, const int32_t *skip) {
     typedef float fv __attribute__((ext_vector_type(V)));
-    const int i = V * (blockIdx.x * blockDim.x + threadIdx.x);  // this thread's first element
+    const int i = V * (blockIdx.x * 256 + threadIdx.x);  // this thread's first element
     if (i >= n_embd) return;
     const size_t tok = blockIdx.y;
     down += tok * n_used * n_embd;
@@ -153,13 +154,14 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
 }
 
+// (nparts = the grid's width, passed so the kernel needs no implicit arguments)
 __global__ __launch_bounds__(256) void argmax_partial(const float *x, int n, int ld, float *pv,
-                                                      int *pi) {
+                                                      int *pi, int nparts) {
     const int seq = blockIdx.y;
     const float *xs = x + (size_t)seq * ld;
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += nparts * 256) {
         const float v = xs[i];
         if (!isnan(v)) better(bv, bi, v, i);
     }
@@ -170,13 +172,14 @@ __global__ __launch_bounds__(256) void argmax_partial(const float *x, int n, int
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w) better(bv, bi, sv[w], si[w]);
-        pv[(size_t)seq * gridDim.x + blockIdx.x] = bv;
-        pi[(size_t)seq * gridDim.x + blockIdx.x] = bi;
+        pv[(size_t)seq * nparts + blockIdx.x] = bv;
+        pi[(size_t)seq * nparts + blockIdx.x] = bi;
     }
 }
 
-__global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, const float *pv,
-                                                     const int *pi, int nparts, int32_t *out) {
+template <int NT>
+__global__ __launch_bounds__(NT) void argmax_final(const float *x, int ld, const float *pv,
+                                                   const int *pi, int nparts, int32_t *out) {
     asm volatile("" ::"s"(x), "s"(ld), "s"(pv), "s"(pi), "s"(nparts), "s"(out));
     const int seq = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -189,12 +192,12 @@ __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, con
     // the reference's incumbent (index 0), loaded before the reduction so its
     // round trip overlaps the candidates'
     const float v0 = threadIdx.x == 0 ? x[(size_t)seq * ld] : 0.0f;
-    for (int base = threadIdx.x; base < nparts; base += U * blockDim.x) {
+    for (int base = threadIdx.x; base < nparts; base += U * NT) {
         float v[U];
         int id[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int i = base + u * blockDim.x;
+            const int i = base + u * NT;
             v[u] = i < nparts ? sv_in[i] : -INFINITY;
             id[u] = i < nparts ? si_in[i] : 0x7FFFFFFF;
         }
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(1024) void argmax_final(const float *x, int ld, con
     if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(bv, bi, sv[w], si[w]);
+        for (int w = 1; w < NT / 64; ++w) better(bv, bi, sv[w], si[w]);
         // the reference's incumbent is index 0: a NaN there is never beaten,
         // and when nothing beats -inf the answer stays 0
         out[seq] = (isnan(v0) || bi == 0x7FFFFFFF) ? 0 : bi;
@@ -333,14 +336,14 @@ int launch_argmax(const float *x, int n, int ld, int nseq, float *pv, int *pi, i
                   hipStream_t st, int max_parts) {
     int parts = argmax_parts(n);
     if (max_parts > 0 && parts > max_parts) parts = max_parts;
-    hipLaunchKernelGGL(argmax_partial, dim3(parts, nseq), dim3(256), 0, st, x, n, ld, pv, pi);
-    hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(64), 0, st, x, ld, pv, pi, parts, out);
+    hipLaunchKernelGGL(argmax_partial, dim3(parts, nseq), dim3(256), 0, st, x, n, ld, pv, pi, parts);
+    hipLaunchKernelGGL(argmax_final<64>, dim3(nseq), dim3(64), 0, st, x, ld, pv, pi, parts, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_argmax_final(const float *x, int ld, int nseq, const float *pv, const int *pi,
                         int nparts, int32_t *out, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_final, dim3(nseq), dim3(1024), 0, st, x, ld, pv, pi, nparts, out);
+    hipLaunchKernelGGL(argmax_final<1024>, dim3(nseq), dim3(1024), 0, st, x, ld, pv, pi, nparts, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -101,9 +101,9 @@ __global__ __launch_bounds__(256) void swiglu_q8k_chunks(const float *gate, cons
     store_chunk(chunk_dword(q, lane), dv, lane, cq, cd, slot, b, blocks);
 }
 
-__global__ void silu_mul_f32(const float *gate, const float *up, float *out, int n) {
+__global__ __launch_bounds__(256) void silu_mul_f32(const float *gate, const float *up, float *out, int n) {
     __shared__ uint64_t tab[32];
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = blockIdx.x * 256 + threadIdx.x;
     expf_ref_tab_fill(tab);
     if (i < n) out[i] = silu_ref(gate[i], tab) * up[i];
 }
