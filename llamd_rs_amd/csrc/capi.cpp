@@ -47,6 +47,7 @@ int g_tune_moe_polls = 1 << 18;
 int llamd::g_tune_model_graph = 1;  // whole-token decode replays a captured graph
 int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else three launches)
 int llamd::g_tune_model_fused_norm = 1;  // decode step: FFN norm inside the MoE decode launch
+int llamd::g_tune_model_norm_qkv = 1;  // decode step: attention norm inside the Q/K/V launch
 namespace {
 
 int fail(const char *fmt, ...) {
@@ -229,6 +230,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "model_fused_norm")) {
         const int prev = g_tune_model_fused_norm;
         g_tune_model_fused_norm = value ? 1 : 0;
+        return prev;
+    }
+    if (!strcmp(key, "model_norm_qkv")) {
+        const int prev = g_tune_model_norm_qkv;
+        g_tune_model_norm_qkv = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "model_fused_attn")) {

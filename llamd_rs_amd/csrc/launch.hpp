@@ -18,6 +18,7 @@ extern int g_tune_mv_ks;  // waves per 16-row tile in q6k_mv_b1: 1, 2, 4 or 8 (0
 extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a captured graph
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
 extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode launch
+extern int g_tune_model_norm_qkv;    // 1: the attention norm inside the Q/K/V launch
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -175,6 +176,12 @@ int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, in
                         float eps, hipStream_t st);
 // rms_norm(x) * w, then Q8_K (qs, d natural layout); out and inv_out optional.
 // rows > 1: rows of n each ([rows][n] x / out / qs, [rows][n/256] d, [rows] inv_out).
+// RMSNorm -> Q8_K -> the Q, K and V matvecs in one launch (norm.hip): y[i] =
+// W[i] (tiled Q6_K, rows[i] rows) . quantize_q8_k(rms_norm(x) * w), the bits of
+// launch_rms_norm_quant followed by the exact matvecs. n <= 2048.
+bool norm_qkv_fits(int n, const int rows[3]);
+int launch_norm_qkv(const float *x, const float *w, float eps, const void *const wt[3],
+                    float *const y[3], const int rows[3], int n, hipStream_t st);
 int launch_rms_norm_quant(const float *x, const float *w, float *out, int8_t *qs, float *d,
                           float *inv_out, int n, float eps, hipStream_t st, int rows = 1);
 

@@ -54,6 +54,7 @@ struct Model {
     bool use_graph = true;
     bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
     bool fused_norm = false;        // the FFN norm inside the MoE decode launch
+    bool norm_qkv = false;          // the attention norm inside the Q/K/V launch
     std::vector<void *> owned;     // device allocations to free
 };
 
@@ -89,9 +90,16 @@ bool enqueue_step(Model *m, hipStream_t st) {
     for (int il = 0; il < m->n_layer && !rc; ++il) {
         Layer &l = m->layers[il];
         // attn_norm = rms_norm(x) * w, quantized once for Q, K and V
-        llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
-        llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb, qdim,
-                            kv_dim, kv_dim);
+        if (m->norm_qkv) {
+            const void *wt[3] = {l.attn_q, l.attn_k, l.attn_v};
+            float *const y[3] = {m->q, m->k, m->v};
+            const int rows[3] = {qdim, kv_dim, kv_dim};
+            rc |= llamd::launch_norm_qkv(m->x, l.attn_norm, m->eps, wt, y, rows, E, st);
+        } else {
+            llamd_fwd_rms_norm_quant(m->x, l.attn_norm, nullptr, m->aq, m->ad, m->inv, E, m->eps);
+            llamd_fwd_matvec_x3(l.attn_q, l.attn_k, l.attn_v, m->aq, m->ad, m->q, m->k, m->v, eb,
+                                qdim, kv_dim, kv_dim);
+        }
         // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append,
         // attention, and Q8_K of its output for the O projection
         if (m->fused_attn) {
@@ -205,6 +213,7 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->max_kv = max_kv;
     m->use_graph = llamd::g_tune_model_graph != 0;
     m->fused_norm = llamd::g_tune_model_fused_norm != 0;
+    m->norm_qkv = llamd::g_tune_model_norm_qkv != 0;
     m->fused_attn = llamd::g_tune_model_fused_attn != 0 &&
                     llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;
@@ -267,6 +276,10 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     // the FFN norm inside the MoE decode launch, when the layer's shapes allow it
     // (decided once here: a launch error in the step is then always an error)
     m->fused_norm = m->fused_norm && llamd::moe_normed_applies(m->layers[0].moe);
+    {
+        const int rows[3] = {qdim, kv_dim, kv_dim};
+        m->norm_qkv = m->norm_qkv && llamd::norm_qkv_fits(n_embd, rows);
+    }
 
     // RoPE table: theta = pos / powf(base, 2i/hd), sin / cos (llamd-cpu lib.rs:196-200),
     // with the host libm the reference's f32 powf / sin / cos call

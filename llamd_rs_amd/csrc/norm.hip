@@ -21,6 +21,7 @@
 #include "row_scale.hpp"
 #include "launch.hpp"
 #include "q8k_wave.hpp"
+#include "q6k_tile.hpp"
 
 namespace llamd {
 namespace {
@@ -206,6 +207,142 @@ __global__ __launch_bounds__(NT ? NT : 1024) void add_rms_norm_mul(const float *
     }
 }
 
+
+// The attention front end of a decode step in one launch: RMSNorm -> Q8_K
+// (rms_norm_quant's bits) -> the Q, K and V matvecs (q6k_mv_b1's bits, the
+// reference's dot_q6k_q8k per row: per-block class terms added in block
+// order, then the eight class sums in order). The 16-row tiles of Q, K and V
+// are numbered one after another; a workgroup takes two consecutive tiles
+// (the norm is formed once per two tiles, and a decode step's 320 tiles fit
+// 160 CUs, one workgroup each).
+// Every workgroup forms the norm and the Q8_K itself, into LDS; its tiles'
+// weights are requested right after the row, so they stream in under the
+// in-order sum.
+constexpr int NQ_MAX_BLOCKS = 8;  // n <= 2048: one activation block per wave
+constexpr int NQ_TPW = 2;         // tiles per workgroup
+constexpr int NQ_UNITS = NQ_TPW * NQ_MAX_BLOCKS;  // (tile, block) units, two per wave
+
+struct NormQkvArgs {
+    const float *x, *w;
+    const uint8_t *wq, *wk, *wv;  // tiled Q6_K
+    float *yq, *yk, *yv;
+    int tq, tk, tv;               // 16-row tiles per matrix
+    int rq, rk, rv;               // rows per matrix
+    int n;
+    float eps;
+};
+
+// Tile T of the Q | K | V numbering: its matrix's weights, output, rows and
+// its index inside that matrix.
+struct NqTile {
+    const uint8_t *w;
+    float *y;
+    int rows, t;
+};
+__device__ __forceinline__ NqTile nq_tile(const NormQkvArgs &a, int T) {
+    if (T < a.tq) return {a.wq, a.yq, a.rq, T};
+    T -= a.tq;
+    if (T < a.tk) return {a.wk, a.yk, a.rk, T};
+    return {a.wv, a.yv, a.rv, T - a.tk};
+}
+
+__global__ __launch_bounds__(512) void norm_qkv(NormQkvArgs a) {
+    constexpr int TPW = NQ_TPW;
+    __shared__ ExactSumLds xl;
+    __shared__ __align__(16) float xs[NQ_MAX_BLOCKS * QK_K];
+    __shared__ __align__(16) int8_t lq[NQ_MAX_BLOCKS * QK_K];
+    __shared__ float ld[NQ_MAX_BLOCKS];
+    __shared__ float terms[NQ_UNITS][TILE_ROWS][8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, s = lane >> 4;
+    const int blocks = a.n / QK_K, total = a.tq + a.tk + a.tv, T0 = blockIdx.x * TPW;
+    // the row first: its loads return before the weights queued behind them
+    // (every load below is unconditional, at a clamped address when its unit
+    // is unused, so the first use of the row waits for the row alone)
+    const int m = xsum_run(a.n, 512), j0 = (int)threadIdx.x * m;
+    const bool run4 = m == 4;  // thread t holds x[4t .. 4t+3]: wave w holds block w
+    float v[XSUM_M];
+    if (run4) {
+        const float4 q = *(const float4 *)(a.x + j0);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+#pragma unroll
+        for (int k = 4; k < XSUM_M; ++k) v[k] = 0.0f;
+    } else {
+        load_run(a.x, a.n, 512, v);
+    }
+    // unit u = j * blocks + b: block b of the workgroup's tile j; wave w
+    // takes units w and w + 8
+    const int u0 = wave, u1 = wave + 8, units = TPW * blocks;
+    const bool live0 = u0 < units && T0 + u0 / blocks < total;
+    const bool live1 = u1 < units && T0 + u1 / blocks < total;
+    BlockRegs r0, r1;
+    {
+        const NqTile t0 = nq_tile(a, live0 ? T0 + u0 / blocks : 0);
+        const NqTile t1 = nq_tile(a, live1 ? T0 + u1 / blocks : 0);
+        load_weights(r0, t0.w + ((size_t)t0.t * blocks + (live0 ? u0 % blocks : 0)) * SEG_BYTES, lane, n);
+        load_weights(r1, t1.w + ((size_t)t1.t * blocks + (live1 ? u1 % blocks : 0)) * SEG_BYTES, lane, n);
+    }
+    // the norm weight of this wave's activation block
+    const float4 nw0 = *(const float4 *)(a.w + min(wave, blocks - 1) * QK_K + 4 * lane);
+    if (!run4) {
+        // the row into LDS for the blocks' quantization below
+#pragma unroll
+        for (int k = 0; k < XSUM_M; ++k)
+            if (k < m && j0 + k < a.n) xs[j0 + k] = v[k];
+    }
+    const float scale = row_scale_block(a.x, v, a.n, 512, a.eps, xl);  // synchronises the workgroup
+    // (x * scale) * w, quantized: wave b quantizes block b
+    const auto quant = [&](const float4 &xv, int b, const float4 &wv) {
+        const float q[4] = {(xv.x * scale) * wv.x, (xv.y * scale) * wv.y, (xv.z * scale) * wv.z,
+                            (xv.w * scale) * wv.w};
+        quantize_wave(q, lane, lq + b * QK_K, ld + b, nullptr);
+    };
+    if (run4)
+        quant(make_float4(v[0], v[1], v[2], v[3]), wave, nw0);
+    else if (wave < blocks)
+        quant(*(const float4 *)(xs + wave * QK_K + 4 * lane), wave, nw0);
+    __syncthreads();
+    // the per-block class terms of this wave's units
+    const MaskSel msel = mask_selectors(n, (n >> 2) == s);
+    const auto terms_of = [&](BlockRegs &r, int u) {
+        const int b = u % blocks;
+        r.g = *(const uint4 *)(lq + b * QK_K + 16 * n);
+        r.ad = ld[b];
+        float te, to;
+        block_terms(r, msel, te, to);
+        terms[u][n][2 * s] = te;
+        terms[u][n][2 * s + 1] = to;
+    };
+    if (live0) terms_of(r0, u0);
+    if (live1) terms_of(r1, u1);
+    __syncthreads();
+    // wave j folds tile j: block order, then the class sums in order
+    if (wave < TPW && T0 + wave < total) {
+        float se = 0.0f, so = 0.0f;
+        for (int b = 0; b < blocks; ++b) {
+            se = se + terms[wave * blocks + b][n][2 * s];
+            so = so + terms[wave * blocks + b][n][2 * s + 1];
+        }
+        float cls[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
+            cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
+        }
+        const NqTile tl = nq_tile(a, T0 + wave);
+        const int row = tl.t * TILE_ROWS + n;
+        if (s == 0 && row < tl.rows) {
+            float tot = -0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) tot = tot + cls[c];
+            tl.y[row] = tot;
+        }
+    }
+}
+
 }  // namespace
 
 int launch_qk_norm_rope_store(float *q, const float *k, const float *v, const float *qw,
@@ -237,6 +374,36 @@ int launch_rms_norm_mul(const float *x, const float *w, float *out, int rows, in
         hipLaunchKernelGGL(rms_norm_mul<512>, dim3(rows), dim3(nt), 0, st, x, w, out, n, w_len, eps);
     else
         hipLaunchKernelGGL(rms_norm_mul<0>, dim3(rows), dim3(nt), 0, st, x, w, out, n, w_len, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+bool norm_qkv_fits(int n, const int rows[3]) {
+    return n > 0 && n % QK_K == 0 && n / QK_K <= NQ_MAX_BLOCKS && rows[0] > 0 &&
+           rows[1] > 0 && rows[2] > 0;
+}
+
+int launch_norm_qkv(const float *x, const float *w, float eps, const void *const wt[3],
+                    float *const y[3], const int rows[3], int n, hipStream_t st) {
+    if (!x || !w || !norm_qkv_fits(n, rows)) return -1;
+    NormQkvArgs a;
+    a.x = x;
+    a.w = w;
+    a.wq = (const uint8_t *)wt[0];
+    a.wk = (const uint8_t *)wt[1];
+    a.wv = (const uint8_t *)wt[2];
+    a.yq = y[0];
+    a.yk = y[1];
+    a.yv = y[2];
+    a.rq = rows[0];
+    a.rk = rows[1];
+    a.rv = rows[2];
+    a.tq = (rows[0] + TILE_ROWS - 1) / TILE_ROWS;
+    a.tk = (rows[1] + TILE_ROWS - 1) / TILE_ROWS;
+    a.tv = (rows[2] + TILE_ROWS - 1) / TILE_ROWS;
+    a.n = n;
+    a.eps = eps;
+    const int total = a.tq + a.tk + a.tv;
+    hipLaunchKernelGGL(norm_qkv, dim3((total + NQ_TPW - 1) / NQ_TPW), dim3(512), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -20,26 +20,31 @@ HP_MHA = dict(MF.HP, n_head=4, n_head_kv=4)             # kv groups of one query
 HP_MHA64 = dict(MF.HP, n_head=8, n_head_kv=8, hd=64)   # hd 64: the three-launch path either way
 
 
-@pytest.mark.parametrize("hp,fused,fnorm,n_tok", [
-    (MF.HP, 1, 1, 10), (MF.HP, 0, 0, 10), (MF.HP, 1, 0, 10), (MF.HP, 0, 1, 10), (MF.HP, 1, 1, 40),
-    (HP_MHA, 1, 1, 12), (HP_MHA64, 1, 1, 12), (HP_MHA64, 0, 0, 12)])
-def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path, hp, fused, fnorm, n_tok):
-    """Every fusion of the step on and off: attend_fused (QK-norm, RoPE, KV
-    append, attention and Q8_K in one launch) or the three launches, and the
-    FFN norm inside the MoE decode launch or before it."""
+@pytest.mark.parametrize("hp,fused,fnorm,nqkv,n_tok", [
+    (MF.HP, 1, 1, 1, 10), (MF.HP, 1, 1, 0, 10), (MF.HP, 0, 0, 1, 10), (MF.HP, 1, 0, 1, 10),
+    (MF.HP, 0, 1, 0, 10), (MF.HP, 1, 1, 1, 40), (HP_MHA, 1, 1, 1, 12), (HP_MHA64, 1, 1, 1, 12),
+    (HP_MHA64, 0, 0, 0, 12)])
+def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path, hp, fused, fnorm, nqkv,
+                                                         n_tok):
+    """Every fusion of the step on and off: the attention RMSNorm and its
+    Q8_K inside the Q/K/V launch or before it, attend_fused (QK-norm, RoPE,
+    KV append, attention and Q8_K in one launch) or the three launches, and
+    the FFN norm inside the MoE decode launch or before it."""
     from llamd_rs_amd._lib import lib
     from llamd_rs_amd.gguf import Gguf
     p = tmp_path / "tiny.gguf"
     w = MF.make(p, seed=3, hp=hp)
     L = lib()
     prev = (L.llamd_hip_tune(b"model_fused_attn", fused),   # read when the model is created
-            L.llamd_hip_tune(b"model_fused_norm", fnorm))
+            L.llamd_hip_tune(b"model_fused_norm", fnorm),
+            L.llamd_hip_tune(b"model_norm_qkv", nqkv))
     try:
         with Gguf(p) as g:
             dm = gpu.DeviceModel(g, max_kv=48)
     finally:
         L.llamd_hip_tune(b"model_fused_attn", prev[0])
         L.llamd_hip_tune(b"model_fused_norm", prev[1])
+        L.llamd_hip_tune(b"model_norm_qkv", prev[2])
     ref = MF.OracleModel(w, hp=hp)
     try:
         assert (dm.n_layer, dm.n_embd, dm.n_vocab) == (2, 512, 768)
