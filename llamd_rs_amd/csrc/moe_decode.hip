@@ -273,12 +273,13 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 __device__ void norm_prologue(const DecodeParams &p, float *xs, ExactSumLds &xl, bool write_sum,
                               const float *wrow, float4 *wdst) {
     const int m = xsum_run(p.k, 512), j0 = min((int)threadIdx.x * m, p.k - 1), lane = threadIdx.x & 63;
-    float a[XSUM_M], b[XSUM_M], v[XSUM_M], sq[XSUM_M];
+    float a[XSUM_M], b[XSUM_M], nw[XSUM_M], v[XSUM_M], sq[XSUM_M];
 #pragma unroll
     for (int j = 0; j < XSUM_M; ++j) {
         const int i = min(j0 + j, p.k - 1);
         a[j] = p.norm_a[i];
         b[j] = p.norm_b[i];
+        nw[j] = p.norm_w[i];  // needed after the sum: loaded with the row
     }
     f4v wr[KMAX / 256];
     if (wrow) {
@@ -306,7 +307,7 @@ __device__ void norm_prologue(const DecodeParams &p, float *xs, ExactSumLds &xl,
     for (int j = 0; j < XSUM_M; ++j) {
         const int i = j0 + j;
         if (j < m && i < p.k) {
-            xs[i] = (v[j] * scale) * p.norm_w[i];
+            xs[i] = (v[j] * scale) * nw[j];
             if (write_sum) p.norm_sum[i] = v[j];
         }
     }
