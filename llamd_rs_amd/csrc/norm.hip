@@ -84,16 +84,23 @@ __global__ __launch_bounds__(NT ? NT : 1024) void rms_norm_mul(const float *x, c
     const float *src = x + (size_t)r * n;
     float v[XSUM_M];
     load_run(src, n, nt, v);
+    const int m = xsum_run(n, nt), j0 = (int)threadIdx.x * m;
+    // the weights of this thread's run, loaded with the row (not after the sum)
+    float wv[XSUM_M];
+#pragma unroll
+    for (int k = 0; k < XSUM_M; ++k) {
+        const int i = min(j0 + k, n - 1);
+        wv[k] = w && m <= XSUM_M ? w[w_len == n ? i : i % w_len] : 1.0f;
+    }
     const float scale = row_scale_block(src, v, n, nt, eps, xs);
     float *dst = out + (size_t)r * n;
-    const int m = xsum_run(n, nt), j0 = (int)threadIdx.x * m;
     if (m <= XSUM_M) {
 #pragma unroll
         for (int k = 0; k < XSUM_M; ++k) {
             const int i = j0 + k;
             if (k < m && i < n) {
                 const float y = v[k] * scale;
-                dst[i] = w ? y * w[w_len == n ? i : i % w_len] : y;
+                dst[i] = w ? y * wv[k] : y;
             }
         }
     } else {
@@ -122,9 +129,24 @@ __global__ __launch_bounds__(NT ? NT : 1024) void rms_norm_quant(const float *x,
     if (inv_out) inv_out += r;
     float v0[XSUM_M];
     load_run(x, n, nt, v0);
+    const int blocks = n / QK_K, waves = nt >> 6;
+    // runs of 4: thread t holds x[4t .. 4t+3], so wave b holds block b and
+    // quantizes it from registers; its weights are loaded with the row
+    const bool run4 = xsum_run(n, nt) == 4;
+    float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (run4 && wave < blocks) w4 = *(const float4 *)(w + wave * QK_K + 4 * lane);
     const float scale = row_scale_block(x, v0, n, nt, eps, xs);
     if (inv_out && threadIdx.x == 0) *inv_out = scale;
-    const int blocks = n / QK_K, waves = nt >> 6;
+    if (run4) {
+        if (wave < blocks) {
+            const size_t o = (size_t)wave * QK_K + 4 * lane;
+            const float v[4] = {(v0[0] * scale) * w4.x, (v0[1] * scale) * w4.y, (v0[2] * scale) * w4.z,
+                                (v0[3] * scale) * w4.w};
+            if (out) *(float4 *)(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+            quantize_wave(v, lane, qs + o - 4 * lane, d + wave, nullptr);
+        }
+        return;
+    }
     for (int b = wave; b < blocks; b += waves) {
         const size_t o = (size_t)b * QK_K + 4 * lane;
         const float4 xv = *(const float4 *)(x + o);
@@ -185,9 +207,12 @@ __global__ __launch_bounds__(NT ? NT : 1024) void add_rms_norm_mul(const float *
     const int nt = NT ? NT : (int)blockDim.x;
     __shared__ ExactSumLds xs;
     const int m = xsum_run(n, nt), j0 = (int)threadIdx.x * m;
-    float v[XSUM_M], ov[XSUM_M];
+    float v[XSUM_M], ov[XSUM_M], wv[XSUM_M];
     load_run(x, n, nt, v);
     load_run(o, n, nt, ov);
+    // the weights of this thread's run, loaded with the rows (not after the sum)
+#pragma unroll
+    for (int k = 0; k < XSUM_M; ++k) wv[k] = m <= XSUM_M ? w[min(j0 + k, n - 1)] : 0.0f;
 #pragma unroll
     for (int k = 0; k < XSUM_M; ++k) {
         v[k] = v[k] + ov[k];
@@ -201,7 +226,7 @@ __global__ __launch_bounds__(NT ? NT : 1024) void add_rms_norm_mul(const float *
     if (m <= XSUM_M) {
 #pragma unroll
         for (int k = 0; k < XSUM_M; ++k)
-            if (k < m && j0 + k < n) out[j0 + k] = (v[k] * scale) * w[j0 + k];
+            if (k < m && j0 + k < n) out[j0 + k] = (v[k] * scale) * wv[k];
     } else {
         for (int i = threadIdx.x; i < n; i += nt) out[i] = (sum_out[i] * scale) * w[i];
     }
