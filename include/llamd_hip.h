@@ -70,7 +70,7 @@ const char *llamd_hip_last_error(void);
  *     waiting wave computes the awaited router logit itself (default 2^18;
  *     0 = at once);
  *   "batch_decode_max", "model_graph", "model_fused_attn",
- *     "model_fused_norm", "model_norm_qkv": batched-decode threshold and
+ *     "model_fused_norm", "model_norm_qkv", "model_prefetch": batched-decode threshold and
  *     decode-step choices. */
 int llamd_hip_tune(const char *key, int value);
 

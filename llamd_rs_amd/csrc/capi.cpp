@@ -48,6 +48,7 @@ int llamd::g_tune_model_graph = 1;  // whole-token decode replays a captured gra
 int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else three launches)
 int llamd::g_tune_model_fused_norm = 1;  // decode step: FFN norm inside the MoE decode launch
 int llamd::g_tune_model_norm_qkv = 1;  // decode step: attention norm inside the Q/K/V launch
+int llamd::g_tune_model_prefetch = 1;  // decode step: O weights into L2 under the attention
 namespace {
 
 int fail(const char *fmt, ...) {
@@ -235,6 +236,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "model_norm_qkv")) {
         const int prev = g_tune_model_norm_qkv;
         g_tune_model_norm_qkv = value ? 1 : 0;
+        return prev;
+    }
+    if (!strcmp(key, "model_prefetch")) {
+        const int prev = g_tune_model_prefetch;
+        g_tune_model_prefetch = value ? 1 : 0;
         return prev;
     }
     if (!strcmp(key, "model_fused_attn")) {
@@ -845,6 +851,16 @@ MoeDecodeLaunch decode_launch(MoeLayer *m, const float *d_x, const float *d_res,
 }
 
 }  // namespace
+
+const float *llamd::moe_router(void *h) {
+    const MoeLayer *m = (const MoeLayer *)h;
+    return m ? (const float *)m->router.p : nullptr;
+}
+
+int llamd::moe_router_rows(void *h) {
+    const MoeLayer *m = (const MoeLayer *)h;
+    return m ? m->n_expert : 0;
+}
 
 bool llamd::moe_normed_applies(void *h) {
     const MoeLayer *m = (const MoeLayer *)h;

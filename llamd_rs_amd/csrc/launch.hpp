@@ -19,6 +19,7 @@ extern int g_tune_model_graph;  // 1: the decode step of llamd_hip_model_* is a 
 extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
 extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode launch
 extern int g_tune_model_norm_qkv;    // 1: the attention norm inside the Q/K/V launch
+extern int g_tune_model_prefetch;    // 1: the O weights read into L2 under the attention
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -92,6 +93,9 @@ int launch_moe_decode(const MoeDecodeLaunch &l, hipStream_t st);
 // out = sum_out + moe(rms_norm(sum_out) * w). Only for layers where
 // moe_normed_applies() holds (decided once, at model create); -1 is an error.
 bool moe_normed_applies(void *moe);
+// The layer's router matrix on the device ([n_expert][n_embd] f32) and its row count.
+const float *moe_router(void *moe);
+int moe_router_rows(void *moe);
 int moe_forward_normed(void *moe, const float *x, const float *o, const float *w, float eps,
                        float *sum_out, float *out);
 int launch_q6k_mv_batched(const void *w, size_t expert_stride, const int32_t *grp_expert,
@@ -197,7 +201,12 @@ int attend_fused_prepare(int n_head, int n_head_kv, int hd, int max_kv);
 int launch_attend_fused(const float *q, const float *k, const float *v, const float *qw,
                         const float *kw, const float2 *cs, const int32_t *pos, int n_head,
                         int n_head_kv, int hd, float eps, float scale, int max_kv, float *kc,
-                        float *vc, int8_t *oq, float *od, float *out, hipStream_t st);
+                        float *vc, int8_t *oq, float *od, float *out, hipStream_t st,
+                        const void *pf0 = nullptr, size_t b0 = 0, int n0 = 0,
+                        const void *pf1 = nullptr, size_t b1 = 0, int n1 = 0);
+// (pf0 / pf1: n0 + n1 extra workgroups read b0 (b1) bytes each from pf0 + i * b0
+// (pf1 + i * b1) into the L2 of XCD i % 8, where workgroup i of the later launch that
+// reads them runs; needs n_head / 2 and n0 to be multiples of 8, else skipped)
 // nseq sequences: n_kv = pos[s * pos_stride] + 1 (pos null: n_kv_fixed); q, out
 // [nseq][n_head * hd]; sequence s's cache starts cache_seq_stride floats after s-1's.
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,

@@ -55,6 +55,7 @@ struct Model {
     bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
     bool fused_norm = false;        // the FFN norm inside the MoE decode launch
     bool norm_qkv = false;          // the attention norm inside the Q/K/V launch
+    bool prefetch = false;          // the O weights into L2 under the attention
     std::vector<void *> owned;     // device allocations to free
 };
 
@@ -103,10 +104,19 @@ bool enqueue_step(Model *m, hipStream_t st) {
         // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append,
         // attention, and Q8_K of its output for the O projection
         if (m->fused_attn) {
-            rc |= llamd::launch_attend_fused(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
-                                             m->tokpos + 1, m->n_head, m->n_head_kv, m->hd, m->eps,
-                                             m->scale, m->max_kv, l.kc, l.vc, m->aq, m->ad,
-                                             nullptr, st);
+            // with the O projection's weight tiles and the MoE router's
+            // rows read into L2 alongside, each on the XCD of the workgroup
+            // that reads them next (O: workgroup t per 16-row tile; the
+            // MoE decode's chain workgroup b: router rows 4b .. 4b + 3)
+            const size_t o_tile = (size_t)(qdim / 256) * 16 * 210;  // 16 rows x 210 B per block
+            const int n_router = llamd::moe_router_rows(l.moe);
+            const float *router = llamd::moe_router(l.moe);
+            rc |= llamd::launch_attend_fused(
+                m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope, m->tokpos + 1, m->n_head,
+                m->n_head_kv, m->hd, m->eps, m->scale, m->max_kv, l.kc, l.vc, m->aq, m->ad, nullptr,
+                st, m->prefetch ? l.attn_out : nullptr, o_tile, m->prefetch ? (E + 15) / 16 : 0,
+                m->prefetch && router ? router : nullptr, (size_t)4 * E * 4,
+                m->prefetch && router ? (n_router + 3) / 4 : 0);
         } else {
             rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
                                                    m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
@@ -214,6 +224,7 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->use_graph = llamd::g_tune_model_graph != 0;
     m->fused_norm = llamd::g_tune_model_fused_norm != 0;
     m->norm_qkv = llamd::g_tune_model_norm_qkv != 0;
+    m->prefetch = llamd::g_tune_model_prefetch != 0;
     m->fused_attn = llamd::g_tune_model_fused_attn != 0 &&
                     llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;
