@@ -50,6 +50,7 @@ struct Model {
     int8_t *aq = nullptr;
     float *ad = nullptr;
     int32_t *tokpos = nullptr, *next = nullptr;
+    int32_t *stage = nullptr;       // page-locked host: token, position, next (async copies)
     hipGraphExec_t exec = nullptr;  // the captured step
     bool use_graph = true;
     bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
@@ -157,6 +158,7 @@ void destroy(Model *m) {
     if (m->output && m->output_owned) llamd_rocm_release(m->output);
     if (m->tok_embd) llamd_rocm_release(m->tok_embd);
     for (void *p : m->owned) llamd_fwd_free(p);
+    if (m->stage) (void)hipHostFree(m->stage);
     delete m;
 }
 
@@ -326,8 +328,9 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->logits = dalloc(*m, (size_t)m->n_vocab * 4);
     m->tokpos = (int32_t *)dalloc(*m, 16);
     m->next = (int32_t *)dalloc(*m, 16);
+    if (hipHostMalloc((void **)&m->stage, 64, hipHostMallocDefault) != hipSuccess) m->stage = nullptr;
     if (!m->x || !m->xn || !m->ffn_inp || !m->fn || !m->o || !m->q || !m->attn || !m->k || !m->v ||
-        !m->aq || !m->ad || !m->inv || !m->logits || !m->tokpos || !m->next) {
+        !m->aq || !m->ad || !m->inv || !m->logits || !m->tokpos || !m->next || !m->stage) {
         set_error("model: activation buffers could not be allocated");
         return fail_out();
     }
@@ -353,8 +356,12 @@ int llamd_hip_model_forward(void *h, int token, int pos, float *logits, int32_t 
     if (token < 0 || token >= m->n_vocab) return set_error("model: token %d outside a vocabulary of %d", token, m->n_vocab);
     if (pos < 0 || pos >= m->max_kv) return set_error("model: position %d beyond the %d allocated", pos, m->max_kv);
     hipStream_t st = (hipStream_t)llamd_fwd_get_stream();
-    const int32_t tp[2] = {token, pos};
-    if (llamd_fwd_upload(m->tokpos, tp, sizeof tp)) return -1;
+    // token and position through the page-locked stage: an asynchronous
+    // copy (the stage is rewritten only after the previous call's sync)
+    m->stage[0] = token;
+    m->stage[1] = pos;
+    if (hipMemcpyAsync(m->tokpos, m->stage, 8, hipMemcpyHostToDevice, st) != hipSuccess)
+        return set_error("model: token upload failed");
     // The step reads token and position from device memory, so its launches
     // are the same for every token: captured once into a HIP graph, replayed
     // per token (no per-launch host work). If capture is refused, the step
@@ -377,9 +384,16 @@ int llamd_hip_model_forward(void *h, int token, int pos, float *logits, int32_t 
     } else if (!enqueue_step(m, st)) {
         return -1;
     }
-    if (logits && llamd_fwd_download(logits, m->logits, (size_t)m->n_vocab * 4)) return -1;
-    if (next && llamd_fwd_download(next, m->next, 4)) return -1;
-    return llamd_fwd_sync() ? -1 : 0;
+    // both results queued, then one synchronisation (logits straight into
+    // the caller's buffer: one DMA when it is page-locked)
+    if (logits && hipMemcpyAsync(logits, m->logits, (size_t)m->n_vocab * 4, hipMemcpyDeviceToHost,
+                                 st) != hipSuccess)
+        return set_error("model: logits download failed");
+    if (hipMemcpyAsync(m->stage + 2, m->next, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+        return set_error("model: download failed");
+    if (hipStreamSynchronize(st) != hipSuccess) return set_error("model: step failed");
+    if (next) *next = m->stage[2];
+    return 0;
 }
 
 }  // extern "C"
