@@ -77,6 +77,39 @@ def test_decode_loop_refuses_bad_tokens_and_positions(gpu, tmp_path):
         dm.close()
 
 
+def test_decode_logits_arrays_held_across_calls(gpu, tmp_path):
+    """forward() hands out logits in page-locked buffers taken from a pool
+    and returned when an array is collected: arrays the caller still holds
+    are never reused, so every one of several held results keeps its own
+    token's bits, and buffers freed in between are reused correctly."""
+    from llamd_rs_amd.gguf import Gguf
+    p = tmp_path / "tiny.gguf"
+    w = MF.make(p, seed=6)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=16)
+    ref = MF.OracleModel(w)
+    try:
+        held, want = [], []
+        tok = 3
+        for pos in range(6):
+            logits, nxt = dm.forward(tok, pos)
+            wl, wn = ref.forward(tok, pos)
+            assert nxt == wn, pos
+            if pos % 2 == 0:
+                held.append(logits)        # kept: its buffer stays out of the pool
+                want.append(wl)
+            view = logits[5:9]             # a view keeps its base array alive
+            del logits
+            assert view.shape == (4,)
+            tok = nxt
+        for i, (a, b) in enumerate(zip(held, want)):
+            assert bits_equal(a, b), i
+        assert len({a.ctypes.data for a in held}) == len(held)
+    finally:
+        dm.close()
+    assert bits_equal(held[0], want[0])    # still readable after close
+
+
 def test_decode_full_qwen3_30b_a3b_widths(gpu, tmp_path):
     """The whole-token step at Qwen3-30B-A3B's real widths: hidden 2048, 32
     query / 4 kv heads of 128, 128 experts top-8 of n_ff 768, vocabulary
