@@ -59,6 +59,31 @@ def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path, hp, fuse
         dm.close()
 
 
+@pytest.mark.parametrize("hp", [MF.HP, HP_MHA])
+def test_decode_loop_long_context(gpu, tmp_path, hp):
+    """attend_fused stages cached K and V in LDS 64 positions at a time:
+    140 tokens cross its chunk boundaries at 64 and 128 (the later chunks
+    take the staging loops inside the logits and weighted-V phases), with
+    one and with two kv heads per workgroup. Every token's logits bits and
+    argmax against the CPU forward."""
+    from llamd_rs_amd.gguf import Gguf
+    p = tmp_path / "tiny.gguf"
+    w = MF.make(p, seed=8, hp=hp)
+    with Gguf(p) as g:
+        dm = gpu.DeviceModel(g, max_kv=160)
+    ref = MF.OracleModel(w, hp=hp, max_kv=160)
+    try:
+        tok = 7
+        for pos in range(140):
+            logits, nxt = dm.forward(tok, pos)
+            want, want_next = ref.forward(tok, pos)
+            assert bits_equal(logits, want), pos
+            assert nxt == want_next, pos
+            tok = nxt if pos % 5 else (tok * 31 + 3) % 768
+    finally:
+        dm.close()
+
+
 def test_decode_loop_refuses_bad_tokens_and_positions(gpu, tmp_path):
     from llamd_rs_amd._lib import HipError
     from llamd_rs_amd.gguf import Gguf
