@@ -71,7 +71,9 @@ const char *llamd_hip_last_error(void);
  *     0 = at once);
  *   "batch_decode_max", "model_graph", "model_fused_attn",
  *     "model_fused_norm", "model_norm_qkv", "model_prefetch": batched-decode threshold and
- *     decode-step choices. */
+ *     decode-step choices;
+ *   "model_long_from": the decode step's position from which the attention
+ *     runs split over the GPU (default 384; -1 never), read at model create. */
 int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */

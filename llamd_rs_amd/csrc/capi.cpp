@@ -49,6 +49,7 @@ int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else thre
 int llamd::g_tune_model_fused_norm = 1;  // decode step: FFN norm inside the MoE decode launch
 int llamd::g_tune_model_norm_qkv = 1;  // decode step: attention norm inside the Q/K/V launch
 int llamd::g_tune_model_prefetch = 1;  // decode step: O weights into L2 under the attention
+int llamd::g_tune_model_long_from = 384;  // decode step: split attention from this position (-1: never)
 namespace {
 
 int fail(const char *fmt, ...) {
@@ -241,6 +242,11 @@ int llamd_hip_tune(const char *key, int value) {
     if (!strcmp(key, "model_prefetch")) {
         const int prev = g_tune_model_prefetch;
         g_tune_model_prefetch = value ? 1 : 0;
+        return prev;
+    }
+    if (!strcmp(key, "model_long_from")) {
+        const int prev = g_tune_model_long_from;
+        g_tune_model_long_from = value;
         return prev;
     }
     if (!strcmp(key, "model_fused_attn")) {

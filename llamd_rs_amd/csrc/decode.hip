@@ -7,6 +7,7 @@
 // The token and position are read from device memory (not kernel
 // arguments), so a step's launches do not change from token to token.
 #include "common.hpp"
+#include "exact_sum.hpp"
 #include "expf_ref.h"
 #include "launch.hpp"
 #include "q8k_wave.hpp"
@@ -408,12 +409,16 @@ __global__ __launch_bounds__(512) void attend_fused(
             const float *vr = vst + (size_t)slot * C * HD + tid;
             int t = 0;
             for (; t + 8 <= np; t += 8) {
+                // the 8 values and their 8 weights read together, then the
+                // ordered adds (lg + c0 + t is 16-byte aligned)
                 float vv[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * HD];
+                const float4 l0 = *(const float4 *)(lg + c0 + t), l1 = *(const float4 *)(lg + c0 + t + 4);
+                const float ll[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float w = lg[c0 + t + j] * inv;
+                    const float w = ll[j] * inv;
                     acc = acc + w * vv[j];
                 }
             }
@@ -431,6 +436,220 @@ __global__ __launch_bounds__(512) void attend_fused(
     }
     __syncthreads();
     if (threadIdx.x < WAVE) {
+        const float4 v4 = *(const float4 *)(ov + 4 * lane);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        quantize_wave(v, lane, oq + (size_t)blockIdx.x * QK_K, od + blockIdx.x, nullptr);
+    }
+}
+
+// ---- attention over long contexts: logits spread over the GPU -------------
+// attend_fused runs n_head / 2 workgroups and walks the positions 64 at a
+// time, so its cost grows by ~50 ns per position and layer. Past a few
+// hundred positions the same arithmetic runs in two launches instead (after
+// qk_norm_rope_store has put the normed, rotated Q in place and K, V in the
+// cache):
+//  - attend_logits: workgroup w keeps kv head w % n_head_kv and takes its
+//    position blocks w / n_head_kv, + gridDim.x / n_head_kv, ...; the block's
+//    K rows are staged in LDS (rows padded to 132 floats) and thread
+//    (query head j of the group, position t) forms logit_t = (q . k_t, the
+//    128 products added in order from 0) * scale into scores.
+//  - attend_finish: one 1024-thread workgroup per head pair: max (order
+//    free), e_t = expf(logit_t - max), their in-order sum by exact_sum_nonneg
+//    (the reference's bits from a workgroup-wide certificate), inv = 1 / sum,
+//    then one thread per dimension adds (e_t * inv) * v_t[d] in position
+//    order, its loads issued 16 positions ahead; then the Q8_K of the pair's
+//    256 outputs for the O projection.
+// The same operations in the same order as attend_fused (and the reference,
+// attention.rs:73-125): the same bits.
+constexpr int AL_KS = ATT_HD + 4;   // padded K row in LDS
+constexpr int AL_MAX_GROUP = 16;    // query heads per kv head
+
+__global__ __launch_bounds__(256) void attend_logits(const float *q, const float *kc,
+                                                     const int32_t *pos_p, int n_head,
+                                                     int n_head_kv, float scale, float *scores,
+                                                     int max_kv) {
+    constexpr int HD = ATT_HD;
+    __shared__ __align__(16) float ks[64 * AL_KS];
+    __shared__ __align__(16) float qs[AL_MAX_GROUP * HD];
+    const int group = n_head / n_head_kv;
+    const int ppi = min(64, 256 / group);  // positions per block
+    const int g = blockIdx.x % n_head_kv;
+    const int stride = gridDim.x / n_head_kv;
+    const int kv_dim = n_head_kv * HD;
+    const int n_kv = pos_p[0] + 1;
+    const int nb = (n_kv + ppi - 1) / ppi;
+    const int tid = threadIdx.x;
+    if ((int)blockIdx.x / n_head_kv >= nb) return;
+    for (int i = tid; i < group * HD / 4; i += 256)
+        *(float4 *)(qs + 4 * i) = *(const float4 *)(q + (size_t)g * group * HD + 4 * i);
+    const int hl = tid / ppi, tl = tid - hl * ppi;
+    for (int pb = blockIdx.x / n_head_kv; pb < nb; pb += stride) {
+        const int t0 = pb * ppi, np = min(ppi, n_kv - t0);
+        __syncthreads();  // the previous block's rows are read
+        for (int i = tid; i < np * (HD / 4); i += 256) {
+            const int t = i / (HD / 4), d4 = i - t * (HD / 4);
+            *(float4 *)(ks + t * AL_KS + 4 * d4) =
+                *(const float4 *)(kc + (size_t)(t0 + t) * kv_dim + (size_t)g * HD + 4 * d4);
+        }
+        __syncthreads();
+        if (hl < group && tl < np) {
+            const float *kr = ks + tl * AL_KS, *qr = qs + hl * HD;
+            float dot = 0.0f;
+#pragma unroll
+            for (int d0 = 0; d0 < HD; d0 += 32) {
+                float4 k4[8], q4[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    k4[j] = *(const float4 *)(kr + d0 + 4 * j);
+                    q4[j] = *(const float4 *)(qr + d0 + 4 * j);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    dot = dot + q4[j].x * k4[j].x;
+                    dot = dot + q4[j].y * k4[j].y;
+                    dot = dot + q4[j].z * k4[j].z;
+                    dot = dot + q4[j].w * k4[j].w;
+                }
+            }
+            scores[(size_t)(g * group + hl) * max_kv + t0 + tl] = dot * scale;
+        }
+    }
+}
+
+constexpr int AF_PER = 8;  // float4s of one V chunk per thread (chunk <= 256 positions x 1 head)
+
+__global__ __launch_bounds__(1024) void attend_finish(const float *scores, const float *vc,
+                                                      const int32_t *pos_p, int n_head,
+                                                      int n_head_kv, int max_kv, int chunk,
+                                                      int8_t *oq, float *od, float *out) {
+    constexpr int HD = ATT_HD;
+    // [2][max_kv] e_t, then the V chunk [nkv][chunk][HD]
+    extern __shared__ __align__(16) float lgs[];
+    __shared__ ExactSumLds xl;
+    __shared__ uint64_t tab[32];
+    __shared__ float red[2][16];
+    __shared__ float inv2[2];
+    __shared__ __align__(16) float ov[2 * HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int group = n_head / n_head_kv, kv_dim = n_head_kv * HD;
+    const int h0 = blockIdx.x * 2;
+    const int n_kv = pos_p[0] + 1;
+    if (wave == 0) expf_ref_tab_fill(tab);
+    // the pair's logits into LDS, and each head's max (f32::max fold: NaN
+    // ignoring, order free)
+    float mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+        for (int t = tid; t < n_kv; t += 1024) {
+            const float l = scores[(size_t)(h0 + hh) * max_kv + t];
+            lgs[hh * max_kv + t] = l;
+            mx[hh] = fmaxf(mx[hh], l);
+        }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const float m = wave_reduce(mx[hh], -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+        if (lane == 0) red[hh][wave] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        float m = -INFINITY;
+        for (int w = 0; w < 16; ++w) m = fmaxf(m, red[hh][w]);
+        mx[hh] = m;
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+        for (int t = tid; t < n_kv; t += 1024)
+            lgs[hh * max_kv + t] = expf_ref_tab(lgs[hh * max_kv + t] - mx[hh], tab);
+    __syncthreads();
+    // each head's sum in order from 0, by the workgroup
+    const int m = xsum_run(n_kv, 1024), j0 = tid * m;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const float *e = lgs + hh * max_kv;
+        float v[XSUM_M];
+#pragma unroll
+        for (int k = 0; k < XSUM_M; ++k) v[k] = (k < m && j0 + k < n_kv) ? e[j0 + k] : 0.0f;
+        const float sum = exact_sum_nonneg(v, n_kv, 1024, xl, [e](int j) { return e[j]; });
+        if (tid == 0) inv2[hh] = __fdiv_rn(1.0f, sum);
+    }
+    __syncthreads();
+    // the weighted V sum, one thread per (head, dimension), in position
+    // order, from V rows staged in LDS a chunk at a time: the next chunk's
+    // loads (all threads, into registers) are in flight while this one is
+    // folded
+    const int nkv = group >= 2 ? 1 : 2;           // distinct kv heads of the pair
+    const int kvh0 = h0 / group;
+    float *vst = lgs + (size_t)2 * max_kv;        // [nkv][chunk][HD]
+    const int units = nkv * chunk * (HD / 4);     // float4s per chunk
+    att_f4 reg[AF_PER];
+    // every load unconditional, at a clamped row (a conditional load makes
+    // the compiler wait for each one before issuing the next); the extra
+    // ones re-read a row of the chunk and are never stored
+    const auto stage_load = [&](int c0) {
+        const int last = min(chunk, n_kv - c0) - 1;
+#pragma unroll
+        for (int k = 0; k < AF_PER; ++k) {
+            const int i = tid + 1024 * k;
+            const int sl = i / (chunk * (HD / 4)), r = i - sl * (chunk * (HD / 4));
+            const int t = min(r / (HD / 4), last), d4 = r % (HD / 4);
+            reg[k] = *(const att_f4 *)(vc + (size_t)(c0 + t) * kv_dim +
+                                       (size_t)(kvh0 + min(sl, nkv - 1)) * HD + 4 * d4);
+        }
+    };
+    const auto stage_store = [&](int c0) {
+        const int np = min(chunk, n_kv - c0);
+#pragma unroll
+        for (int k = 0; k < AF_PER; ++k) {
+            const int i = tid + 1024 * k;
+            const int sl = i / (chunk * (HD / 4)), r = i - sl * (chunk * (HD / 4));
+            const int t = r / (HD / 4);
+            if (i < units && t < np) *(att_f4 *)(vst + 4 * i) = reg[k];
+        }
+    };
+    const int hh = tid / HD, d = tid - hh * HD;
+    const bool folder = tid < 2 * HD;
+    const int slot = nkv == 1 ? 0 : hh;
+    const float inv = folder ? inv2[hh] : 0.0f;
+    const float *e = lgs + (folder ? hh : 0) * max_kv;
+    float acc = 0.0f;
+    stage_load(0);
+    for (int c0 = 0; c0 < n_kv; c0 += chunk) {
+        stage_store(c0);
+        __syncthreads();
+        if (c0 + chunk < n_kv) stage_load(c0 + chunk);
+        if (folder) {
+            const int np = min(chunk, n_kv - c0);
+            const float *vr = vst + (size_t)slot * chunk * HD + d;
+            int t = 0;
+            for (; t + 8 <= np; t += 8) {
+                // the 8 values and their 8 weights read together, then the
+                // ordered adds (e + c0 + t is 16-byte aligned: c0 and t are
+                // multiples of 8)
+                float vv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * HD];
+                const float4 e0 = *(const float4 *)(e + c0 + t), e1 = *(const float4 *)(e + c0 + t + 4);
+                const float ee[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float w = ee[j] * inv;
+                    acc = acc + w * vv[j];
+                }
+            }
+            for (; t < np; ++t) {
+                const float w = e[c0 + t] * inv;
+                acc = acc + w * vr[(size_t)t * HD];
+            }
+        }
+        __syncthreads();  // the chunk is read before the next one is stored
+    }
+    if (folder) {
+        ov[tid] = acc;
+        if (out) out[(size_t)(h0 + hh) * HD + d] = acc;
+    }
+    __syncthreads();
+    if (tid < WAVE) {
         const float4 v4 = *(const float4 *)(ov + 4 * lane);
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
         quantize_wave(v, lane, oq + (size_t)blockIdx.x * QK_K, od + blockIdx.x, nullptr);
@@ -492,6 +711,59 @@ int launch_attend_fused(const float *q, const float *k, const float *v, const fl
     hipLaunchKernelGGL(attend_fused, dim3(n_head / 2 + pf.n0 + pf.n1), dim3(512), lds, st, q, k, v,
                        qw, kw, cs, pos, n_head, n_head_kv, eps, scale, max_kv, kc, vc, oq, od, out,
                        pf);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+namespace {
+size_t g_split_lds = 0;  // the dynamic LDS attend_finish may use (raised by prepare)
+
+// V positions per LDS chunk: what the e_t rows leave of 152 KB, at most
+// AF_PER float4s per thread, a multiple of 16 (0: does not fit)
+int split_chunk(int n_head, int n_head_kv, int max_kv) {
+    const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
+    const long room = 152L * 1024 - 2L * max_kv * 4 - 8 * 1024;
+    long c = room / (nkv * ATT_HD * 4);
+    c = std::min<long>(c, (long)AF_PER * 1024 / (nkv * (ATT_HD / 4)));
+    c -= c % 16;
+    return c >= 16 ? (int)c : 0;
+}
+size_t split_lds(int n_head, int n_head_kv, int max_kv) {
+    const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
+    return (size_t)2 * max_kv * 4 + (size_t)nkv * split_chunk(n_head, n_head_kv, max_kv) * ATT_HD * 4;
+}
+}  // namespace
+
+bool attend_split_fits(int n_head, int n_head_kv, int hd, int max_kv) {
+    if (hd != ATT_HD || n_head_kv <= 0 || n_head % n_head_kv || n_head % 2 || max_kv <= 0) return false;
+    const int group = n_head / n_head_kv;
+    return group <= AL_MAX_GROUP && split_chunk(n_head, n_head_kv, max_kv) > 0;
+}
+
+int attend_split_prepare(int n_head, int n_head_kv, int hd, int max_kv) {
+    if (!attend_split_fits(n_head, n_head_kv, hd, max_kv)) return -1;
+    const size_t lds = split_lds(n_head, n_head_kv, max_kv);
+    if (lds <= g_split_lds) return 0;
+    if (hipFuncSetAttribute((const void *)attend_finish, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+        return -1;
+    g_split_lds = lds;
+    return 0;
+}
+
+int launch_attend_split(const float *q, const float *kc, const float *vc, const int32_t *pos,
+                        int n_head, int n_head_kv, int hd, float scale, int max_kv, float *scores,
+                        int8_t *oq, float *od, float *out, hipStream_t st) {
+    if (!attend_split_fits(n_head, n_head_kv, hd, max_kv)) return -1;
+    const size_t lds = split_lds(n_head, n_head_kv, max_kv);
+    if (lds > g_split_lds) return -1;  // attend_split_prepare first
+    const int chunk = split_chunk(n_head, n_head_kv, max_kv);
+    // 256 workgroups (a multiple of n_head_kv), each fixed to one kv head
+    const int grid = (256 / n_head_kv) * n_head_kv;
+    if (grid <= 0) return -1;
+    hipLaunchKernelGGL(attend_logits, dim3(grid), dim3(256), 0, st, q, kc, pos, n_head, n_head_kv,
+                       scale, scores, max_kv);
+    hipLaunchKernelGGL(attend_finish, dim3(n_head / 2), dim3(1024), lds, st, scores, vc, pos, n_head,
+                       n_head_kv, max_kv, chunk, oq, od, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -20,6 +20,7 @@ extern int g_tune_model_fused_attn;  // 1: attend_fused in the decode step
 extern int g_tune_model_fused_norm;  // 1: the FFN norm inside the MoE decode launch
 extern int g_tune_model_norm_qkv;    // 1: the attention norm inside the Q/K/V launch
 extern int g_tune_model_prefetch;    // 1: the O weights read into L2 under the attention
+extern int g_tune_model_long_from;   // decode step: the split attention from this position (-1: never)
 
 // q6k_mv.hip
 // y[slot][rows] = W[ids[slot]] . act; with w_b, also y[n_slots + slot] from
@@ -207,6 +208,16 @@ int launch_attend_fused(const float *q, const float *k, const float *v, const fl
 // (pf0 / pf1: n0 + n1 extra workgroups read b0 (b1) bytes each from pf0 + i * b0
 // (pf1 + i * b1) into the L2 of XCD i % 8, where workgroup i of the later launch that
 // reads them runs; needs n_head / 2 and n0 to be multiples of 8, else skipped)
+// Attention over long contexts in two launches (after launch_qk_norm_rope_store):
+// logits spread over 256 workgroups, then the softmax (exact in-order sum)
+// and the in-order weighted V sum per head pair, and the Q8_K of the output;
+// the bits of launch_attend_fused. scores: [n_head][max_kv] floats.
+bool attend_split_fits(int n_head, int n_head_kv, int hd, int max_kv);
+// raises attend_finish's dynamic LDS limit for max_kv positions (outside graph capture)
+int attend_split_prepare(int n_head, int n_head_kv, int hd, int max_kv);
+int launch_attend_split(const float *q, const float *kc, const float *vc, const int32_t *pos,
+                        int n_head, int n_head_kv, int hd, float scale, int max_kv, float *scores,
+                        int8_t *oq, float *od, float *out, hipStream_t st);
 // nseq sequences: n_kv = pos[s * pos_stride] + 1 (pos null: n_kv_fixed); q, out
 // [nseq][n_head * hd]; sequence s's cache starts cache_seq_stride floats after s-1's.
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,

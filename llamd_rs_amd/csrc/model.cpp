@@ -52,6 +52,10 @@ struct Model {
     int32_t *tokpos = nullptr, *next = nullptr;
     int32_t *stage = nullptr;       // page-locked host: token, position, next (async copies)
     hipGraphExec_t exec = nullptr;  // the captured step
+    hipGraphExec_t exec_long = nullptr;  // the same with the split attention
+    bool split_attn = false;        // attend_split for positions >= long_from
+    int long_from = 0;
+    float *scores = nullptr;        // [n_head][max_kv] (split attention)
     bool use_graph = true;
     bool fused_attn = false;        // attend_fused: QK-norm, RoPE, attention, Q8_K in one launch
     bool fused_norm = false;        // the FFN norm inside the MoE decode launch
@@ -86,7 +90,7 @@ float *upload_f32(Model &m, void *g, const std::string &name, uint64_t n) {
 
 // Every launch of one token's step (embedding .. argmax) on stream st; the
 // token and position come from m->tokpos.
-bool enqueue_step(Model *m, hipStream_t st) {
+bool enqueue_step(Model *m, hipStream_t st, bool long_ctx) {
     const int E = m->n_embd, eb = E / 256, qdim = m->n_head * m->hd, kv_dim = m->n_head_kv * m->hd;
     int rc = llamd::launch_embed_q6k(m->tok_embd, m->tokpos, eb, m->x, st);
     for (int il = 0; il < m->n_layer && !rc; ++il) {
@@ -104,7 +108,17 @@ bool enqueue_step(Model *m, hipStream_t st) {
         }
         // QK-norm per head before RoPE (layer.rs:113-136), RoPE, KV append,
         // attention, and Q8_K of its output for the O projection
-        if (m->fused_attn) {
+        if (long_ctx) {
+            // long contexts: QK-norm, RoPE and the KV append, then the
+            // logits over the whole GPU and the softmax / weighted V sum per
+            // head pair (the same bits)
+            rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
+                                                   m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
+                                                   m->eps, l.kc, l.vc, st);
+            rc |= llamd::launch_attend_split(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head,
+                                             m->n_head_kv, m->hd, m->scale, m->max_kv, m->scores,
+                                             m->aq, m->ad, nullptr, st);
+        } else if (m->fused_attn) {
             // with the O projection's weight tiles and the MoE router's
             // rows read into L2 alongside, each on the XCD of the workgroup
             // that reads them next (O: workgroup t per 16-row tile; the
@@ -149,6 +163,7 @@ void destroy(Model *m) {
     if (!m) return;
     (void)llamd_fwd_sync();
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->exec_long) (void)hipGraphExecDestroy(m->exec_long);
     if (m->lmhead) llamd_hip_lmhead_destroy(m->lmhead);
     for (Layer &l : m->layers) {
         if (l.moe) llamd_hip_moe_destroy(l.moe);
@@ -229,6 +244,9 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->prefetch = llamd::g_tune_model_prefetch != 0;
     m->fused_attn = llamd::g_tune_model_fused_attn != 0 &&
                     llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
+    m->long_from = llamd::g_tune_model_long_from;
+    m->split_attn = m->long_from >= 0 && m->long_from < max_kv &&
+                    llamd::attend_split_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;
     m->rope_base = base;
     m->scale = 1.0f / sqrtf((float)hd);  // attention.rs:95
@@ -328,6 +346,10 @@ void *llamd_hip_model_create(void *g, int max_kv) {
     m->logits = dalloc(*m, (size_t)m->n_vocab * 4);
     m->tokpos = (int32_t *)dalloc(*m, 16);
     m->next = (int32_t *)dalloc(*m, 16);
+    if (m->split_attn) {
+        m->scores = dalloc(*m, (size_t)m->n_head * max_kv * 4);
+        if (!m->scores) m->split_attn = false;
+    }
     if (hipHostMalloc((void **)&m->stage, 64, hipHostMallocDefault) != hipSuccess) m->stage = nullptr;
     if (!m->x || !m->xn || !m->ffn_inp || !m->fn || !m->o || !m->q || !m->attn || !m->k || !m->v ||
         !m->aq || !m->ad || !m->inv || !m->logits || !m->tokpos || !m->next || !m->stage) {
@@ -366,22 +388,25 @@ int llamd_hip_model_forward(void *h, int token, int pos, float *logits, int32_t 
     // are the same for every token: captured once into a HIP graph, replayed
     // per token (no per-launch host work). If capture is refused, the step
     // runs as plain launches.
-    if (!m->exec && m->use_graph) {
+    // positions from long_from on take the split attention (its own graph)
+    const bool long_ctx = m->split_attn && pos >= m->long_from;
+    hipGraphExec_t &exec = long_ctx ? m->exec_long : m->exec;
+    if (!exec && m->use_graph) {
         hipGraph_t graph = nullptr;
         bool ok = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess;
-        const bool enq = ok && enqueue_step(m, st);
+        const bool enq = ok && enqueue_step(m, st, long_ctx);
         ok = hipStreamEndCapture(st, &graph) == hipSuccess && ok && enq;
-        ok = ok && hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0) == hipSuccess;
+        ok = ok && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
         if (graph) (void)hipGraphDestroy(graph);
         if (!ok) {
-            m->exec = nullptr;
+            exec = nullptr;
             m->use_graph = false;
             (void)hipGetLastError();
         }
     }
-    if (m->exec) {
-        if (hipGraphLaunch(m->exec, st) != hipSuccess) return set_error("model: graph launch failed");
-    } else if (!enqueue_step(m, st)) {
+    if (exec) {
+        if (hipGraphLaunch(exec, st) != hipSuccess) return set_error("model: graph launch failed");
+    } else if (!enqueue_step(m, st, long_ctx)) {
         return -1;
     }
     // both results queued, then one synchronisation (logits straight into

@@ -59,18 +59,27 @@ def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path, hp, fuse
         dm.close()
 
 
-@pytest.mark.parametrize("hp", [MF.HP, HP_MHA])
-def test_decode_loop_long_context(gpu, tmp_path, hp):
-    """attend_fused stages cached K and V in LDS 64 positions at a time:
-    140 tokens cross its chunk boundaries at 64 and 128 (the later chunks
-    take the staging loops inside the logits and weighted-V phases), with
-    one and with two kv heads per workgroup. Every token's logits bits and
-    argmax against the CPU forward."""
+@pytest.mark.parametrize("hp,max_kv,long_from", [
+    (MF.HP, 160, -1), (HP_MHA, 160, -1),     # attend_fused throughout
+    (MF.HP, 160, 70), (HP_MHA, 160, 70),     # attend_fused, then the split attention from 70
+    (MF.HP, 16384, 0), (HP_MHA, 16384, 0)])  # split attention throughout, 32-position V chunks
+def test_decode_loop_long_context(gpu, tmp_path, hp, max_kv, long_from):
+    """140 tokens: attend_fused stages cached K and V in LDS 64 positions at a
+    time (chunk boundaries at 64 and 128), and the split attention of long
+    contexts (logits over the whole GPU, then the softmax and the weighted V
+    sum per head pair from V chunks in LDS) takes over at long_from, with one
+    and with two kv heads per head pair. Every token's logits bits and
+    argmax against the CPU forward, across the switch."""
+    from llamd_rs_amd._lib import lib
     from llamd_rs_amd.gguf import Gguf
     p = tmp_path / "tiny.gguf"
     w = MF.make(p, seed=8, hp=hp)
-    with Gguf(p) as g:
-        dm = gpu.DeviceModel(g, max_kv=160)
+    prev = lib().llamd_hip_tune(b"model_long_from", long_from)   # read when the model is created
+    try:
+        with Gguf(p) as g:
+            dm = gpu.DeviceModel(g, max_kv=max_kv)
+    finally:
+        lib().llamd_hip_tune(b"model_long_from", prev)
     ref = MF.OracleModel(w, hp=hp, max_kv=160)
     try:
         tok = 7
@@ -139,21 +148,27 @@ def test_decode_full_qwen3_30b_a3b_widths(gpu, tmp_path):
     """The whole-token step at Qwen3-30B-A3B's real widths: hidden 2048, 32
     query / 4 kv heads of 128, 128 experts top-8 of n_ff 768, vocabulary
     151936; 4 layers (each with its own norms, router and attention; two
-    distinct expert sets alternate), 3 tokens. Every logit's bits and the
-    argmax against the CPU forward composed from the oracle."""
+    distinct expert sets alternate), 4 tokens, the last two through the split
+    attention of long contexts (8 query heads per kv head). Every logit's bits
+    and the argmax against the CPU forward composed from the oracle."""
     from llamd_rs_amd import synth_model
+    from llamd_rs_amd._lib import lib
     from llamd_rs_amd.gguf import Gguf
     hp = dict(synth_model.QWEN3_30B_A3B, n_layer=4)
     p = tmp_path / "qwen3-30b-a3b-4l.gguf"
     w = synth_model.write_model(p, hp, seed=7, expert_sets=2, distinct_layers=True)
-    with Gguf(p) as g:
-        dm = gpu.DeviceModel(g, max_kv=16)
+    prev = lib().llamd_hip_tune(b"model_long_from", 2)
+    try:
+        with Gguf(p) as g:
+            dm = gpu.DeviceModel(g, max_kv=16)
+    finally:
+        lib().llamd_hip_tune(b"model_long_from", prev)
     p.unlink()
     ref = MF.OracleModel(w, hp=hp, max_kv=16)
     try:
         assert (dm.n_layer, dm.n_embd, dm.n_vocab) == (4, 2048, 151936)
         tok = 1234
-        for pos in range(3):
+        for pos in range(4):
             logits, nxt = dm.forward(tok, pos)
             want, want_next = ref.forward(tok, pos)
             assert bits_equal(logits, want), pos
