@@ -453,12 +453,14 @@ __global__ __launch_bounds__(512) void attend_fused(
 //    K rows are staged in LDS (rows padded to 132 floats) and thread
 //    (query head j of the group, position t) forms logit_t = (q . k_t, the
 //    128 products added in order from 0) * scale into scores.
-//  - attend_finish: one 1024-thread workgroup per head pair: max (order
-//    free), e_t = expf(logit_t - max), their in-order sum by exact_sum_nonneg
-//    (the reference's bits from a workgroup-wide certificate), inv = 1 / sum,
-//    then one thread per dimension adds (e_t * inv) * v_t[d] in position
-//    order, its loads issued 16 positions ahead; then the Q8_K of the pair's
-//    256 outputs for the O projection.
+//  - attend_finish: AF_SL 1024-thread workgroups per head pair, each on
+//    128 / AF_SL dimensions of both heads: max (order free), e_t =
+//    expf(logit_t - max), their in-order sum by exact_sum_nonneg (the
+//    reference's bits from a workgroup-wide certificate), inv = 1 / sum
+//    (every workgroup of the pair the same), then one thread per dimension
+//    adds (e_t * inv) * v_t[d] in position order from V rows staged in LDS
+//    (a quarter row per position, so a chunk holds up to ~900 positions);
+//    the f32 outputs then go through q8k_quantize for the O projection.
 // The same operations in the same order as attend_fused (and the reference,
 // attention.rs:73-125): the same bits.
 constexpr int AL_KS = ATT_HD + 4;   // padded K row in LDS
@@ -516,12 +518,14 @@ __global__ __launch_bounds__(256) void attend_logits(const float *q, const float
     }
 }
 
-constexpr int AF_PER = 8;  // float4s of one V chunk per thread (chunk <= 256 positions x 1 head)
+constexpr int AF_PER = 8;  // float4s of one V chunk per thread
+constexpr int AF_SL = 4;   // workgroups per head pair (dimension slices)
+constexpr int AF_DS = ATT_HD / AF_SL;
 
 __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const float *vc,
                                                       const int32_t *pos_p, int n_head,
                                                       int n_head_kv, int max_kv, int chunk,
-                                                      int8_t *oq, float *od, float *out) {
+                                                      float *out) {
     constexpr int HD = ATT_HD;
     // [2][max_kv] e_t, then the V chunk [nkv][chunk][HD]
     extern __shared__ __align__(16) float lgs[];
@@ -529,7 +533,6 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
     __shared__ uint64_t tab[32];
     __shared__ float red[2][16];
     __shared__ float inv2[2];
-    __shared__ __align__(16) float ov[2 * HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int group = n_head / n_head_kv, kv_dim = n_head_kv * HD;
     const int h0 = blockIdx.x * 2;
@@ -574,14 +577,16 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
         if (tid == 0) inv2[hh] = __fdiv_rn(1.0f, sum);
     }
     __syncthreads();
-    // the weighted V sum, one thread per (head, dimension), in position
-    // order, from V rows staged in LDS a chunk at a time: the next chunk's
-    // loads (all threads, into registers) are in flight while this one is
-    // folded
+    // the weighted V sum, one thread per (head, dimension of this slice), in
+    // position order, from V rows staged in LDS a chunk at a time: the next
+    // chunk's loads (all threads, into registers) are in flight while this
+    // one is folded
+    constexpr int DS = AF_DS, DS4 = AF_DS / 4;
+    const int sd = blockIdx.y * DS;                // the slice's first dimension
     const int nkv = group >= 2 ? 1 : 2;           // distinct kv heads of the pair
     const int kvh0 = h0 / group;
-    float *vst = lgs + (size_t)2 * max_kv;        // [nkv][chunk][HD]
-    const int units = nkv * chunk * (HD / 4);     // float4s per chunk
+    float *vst = lgs + (size_t)2 * max_kv;        // [nkv][chunk][DS]
+    const int units = nkv * chunk * DS4;          // float4s per chunk
     att_f4 reg[AF_PER];
     // every load unconditional, at a clamped row (a conditional load makes
     // the compiler wait for each one before issuing the next); the extra
@@ -591,10 +596,10 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
 #pragma unroll
         for (int k = 0; k < AF_PER; ++k) {
             const int i = tid + 1024 * k;
-            const int sl = i / (chunk * (HD / 4)), r = i - sl * (chunk * (HD / 4));
-            const int t = min(r / (HD / 4), last), d4 = r % (HD / 4);
+            const int sl = i / (chunk * DS4), r = i - sl * (chunk * DS4);
+            const int t = min(r / DS4, last), d4 = r % DS4;
             reg[k] = *(const att_f4 *)(vc + (size_t)(c0 + t) * kv_dim +
-                                       (size_t)(kvh0 + min(sl, nkv - 1)) * HD + 4 * d4);
+                                       (size_t)(kvh0 + min(sl, nkv - 1)) * HD + sd + 4 * d4);
         }
     };
     const auto stage_store = [&](int c0) {
@@ -602,13 +607,13 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
 #pragma unroll
         for (int k = 0; k < AF_PER; ++k) {
             const int i = tid + 1024 * k;
-            const int sl = i / (chunk * (HD / 4)), r = i - sl * (chunk * (HD / 4));
-            const int t = r / (HD / 4);
+            const int sl = i / (chunk * DS4), r = i - sl * (chunk * DS4);
+            const int t = r / DS4;
             if (i < units && t < np) *(att_f4 *)(vst + 4 * i) = reg[k];
         }
     };
-    const int hh = tid / HD, d = tid - hh * HD;
-    const bool folder = tid < 2 * HD;
+    const int hh = tid / DS, dd = tid - hh * DS;
+    const bool folder = tid < 2 * DS;
     const int slot = nkv == 1 ? 0 : hh;
     const float inv = folder ? inv2[hh] : 0.0f;
     const float *e = lgs + (folder ? hh : 0) * max_kv;
@@ -620,7 +625,7 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
         if (c0 + chunk < n_kv) stage_load(c0 + chunk);
         if (folder) {
             const int np = min(chunk, n_kv - c0);
-            const float *vr = vst + (size_t)slot * chunk * HD + d;
+            const float *vr = vst + (size_t)slot * chunk * DS + dd;
             int t = 0;
             for (; t + 8 <= np; t += 8) {
                 // the 8 values and their 8 weights read together, then the
@@ -628,7 +633,7 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
                 // multiples of 8)
                 float vv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * HD];
+                for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * DS];
                 const float4 e0 = *(const float4 *)(e + c0 + t), e1 = *(const float4 *)(e + c0 + t + 4);
                 const float ee[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
@@ -639,21 +644,12 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
             }
             for (; t < np; ++t) {
                 const float w = e[c0 + t] * inv;
-                acc = acc + w * vr[(size_t)t * HD];
+                acc = acc + w * vr[(size_t)t * DS];
             }
         }
         __syncthreads();  // the chunk is read before the next one is stored
     }
-    if (folder) {
-        ov[tid] = acc;
-        if (out) out[(size_t)(h0 + hh) * HD + d] = acc;
-    }
-    __syncthreads();
-    if (tid < WAVE) {
-        const float4 v4 = *(const float4 *)(ov + 4 * lane);
-        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-        quantize_wave(v, lane, oq + (size_t)blockIdx.x * QK_K, od + blockIdx.x, nullptr);
-    }
+    if (folder) out[(size_t)(h0 + hh) * HD + sd + dd] = acc;
 }
 
 }  // namespace
@@ -722,14 +718,14 @@ size_t g_split_lds = 0;  // the dynamic LDS attend_finish may use (raised by pre
 int split_chunk(int n_head, int n_head_kv, int max_kv) {
     const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
     const long room = 152L * 1024 - 2L * max_kv * 4 - 8 * 1024;
-    long c = room / (nkv * ATT_HD * 4);
-    c = std::min<long>(c, (long)AF_PER * 1024 / (nkv * (ATT_HD / 4)));
+    long c = room / (nkv * AF_DS * 4);
+    c = std::min<long>(c, (long)AF_PER * 1024 / (nkv * (AF_DS / 4)));
     c -= c % 16;
     return c >= 16 ? (int)c : 0;
 }
 size_t split_lds(int n_head, int n_head_kv, int max_kv) {
     const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
-    return (size_t)2 * max_kv * 4 + (size_t)nkv * split_chunk(n_head, n_head_kv, max_kv) * ATT_HD * 4;
+    return (size_t)2 * max_kv * 4 + (size_t)nkv * split_chunk(n_head, n_head_kv, max_kv) * AF_DS * 4;
 }
 }  // namespace
 
@@ -753,7 +749,7 @@ int attend_split_prepare(int n_head, int n_head_kv, int hd, int max_kv) {
 int launch_attend_split(const float *q, const float *kc, const float *vc, const int32_t *pos,
                         int n_head, int n_head_kv, int hd, float scale, int max_kv, float *scores,
                         int8_t *oq, float *od, float *out, hipStream_t st) {
-    if (!attend_split_fits(n_head, n_head_kv, hd, max_kv)) return -1;
+    if (!attend_split_fits(n_head, n_head_kv, hd, max_kv) || !out) return -1;
     const size_t lds = split_lds(n_head, n_head_kv, max_kv);
     if (lds > g_split_lds) return -1;  // attend_split_prepare first
     const int chunk = split_chunk(n_head, n_head_kv, max_kv);
@@ -762,9 +758,10 @@ int launch_attend_split(const float *q, const float *kc, const float *vc, const 
     if (grid <= 0) return -1;
     hipLaunchKernelGGL(attend_logits, dim3(grid), dim3(256), 0, st, q, kc, pos, n_head, n_head_kv,
                        scale, scores, max_kv);
-    hipLaunchKernelGGL(attend_finish, dim3(n_head / 2), dim3(1024), lds, st, scores, vc, pos, n_head,
-                       n_head_kv, max_kv, chunk, oq, od, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    hipLaunchKernelGGL(attend_finish, dim3(n_head / 2, AF_SL), dim3(1024), lds, st, scores, vc, pos,
+                       n_head, n_head_kv, max_kv, chunk, out);
+    if (hipGetLastError() != hipSuccess) return -1;
+    return launch_q8k_quantize(out, oq, od, nullptr, n_head / 2, st);
 }
 
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,

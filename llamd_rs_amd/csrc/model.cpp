@@ -117,7 +117,7 @@ bool enqueue_step(Model *m, hipStream_t st, bool long_ctx) {
                                                    m->eps, l.kc, l.vc, st);
             rc |= llamd::launch_attend_split(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head,
                                              m->n_head_kv, m->hd, m->scale, m->max_kv, m->scores,
-                                             m->aq, m->ad, nullptr, st);
+                                             m->aq, m->ad, m->attn, st);
         } else if (m->fused_attn) {
             // with the O projection's weight tiles and the MoE router's
             // rows read into L2 alongside, each on the XCD of the workgroup
