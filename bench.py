@@ -772,6 +772,20 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                            "parity": "bit-identical to the CPU forward at these widths on 4 layers x 3 tokens "
                                      "(tests/test_gpu_model.py::test_decode_full_qwen3_30b_a3b_widths)"}
     log(f"  decode token: {out['decode_token']}")
+    # the same model near the end of its 1024-position cache: every position
+    # filled in order (untimed), then 32 timed tokens; from position 384 on
+    # the step takes the split attention (logits over the whole GPU)
+    for pos in range(3 + n, 992):
+        _, tok = dm.forward(tok, pos)
+    t0 = time.perf_counter()
+    for pos in range(992, 1024):
+        _, tok = dm.forward(tok, pos)
+    dt = time.perf_counter() - t0
+    out["decode_token_ctx1k"] = {"us_per_token": dt / 32 * 1e6, "tok_s": 32 / dt, "tokens": 32,
+                                 "positions": "992..1023", "graph": not EAGER_ONLY,
+                                 "parity": "bit-identical to the CPU forward through the split attention "
+                                           "(tests/test_gpu_model.py::test_decode_loop_long_context)"}
+    log(f"  decode token at 1k context: {out['decode_token_ctx1k']}")
     dm.close()
     try:
         out.update(bench_ffi_decode(path))
