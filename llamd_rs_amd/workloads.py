@@ -145,6 +145,31 @@ def decode(L, iters):
     dm.close()
 
 
+def decode_long(L, iters):
+    """The decode step near position 1000 (the split attention of long
+    contexts): the 4-layer cut of the Qwen3-30B-A3B shapes, its cache filled
+    in order to position 999, then `iters` tokens; plain launches."""
+    import os
+    import tempfile
+    from . import synth_model
+    from .gguf import Gguf
+    hp = dict(synth_model.QWEN3_30B_A3B, n_layer=4)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    if L.llamd_hip_tune(b"model_graph", 0) < 0:  # read when the model is created
+        raise RuntimeError("tune")
+    try:
+        synth_model.write_model(path, hp)
+        with Gguf(path) as g:
+            dm = rocm.DeviceModel(g, max_kv=1024)
+    finally:
+        os.unlink(path)
+    tok = 1
+    for pos in range(1000 + iters):
+        _, tok = dm.forward(tok, pos)
+    dm.close()
+
+
 def ffi_decode(L, iters, nseq=1):
     """The reference's DeviceModel call sequence on the exported FFI
     (ffi_replay.py), the 4-layer cut of the Qwen3-30B-A3B shapes; plain
@@ -184,6 +209,7 @@ WORKLOADS = {
     "prefill": prefill,
     "prefill_reduction": lambda L, n: prefill(L, n, 1),
     "decode": decode,
+    "decode_long": decode_long,
     "ffi_decode": ffi_decode,
     "ffi_decode_batch16": lambda L, n: ffi_decode(L, n, 16),
 }
