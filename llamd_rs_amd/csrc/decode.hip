@@ -453,13 +453,12 @@ __global__ __launch_bounds__(512) void attend_fused(
 //    K rows are staged in LDS (rows padded to 132 floats) and thread
 //    (query head j of the group, position t) forms logit_t = (q . k_t, the
 //    128 products added in order from 0) * scale into scores.
-//  - attend_finish: AF_SL 1024-thread workgroups per head pair, each on
-//    128 / AF_SL dimensions of both heads: max (order free), e_t =
-//    expf(logit_t - max), their in-order sum by exact_sum_nonneg (the
-//    reference's bits from a workgroup-wide certificate), inv = 1 / sum
-//    (every workgroup of the pair the same), then one thread per dimension
-//    adds (e_t * inv) * v_t[d] in position order from V rows staged in LDS
-//    (a quarter row per position, so a chunk holds up to ~900 positions);
+//  - attend_finish: AF_SL 1024-thread workgroups per head, each on
+//    128 / AF_SL dimensions: max (order free), e_t = expf(logit_t - max),
+//    their in-order sum by exact_sum_nonneg (the reference's bits from a
+//    workgroup-wide certificate), inv = 1 / sum (every workgroup of the head
+//    the same), then one thread per dimension adds (e_t * inv) * v_t[d] in
+//    position order from V rows staged in LDS (half a row per position);
 //    the f32 outputs then go through q8k_quantize for the O projection.
 // The same operations in the same order as attend_fused (and the reference,
 // attention.rs:73-125): the same bits.
@@ -519,74 +518,57 @@ __global__ __launch_bounds__(256) void attend_logits(const float *q, const float
 }
 
 constexpr int AF_PER = 8;  // float4s of one V chunk per thread
-constexpr int AF_SL = 4;   // workgroups per head pair (dimension slices)
+constexpr int AF_SL = 2;   // workgroups per head (dimension slices)
 constexpr int AF_DS = ATT_HD / AF_SL;
 
 __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const float *vc,
                                                       const int32_t *pos_p, int n_head,
                                                       int n_head_kv, int max_kv, int chunk,
                                                       float *out) {
-    constexpr int HD = ATT_HD;
-    // [2][max_kv] e_t, then the V chunk [nkv][chunk][HD]
+    constexpr int HD = ATT_HD, DS = AF_DS, DS4 = AF_DS / 4;
+    // e_t [max_kv], then the V chunk [chunk][DS]
     extern __shared__ __align__(16) float lgs[];
     __shared__ ExactSumLds xl;
     __shared__ uint64_t tab[32];
-    __shared__ float red[2][16];
-    __shared__ float inv2[2];
+    __shared__ float red[16];
+    __shared__ float inv1;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int group = n_head / n_head_kv, kv_dim = n_head_kv * HD;
-    const int h0 = blockIdx.x * 2;
+    const int h = blockIdx.x, sd = blockIdx.y * DS;  // the head and the slice's first dimension
+    const int kv_dim = n_head_kv * HD, kvh = h / (n_head / n_head_kv);
     const int n_kv = pos_p[0] + 1;
     if (wave == 0) expf_ref_tab_fill(tab);
-    // the pair's logits into LDS, and each head's max (f32::max fold: NaN
+    // the head's logits into LDS, and their max (f32::max fold: NaN
     // ignoring, order free)
-    float mx[2] = {-INFINITY, -INFINITY};
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-        for (int t = tid; t < n_kv; t += 1024) {
-            const float l = scores[(size_t)(h0 + hh) * max_kv + t];
-            lgs[hh * max_kv + t] = l;
-            mx[hh] = fmaxf(mx[hh], l);
-        }
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const float m = wave_reduce(mx[hh], -INFINITY, [](float a, float b) { return fmaxf(a, b); });
-        if (lane == 0) red[hh][wave] = m;
+    float mx = -INFINITY;
+    for (int t = tid; t < n_kv; t += 1024) {
+        const float l = scores[(size_t)h * max_kv + t];
+        lgs[t] = l;
+        mx = fmaxf(mx, l);
     }
+    mx = wave_reduce(mx, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        float m = -INFINITY;
-        for (int w = 0; w < 16; ++w) m = fmaxf(m, red[hh][w]);
-        mx[hh] = m;
-    }
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-        for (int t = tid; t < n_kv; t += 1024)
-            lgs[hh * max_kv + t] = expf_ref_tab(lgs[hh * max_kv + t] - mx[hh], tab);
+    mx = -INFINITY;
+    for (int w = 0; w < 16; ++w) mx = fmaxf(mx, red[w]);
+    for (int t = tid; t < n_kv; t += 1024) lgs[t] = expf_ref_tab(lgs[t] - mx, tab);
     __syncthreads();
-    // each head's sum in order from 0, by the workgroup
-    const int m = xsum_run(n_kv, 1024), j0 = tid * m;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const float *e = lgs + hh * max_kv;
+    // their sum in order from 0, by the workgroup
+    {
+        const int m = xsum_run(n_kv, 1024), j0 = tid * m;
         float v[XSUM_M];
 #pragma unroll
-        for (int k = 0; k < XSUM_M; ++k) v[k] = (k < m && j0 + k < n_kv) ? e[j0 + k] : 0.0f;
+        for (int k = 0; k < XSUM_M; ++k) v[k] = (k < m && j0 + k < n_kv) ? lgs[j0 + k] : 0.0f;
+        const float *e = lgs;
         const float sum = exact_sum_nonneg(v, n_kv, 1024, xl, [e](int j) { return e[j]; });
-        if (tid == 0) inv2[hh] = __fdiv_rn(1.0f, sum);
+        if (tid == 0) inv1 = __fdiv_rn(1.0f, sum);
     }
     __syncthreads();
-    // the weighted V sum, one thread per (head, dimension of this slice), in
+    // the weighted V sum, one thread per dimension of this slice, in
     // position order, from V rows staged in LDS a chunk at a time: the next
     // chunk's loads (all threads, into registers) are in flight while this
     // one is folded
-    constexpr int DS = AF_DS, DS4 = AF_DS / 4;
-    const int sd = blockIdx.y * DS;                // the slice's first dimension
-    const int nkv = group >= 2 ? 1 : 2;           // distinct kv heads of the pair
-    const int kvh0 = h0 / group;
-    float *vst = lgs + (size_t)2 * max_kv;        // [nkv][chunk][DS]
-    const int units = nkv * chunk * DS4;          // float4s per chunk
+    float *vst = lgs + max_kv;                    // [chunk][DS]
+    const int units = chunk * DS4;                // float4s per chunk
     att_f4 reg[AF_PER];
     // every load unconditional, at a clamped row (a conditional load makes
     // the compiler wait for each one before issuing the next); the extra
@@ -596,10 +578,8 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
 #pragma unroll
         for (int k = 0; k < AF_PER; ++k) {
             const int i = tid + 1024 * k;
-            const int sl = i / (chunk * DS4), r = i - sl * (chunk * DS4);
-            const int t = min(r / DS4, last), d4 = r % DS4;
-            reg[k] = *(const att_f4 *)(vc + (size_t)(c0 + t) * kv_dim +
-                                       (size_t)(kvh0 + min(sl, nkv - 1)) * HD + sd + 4 * d4);
+            const int t = min(i / DS4, last), d4 = i % DS4;
+            reg[k] = *(const att_f4 *)(vc + (size_t)(c0 + t) * kv_dim + (size_t)kvh * HD + sd + 4 * d4);
         }
     };
     const auto stage_store = [&](int c0) {
@@ -607,16 +587,11 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
 #pragma unroll
         for (int k = 0; k < AF_PER; ++k) {
             const int i = tid + 1024 * k;
-            const int sl = i / (chunk * DS4), r = i - sl * (chunk * DS4);
-            const int t = r / DS4;
-            if (i < units && t < np) *(att_f4 *)(vst + 4 * i) = reg[k];
+            if (i < units && i / DS4 < np) *(att_f4 *)(vst + 4 * i) = reg[k];
         }
     };
-    const int hh = tid / DS, dd = tid - hh * DS;
-    const bool folder = tid < 2 * DS;
-    const int slot = nkv == 1 ? 0 : hh;
-    const float inv = folder ? inv2[hh] : 0.0f;
-    const float *e = lgs + (folder ? hh : 0) * max_kv;
+    const bool folder = tid < DS;
+    const float inv = inv1;
     float acc = 0.0f;
     stage_load(0);
     for (int c0 = 0; c0 < n_kv; c0 += chunk) {
@@ -625,16 +600,16 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
         if (c0 + chunk < n_kv) stage_load(c0 + chunk);
         if (folder) {
             const int np = min(chunk, n_kv - c0);
-            const float *vr = vst + (size_t)slot * chunk * DS + dd;
+            const float *vr = vst + tid;
             int t = 0;
             for (; t + 8 <= np; t += 8) {
                 // the 8 values and their 8 weights read together, then the
-                // ordered adds (e + c0 + t is 16-byte aligned: c0 and t are
+                // ordered adds (lgs + c0 + t is 16-byte aligned: c0 and t are
                 // multiples of 8)
                 float vv[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) vv[j] = vr[(size_t)(t + j) * DS];
-                const float4 e0 = *(const float4 *)(e + c0 + t), e1 = *(const float4 *)(e + c0 + t + 4);
+                const float4 e0 = *(const float4 *)(lgs + c0 + t), e1 = *(const float4 *)(lgs + c0 + t + 4);
                 const float ee[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -643,13 +618,13 @@ __global__ __launch_bounds__(1024) void attend_finish(const float *scores, const
                 }
             }
             for (; t < np; ++t) {
-                const float w = e[c0 + t] * inv;
+                const float w = lgs[c0 + t] * inv;
                 acc = acc + w * vr[(size_t)t * DS];
             }
         }
         __syncthreads();  // the chunk is read before the next one is stored
     }
-    if (folder) out[(size_t)(h0 + hh) * HD + sd + dd] = acc;
+    if (folder) out[(size_t)h * HD + sd + tid] = acc;
 }
 
 }  // namespace
@@ -716,16 +691,16 @@ size_t g_split_lds = 0;  // the dynamic LDS attend_finish may use (raised by pre
 // V positions per LDS chunk: what the e_t rows leave of 152 KB, at most
 // AF_PER float4s per thread, a multiple of 16 (0: does not fit)
 int split_chunk(int n_head, int n_head_kv, int max_kv) {
-    const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
-    const long room = 152L * 1024 - 2L * max_kv * 4 - 8 * 1024;
-    long c = room / (nkv * AF_DS * 4);
-    c = std::min<long>(c, (long)AF_PER * 1024 / (nkv * (AF_DS / 4)));
+    (void)n_head;
+    (void)n_head_kv;
+    const long room = 152L * 1024 - (long)max_kv * 4 - 8 * 1024;
+    long c = room / (AF_DS * 4);
+    c = std::min<long>(c, (long)AF_PER * 1024 / (AF_DS / 4));
     c -= c % 16;
     return c >= 16 ? (int)c : 0;
 }
 size_t split_lds(int n_head, int n_head_kv, int max_kv) {
-    const int nkv = n_head / n_head_kv >= 2 ? 1 : 2;
-    return (size_t)2 * max_kv * 4 + (size_t)nkv * split_chunk(n_head, n_head_kv, max_kv) * AF_DS * 4;
+    return (size_t)max_kv * 4 + (size_t)split_chunk(n_head, n_head_kv, max_kv) * AF_DS * 4;
 }
 }  // namespace
 
@@ -758,7 +733,7 @@ int launch_attend_split(const float *q, const float *kc, const float *vc, const 
     if (grid <= 0) return -1;
     hipLaunchKernelGGL(attend_logits, dim3(grid), dim3(256), 0, st, q, kc, pos, n_head, n_head_kv,
                        scale, scores, max_kv);
-    hipLaunchKernelGGL(attend_finish, dim3(n_head / 2, AF_SL), dim3(1024), lds, st, scores, vc, pos,
+    hipLaunchKernelGGL(attend_finish, dim3(n_head, AF_SL), dim3(1024), lds, st, scores, vc, pos,
                        n_head, n_head_kv, max_kv, chunk, out);
     if (hipGetLastError() != hipSuccess) return -1;
     return launch_q8k_quantize(out, oq, od, nullptr, n_head / 2, st);

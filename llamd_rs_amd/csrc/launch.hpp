@@ -210,7 +210,7 @@ int launch_attend_fused(const float *q, const float *k, const float *v, const fl
 // reads them runs; needs n_head / 2 and n0 to be multiples of 8, else skipped)
 // Attention over long contexts in two launches (after launch_qk_norm_rope_store):
 // logits spread over 256 workgroups, then the softmax (exact in-order sum)
-// and the in-order weighted V sum (four workgroups per head pair) into out
+// and the in-order weighted V sum (two workgroups per head) into out
 // [n_head * hd], and its Q8_K; the bits of launch_attend_fused. scores:
 // [n_head][max_kv] floats.
 bool attend_split_fits(int n_head, int n_head_kv, int hd, int max_kv);
