@@ -447,7 +447,7 @@ __global__ __launch_bounds__(512) void attend_fused(
 // time, so its cost grows by ~50 ns per position and layer. Past a few
 // hundred positions the same arithmetic runs in two launches instead (after
 // qk_norm_rope_store has put the normed, rotated Q in place and K, V in the
-// cache):
+// cache, and before q8k_quantize of the output):
 //  - attend_logits: workgroup w keeps kv head w % n_head_kv and takes its
 //    position blocks w / n_head_kv, + gridDim.x / n_head_kv, ...; the block's
 //    K rows are staged in LDS (rows padded to 132 floats) and thread
