@@ -59,16 +59,17 @@ def test_decode_loop_is_bit_identical_to_the_cpu_forward(gpu, tmp_path, hp, fuse
         dm.close()
 
 
-@pytest.mark.parametrize("hp,max_kv,long_from", [
-    (MF.HP, 160, -1), (HP_MHA, 160, -1),     # attend_fused throughout
-    (MF.HP, 160, 70), (HP_MHA, 160, 70),     # attend_fused, then the split attention from 70
-    (MF.HP, 16384, 0), (HP_MHA, 16384, 0)])  # split attention throughout, 32-position V chunks
-def test_decode_loop_long_context(gpu, tmp_path, hp, max_kv, long_from):
-    """140 tokens: attend_fused stages cached K and V in LDS 64 positions at a
-    time (chunk boundaries at 64 and 128), and the split attention of long
+@pytest.mark.parametrize("hp,max_kv,long_from,n_tok", [
+    (MF.HP, 160, -1, 140), (HP_MHA, 160, -1, 140),   # attend_fused throughout
+    (MF.HP, 160, 70, 140), (HP_MHA, 160, 70, 140),   # attend_fused, then the split attention
+    (MF.HP, 16384, 0, 140), (HP_MHA, 16384, 0, 140),  # split attention throughout
+    (MF.HP, 16384, 300, 400)])   # past the split attention's 320-position V chunks
+def test_decode_loop_long_context(gpu, tmp_path, hp, max_kv, long_from, n_tok):
+    """attend_fused stages cached K and V in LDS 64 positions at a time
+    (chunk boundaries at 64 and 128), and the split attention of long
     contexts (logits over the whole GPU, then the softmax and the weighted V
-    sum per head pair from V chunks in LDS) takes over at long_from, with one
-    and with two kv heads per head pair. Every token's logits bits and
+    sum from V chunks in LDS, 320 positions each at max_kv 16384) takes over
+    at long_from, with one and two query heads per kv head. Every token's logits bits and
     argmax against the CPU forward, across the switch."""
     from llamd_rs_amd._lib import lib
     from llamd_rs_amd.gguf import Gguf
@@ -80,10 +81,10 @@ def test_decode_loop_long_context(gpu, tmp_path, hp, max_kv, long_from):
             dm = gpu.DeviceModel(g, max_kv=max_kv)
     finally:
         lib().llamd_hip_tune(b"model_long_from", prev)
-    ref = MF.OracleModel(w, hp=hp, max_kv=160)
+    ref = MF.OracleModel(w, hp=hp, max_kv=n_tok)
     try:
         tok = 7
-        for pos in range(140):
+        for pos in range(n_tok):
             logits, nxt = dm.forward(tok, pos)
             want, want_next = ref.forward(tok, pos)
             assert bits_equal(logits, want), pos
