@@ -773,7 +773,7 @@ def bench_extra(L, rocm, synth, K, W, p, moe_cpu_seconds):
                                      "(tests/test_gpu_model.py::test_decode_full_qwen3_30b_a3b_widths)"}
     log(f"  decode token: {out['decode_token']}")
     # the same model near the end of its 1024-position cache: every position
-    # filled in order (untimed), then 32 timed tokens; from position 384 on
+    # filled in order (untimed), then 32 timed tokens; from position 256 on
     # the step takes the split attention (logits over the whole GPU)
     for pos in range(3 + n, 992):
         _, tok = dm.forward(tok, pos)

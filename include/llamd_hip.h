@@ -73,7 +73,7 @@ const char *llamd_hip_last_error(void);
  *     "model_fused_norm", "model_norm_qkv", "model_prefetch": batched-decode threshold and
  *     decode-step choices;
  *   "model_long_from": the decode step's position from which the attention
- *     runs split over the GPU (default 384; -1 never), read at model create. */
+ *     runs split over the GPU (default 256; -1 never), read at model create. */
 int llamd_hip_tune(const char *key, int value);
 
 /* ---- raw device memory and the stream ------------------------------------ */

@@ -49,7 +49,7 @@ int llamd::g_tune_model_fused_attn = 1;  // decode step: attend_fused (else thre
 int llamd::g_tune_model_fused_norm = 1;  // decode step: FFN norm inside the MoE decode launch
 int llamd::g_tune_model_norm_qkv = 1;  // decode step: attention norm inside the Q/K/V launch
 int llamd::g_tune_model_prefetch = 1;  // decode step: O weights into L2 under the attention
-int llamd::g_tune_model_long_from = 384;  // decode step: split attention from this position (-1: never)
+int llamd::g_tune_model_long_from = 256;  // decode step: split attention from this position (-1: never)
 namespace {
 
 int fail(const char *fmt, ...) {
