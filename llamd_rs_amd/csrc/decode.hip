@@ -447,7 +447,8 @@ __global__ __launch_bounds__(512) void attend_fused(
 // time, so its cost grows by ~50 ns per position and layer. Past a few
 // hundred positions the same arithmetic runs in two launches instead (after
 // qk_norm_rope_store has put the normed, rotated Q in place and K, V in the
-// cache, and before q8k_quantize of the output):
+// cache, and before the Q8_K of the output: q8k_quantize, or inside the O
+// projection, q6k_mv_f32x):
 //  - attend_logits: workgroup w keeps kv head w % n_head_kv and takes its
 //    position blocks w / n_head_kv, + gridDim.x / n_head_kv, ...; the block's
 //    K rows are staged in LDS (rows padded to 132 floats) and thread
@@ -458,8 +459,8 @@ __global__ __launch_bounds__(512) void attend_fused(
 //    their in-order sum by exact_sum_nonneg (the reference's bits from a
 //    workgroup-wide certificate), inv = 1 / sum (every workgroup of the head
 //    the same), then one thread per dimension adds (e_t * inv) * v_t[d] in
-//    position order from V rows staged in LDS (half a row per position);
-//    the f32 outputs then go through q8k_quantize for the O projection.
+//    position order from V rows staged in LDS (half a row per position)
+//    into the f32 output.
 // The same operations in the same order as attend_fused (and the reference,
 // attention.rs:73-125): the same bits.
 constexpr int AL_KS = ATT_HD + 4;   // padded K row in LDS
@@ -736,7 +737,8 @@ int launch_attend_split(const float *q, const float *kc, const float *vc, const 
     hipLaunchKernelGGL(attend_finish, dim3(n_head, AF_SL), dim3(1024), lds, st, scores, vc, pos,
                        n_head, n_head_kv, max_kv, chunk, out);
     if (hipGetLastError() != hipSuccess) return -1;
-    return launch_q8k_quantize(out, oq, od, nullptr, n_head / 2, st);
+    // oq null: the caller takes the f32 output (launch_q6k_mv_f32x)
+    return oq ? launch_q8k_quantize(out, oq, od, nullptr, n_head / 2, st) : 0;
 }
 
 int launch_attend_decode(const float *q, const float *kc, const float *vc, const int32_t *pos,

@@ -131,6 +131,10 @@ int launch_q6k_tile_bound(const void *w, int rows, int blocks, float *mt, hipStr
 // largest certified lower bound is recomputed exactly (dot_q6k_q8k's bits,
 // written back into logits), and ids = the reference's arg-max of the exact
 // logits. nq / nd: the tokens' Q8_K in the natural layout.
+// y[rows] = W (tiled Q6_K, blocks <= 16) . Q8_K(x), x f32 [blocks * 256]: the
+// bits of launch_q8k_quantize + launch_q6k_mv_b1 in one launch
+int launch_q6k_mv_f32x(const void *w, const float *x, float *y, int rows, int blocks,
+                       hipStream_t st);
 int launch_lmhead_certify(const void *w, int rows, int blocks, int nseq, const int8_t *nq,
                           const float *nd, const float *pv, const int *pi, const float *mt,
                           float *logits, int32_t *ids, hipStream_t st);

@@ -117,7 +117,7 @@ bool enqueue_step(Model *m, hipStream_t st, bool long_ctx) {
                                                    m->eps, l.kc, l.vc, st);
             rc |= llamd::launch_attend_split(m->q, l.kc, l.vc, m->tokpos + 1, m->n_head,
                                              m->n_head_kv, m->hd, m->scale, m->max_kv, m->scores,
-                                             m->aq, m->ad, m->attn, st);
+                                             nullptr, nullptr, m->attn, st);
         } else if (m->fused_attn) {
             // with the O projection's weight tiles and the MoE router's
             // rows read into L2 alongside, each on the XCD of the workgroup
@@ -140,8 +140,10 @@ bool enqueue_step(Model *m, hipStream_t st, bool long_ctx) {
                                               m->n_head_kv, m->hd, m->scale, m->attn, st);
             llamd_fwd_quantize(m->attn, m->aq, m->ad, qdim / 256);
         }
-        // O projection, residual
-        llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
+        // O projection (from the f32 attention output after the split
+        // attention: its Q8_K formed inside the matvec)
+        if (long_ctx) rc |= llamd::launch_q6k_mv_f32x(l.attn_out, m->attn, m->o, E, qdim / 256, st);
+        else llamd_fwd_matvec(l.attn_out, m->aq, m->ad, m->o, qdim / 256, E);
         // ffn_inp = x + O, ffn_norm; then the MoE FFN with the second
         // residual: x = ffn_inp + moe
         if (m->fused_norm) {
@@ -246,6 +248,7 @@ void *llamd_hip_model_create(void *g, int max_kv) {
                     llamd::attend_fused_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->long_from = llamd::g_tune_model_long_from;
     m->split_attn = m->long_from >= 0 && m->long_from < max_kv &&
+                    (int)(n_head * hd) / 256 <= 16 &&  // the f32-input O matvec (launch_q6k_mv_f32x)
                     llamd::attend_split_prepare((int)n_head, (int)n_head_kv, (int)hd, max_kv) == 0;
     m->eps = eps;
     m->rope_base = base;

@@ -1398,6 +1398,73 @@ __global__ __launch_bounds__(1024) void lmhead_certify(CertifyParams p) {
     }
 }
 
+// y = W . Q8_K(x) with x in f32 (the long-context decode step's O
+// projection, whose activation comes from the attention as f32): the bits of
+// launch_q8k_quantize + q6k_mv_b1<8> in one launch. One 16-row tile per
+// 8-wave workgroup; wave k quantizes the blocks it multiplies, [bpc k,
+// bpc k + bpc), with quantize_wave into its own LDS rows while its weight
+// loads are in flight; the per-block terms are folded in block order.
+constexpr int F32X_MAX_BLOCKS = 16;
+
+__global__ __launch_bounds__(512) void q6k_mv_f32x(const uint8_t *w, const float *x, float *y,
+                                                   int rows, int blocks) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, s = lane >> 4;
+    const int t = blockIdx.x;
+    const int bpc = (blocks + 7) / 8;  // at most 2
+    const int b0 = wave * bpc, b1 = min(blocks, b0 + bpc);
+    __shared__ float terms[F32X_MAX_BLOCKS][TILE_ROWS][8];
+    __shared__ __align__(16) int8_t lq[F32X_MAX_BLOCKS * QK_K];
+    __shared__ float ld[F32X_MAX_BLOCKS];
+    const uint8_t *seg = w + (size_t)t * blocks * SEG_BYTES;
+    BlockRegs r[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < bpc) load_weights(r[i], seg + (size_t)min(b0 + i, blocks - 1) * SEG_BYTES, lane, n);
+    float4 xv[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < bpc) xv[i] = *(const float4 *)(x + (size_t)min(b0 + i, blocks - 1) * QK_K + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < bpc && b0 + i < b1) {
+            const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            quantize_wave(v, lane, lq + (b0 + i) * QK_K, ld + b0 + i, nullptr);
+        }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const MaskSel msel = mask_selectors(n, (n >> 2) == s);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < bpc && b0 + i < b1) {
+            r[i].g = *(const uint4 *)(lq + (b0 + i) * QK_K + 16 * n);
+            r[i].ad = ld[b0 + i];
+            float te, to;
+            block_terms(r[i], msel, te, to);
+            terms[b0 + i][n][2 * s] = te;
+            terms[b0 + i][n][2 * s + 1] = to;
+        }
+    __syncthreads();
+    if (wave != 0) return;
+    float se = 0.0f, so = 0.0f;
+    for (int b = 0; b < blocks; ++b) {
+        se = se + terms[b][n][2 * s];
+        so = so + terms[b][n][2 * s + 1];
+    }
+    float cls[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        cls[2 * q] = __shfl(se, n + 16 * q, WAVE);
+        cls[2 * q + 1] = __shfl(so, n + 16 * q, WAVE);
+    }
+    const int row = t * TILE_ROWS + n;
+    float tot = -0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) tot = tot + cls[c];
+    if (s == 0 && row < rows) y[row] = tot;
+}
+
 }  // namespace
 
 int g_tune_mv_ks = 0;
@@ -1716,6 +1783,14 @@ int launch_q6k_tile_bound(const void *w, int rows, int blocks, float *mt, hipStr
     if (tiles <= 0 || blocks <= 0) return -1;
     hipLaunchKernelGGL(q6k_tile_bound, dim3((tiles + 3) / 4), dim3(256), 0, st, (const uint8_t *)w,
                        tiles, blocks, mt);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_q6k_mv_f32x(const void *w, const float *x, float *y, int rows, int blocks,
+                       hipStream_t st) {
+    if (!w || !x || !y || rows <= 0 || blocks <= 0 || blocks > F32X_MAX_BLOCKS) return -1;
+    hipLaunchKernelGGL(q6k_mv_f32x, dim3((rows + TILE_ROWS - 1) / TILE_ROWS), dim3(512), 0, st,
+                       (const uint8_t *)w, x, y, rows, blocks);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
