@@ -110,8 +110,8 @@ bool enqueue_step(Model *m, hipStream_t st, bool long_ctx) {
         // attention, and Q8_K of its output for the O projection
         if (long_ctx) {
             // long contexts: QK-norm, RoPE and the KV append, then the
-            // logits over the whole GPU and the softmax / weighted V sum per
-            // head pair (the same bits)
+            // logits over the whole GPU and the softmax / weighted V sum on
+            // two workgroups per head, into the f32 attn (the same bits)
             rc |= llamd::launch_qk_norm_rope_store(m->q, m->k, m->v, l.q_norm, l.k_norm, m->rope,
                                                    m->tokpos + 1, m->n_head, m->n_head_kv, m->hd,
                                                    m->eps, l.kc, l.vc, st);
